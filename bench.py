@@ -1,0 +1,155 @@
+"""Headline benchmark: paged GQA decode attention at the Llama-3-8B layer shape
+on one MI355X, plus the CPU oracle timed on the same host.
+
+A "step" is one paged decode-attention pass over the whole batch: 64 query
+rows (one per sequence, contexts U[128, 4096]), 32 query / 8 KV heads,
+head_dim 128, bf16 KV cache in the reference arena layout, block size 16,
+block tables scattered over a pool of 1.25x the blocks needed.  Inputs are
+resident in HBM before the timed region.
+
+value = algorithmic HBM bytes per step / step time, where the bytes are the
+compulsory traffic: every attended K and V vector once (sum(ctx) * 2 * Hkv *
+d * 2 B), the f32 queries and outputs, and the block-table entries.
+
+Prints ONE JSON line (the driver's contract).
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+for _p in (ROOT, os.path.join(ROOT, "orionserve-rs_amd"), os.path.join(ROOT, "tests")):
+    if _p not in sys.path:
+        sys.path.insert(0, _p)
+
+import numpy as np  # noqa: E402
+
+HBM_PEAK_GBS = 8000.0  # MI355X HBM3E, published
+
+
+def algorithmic_bytes(case):
+    kv = case.kv_bytes_read()
+    q = case.S * case.hq * case.d * 4
+    out = case.S * case.hq * case.d * 4
+    tables = int(sum(len(t) for t in case.tables)) * 4
+    return kv + q + out + tables
+
+
+def cpu_baseline(case, seconds_budget=30.0):
+    """The oracle (C++ restatement of the reference CPU attention) on the same
+    workload, all host threads (OpenMP over independent (row, head) pairs)."""
+    import oracle as orc
+
+    threads = min(16, os.cpu_count() or 1)
+    orc.set_num_threads(threads)
+    case.oracle()  # warm caches / page in
+    t0 = time.perf_counter()
+    reps = 0
+    while True:
+        case.oracle()
+        reps += 1
+        if time.perf_counter() - t0 > min(seconds_budget, 5.0) or reps >= 3:
+            break
+    dt = (time.perf_counter() - t0) / reps
+    return {
+        "value": algorithmic_bytes(case) / dt / 1e9,
+        "unit": "GB/s",
+        "cores": threads,
+        "kind": "port",
+        "sample": f"full config-2 step ({case.S} rows, sum ctx {int(case.ctxs.sum())}), "
+                  f"{reps} reps, {dt * 1e3:.1f} ms/step, f32 arena holding the same bf16 values",
+    }
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU oracle baseline")
+    a = ap.parse_args()
+    if a.gpus != 1:
+        print(f"bench.py measures one GPU only (this build is single-GPU); --gpus {a.gpus} "
+              "is not supported", file=sys.stderr)
+        sys.exit(2)
+
+    import orion_hip as oh
+    from paged_cases import cfg2
+
+    case = cfg2()
+    be = oh.HipBackend(0)
+    kv = oh.kv_layout(1, case.num_blocks, case.bs, case.hkv, case.d, oh.BF16)
+    arena = be.to_device(case.arena_device_bytes())
+    dq = be.to_device(case.q)
+    dpos = be.to_device(case.positions)
+    drs = be.to_device(case.row_seq)
+    dbo = be.to_device(case.bt_offsets)
+    dbi = be.to_device(case.bt_ids)
+    dout = be.alloc(case.S * case.hq * case.d * 4)
+    maxpos = int(case.positions.max())
+
+    def step():
+        oh.paged_attention_decode(be, kv, arena.ptr, 0, dq.ptr, case.S, case.hq, dpos.ptr,
+                                  drs.ptr, dbo.ptr, dbi.ptr, maxpos, dout.ptr)
+
+    for _ in range(a.warmup):
+        step()
+    be.synchronize()
+    be.timer_start()
+    for _ in range(a.steps):
+        step()
+    ms = be.timer_stop()
+    be.synchronize()
+    ms_per_step = ms / a.steps
+
+    # correctness spot-check of the measured output (cheap: 4 rows)
+    got = dout.download(np.float32, (case.S, case.hq * case.d))
+    rows = np.arange(4)
+    want = case.oracle(case.positions[rows], case.row_seq[rows], case.q[rows])
+    max_err = float(np.abs(got[rows] - want).max())
+
+    nbytes = algorithmic_bytes(case)
+    gbs = nbytes / (ms_per_step * 1e-3) / 1e9
+    result = {
+        "metric": "paged-attn decode HBM GB/s (% peak) at Llama-3-8B shape; decode tokens/sec",
+        "value": round(gbs, 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": a.steps,
+        "warmup": a.warmup,
+        "ms_per_step": round(ms_per_step, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic",
+        "config": {
+            "workload": "paged GQA decode attention, Llama-3-8B layer shape (config 2): 64 seqs, "
+                        "ctx U[128,4096], 32q/8kv heads, head_dim 128, bf16 KV, block 16, "
+                        "pool 1.25x",
+            "num_seqs": case.S,
+            "sum_context": int(case.ctxs.sum()),
+            "algorithmic_bytes_per_step": nbytes,
+            "kv_dtype": "bf16",
+            "accumulate": "f32",
+        },
+        "roofline": {
+            "bound": "hbm",
+            "achieved": round(gbs, 1),
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(gbs / HBM_PEAK_GBS, 4),
+            "traffic": None,
+        },
+        "max_abs_err_vs_oracle": max_err,
+    }
+    if not a.no_cpu:
+        result["cpu_baseline"] = cpu_baseline(case)
+    be.close()
+    print(json.dumps(result))
+
+
+if __name__ == "__main__":
+    main()

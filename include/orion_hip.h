@@ -1,0 +1,291 @@
+/*
+ * orion_hip.h — C ABI of the MI355X (gfx950) backend for OrionServe-RS's hot path.
+ *
+ * The hot path is the reference's TransformerModel::forward
+ * (crates/orion-models/src/transformer.rs:359-442): RMSNorm, Q/K/V projections,
+ * RoPE, the paged KV-cache write, paged grouped-query attention over block
+ * tables, the output projection, the SwiGLU MLP and the LM head.  This library
+ * runs all of it on one AMD Instinct MI355X with hand-written HIP kernels.
+ *
+ * The reference binds a device through two Rust traits
+ * (crates/orion-core/src/traits.rs):
+ *   - `Backend` (traits.rs:159-183): name/device/memory/synchronize/dtype.
+ *     -> orion_hip_device_* below.
+ *   - `LanguageModel` (traits.rs:297-309): `forward(&ForwardBatch) ->
+ *     ForwardOutput`.  -> orion_hip_model_* below.
+ * A Rust crate wraps these entry points as `HipBackend: Backend` and
+ * `HipTransformerModel: LanguageModel` so the scheduler and engine drive it
+ * unchanged.
+ *
+ * Conventions
+ *   - Every call returns an int status: 0 = ok, ORION_HIP_ERR_INTERNAL for an
+ *     invariant/index violation (the reference's EngineError::Internal,
+ *     crates/orion-core/src/error.rs:125-130), ORION_HIP_ERR_BACKEND for a
+ *     device failure (EngineError::Backend, error.rs:118-124).  The message is
+ *     in orion_hip_last_error() and the failing stage in
+ *     orion_hip_last_error_stage(); both are thread-local.
+ *   - Handles are opaque.  A device owns one HIP stream; every operation on
+ *     the device (and on models created on it) is enqueued on that stream in
+ *     call order.  Calls on one handle must not overlap (the reference engine
+ *     is single-threaded, docs/adr/006-single-threaded-engine-loop.md); handles
+ *     may be moved between threads.
+ *   - Pointers named `d_*` are device pointers (from orion_hip_alloc); all
+ *     others are host pointers.
+ */
+#ifndef ORION_HIP_H
+#define ORION_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define ORION_HIP_OK 0
+#define ORION_HIP_ERR_INTERNAL 1
+#define ORION_HIP_ERR_BACKEND 2
+
+/* DType, same order as the reference enum (traits.rs:21-29). */
+#define ORION_DTYPE_F32 0
+#define ORION_DTYPE_F16 1
+#define ORION_DTYPE_BF16 2
+#define ORION_DTYPE_I8 3
+#define ORION_DTYPE_I4 4
+
+typedef struct orion_hip_device orion_hip_device;
+typedef struct orion_hip_model orion_hip_model;
+
+/* Last error on this thread. */
+const char* orion_hip_last_error(void);
+const char* orion_hip_last_error_stage(void);
+
+/* ---------------------------------------------------------------------------
+ * Backend (traits.rs:159-183)
+ * ------------------------------------------------------------------------- */
+
+/* Number of visible GPUs; 0 when none (reference: orion-cuda device_count,
+ * crates/orion-cuda/src/lib.rs:82-90). */
+int orion_hip_device_count(int* count);
+
+/* Opens a device.  Fails instead of returning a dead handle
+ * (CudaBackend::new, crates/orion-cuda/src/lib.rs:110-132). */
+int orion_hip_device_open(int ordinal, orion_hip_device** out);
+void orion_hip_device_close(orion_hip_device* dev);
+
+/* Backend::name is "hip"; this gives the marketing name of the GPU. */
+int orion_hip_device_name(orion_hip_device* dev, char* buf, size_t len);
+
+/* Backend::total_memory / available_memory (traits.rs:167-173). */
+int orion_hip_mem_info(orion_hip_device* dev, uint64_t* total, uint64_t* free_bytes);
+
+/* Backend::synchronize (traits.rs:175-179): waits for the device stream. */
+int orion_hip_synchronize(orion_hip_device* dev);
+
+/* Backend::supports_dtype (traits.rs:182): F32, F16 and BF16 -> 1, else 0. */
+int orion_hip_supports_dtype(orion_hip_device* dev, int dtype);
+
+/* Device buffers and copies (used by the op-level entry points below). */
+int orion_hip_alloc(orion_hip_device* dev, size_t bytes, void** d_ptr);
+int orion_hip_free(orion_hip_device* dev, void* d_ptr);
+int orion_hip_memcpy_h2d(orion_hip_device* dev, void* d_dst, const void* src, size_t bytes);
+int orion_hip_memcpy_d2h(orion_hip_device* dev, void* dst, const void* d_src, size_t bytes);
+int orion_hip_memcpy_d2d(orion_hip_device* dev, void* d_dst, const void* d_src, size_t bytes);
+int orion_hip_memset(orion_hip_device* dev, void* d_dst, int value, size_t bytes);
+
+/* Stream-ordered timer: start records an event on the device stream; stop
+ * records a second one, waits for it and returns the elapsed milliseconds. */
+int orion_hip_timer_start(orion_hip_device* dev);
+int orion_hip_timer_stop(orion_hip_device* dev, float* ms);
+
+/* ---------------------------------------------------------------------------
+ * LanguageModel (traits.rs:297-309) over TransformerModel
+ * (transformer.rs:137-443)
+ * ------------------------------------------------------------------------- */
+
+/* Shape of a Llama/Qwen2 decoder (ModelMetadata, traits.rs:95-123, plus the
+ * paged-cache geometry passed to TransformerModel::new, transformer.rs:148-177). */
+typedef struct orion_hip_model_desc {
+  int32_t num_layers;
+  int32_t hidden_size;
+  int32_t num_attention_heads;
+  int32_t num_kv_heads;
+  int32_t head_dim;
+  int32_t intermediate_size; /* ffn_dim, config.rs:238-240 */
+  int32_t vocab_size;
+  int32_t max_position_embeddings;
+  float rms_norm_eps;
+  float rope_theta;
+  int32_t has_qkv_bias; /* Architecture::has_qkv_bias, config.rs:134-139 */
+  int32_t tied_lm_head; /* lm_head absent -> embed_tokens, transformer.rs:108-112 */
+  int32_t num_blocks;   /* KV arena capacity in blocks */
+  int32_t block_size;   /* tokens per block, power of two in [4, 256] */
+  int32_t kv_dtype;     /* ORION_DTYPE_F32 or ORION_DTYPE_BF16 */
+} orion_hip_model_desc;
+
+/* Weight identifiers (HF names, transformer.rs:6-19).  Ids >= ORION_W_INPUT_NORM
+ * are per layer. */
+#define ORION_W_EMBED 0      /* model.embed_tokens.weight     [vocab, hidden]    */
+#define ORION_W_FINAL_NORM 1 /* model.norm.weight             [hidden]           */
+#define ORION_W_LM_HEAD 2    /* lm_head.weight                [vocab, hidden]    */
+#define ORION_W_INPUT_NORM 3 /* input_layernorm.weight        [hidden]           */
+#define ORION_W_Q 4          /* self_attn.q_proj.weight       [Hq*d, hidden]     */
+#define ORION_W_K 5          /* self_attn.k_proj.weight       [Hkv*d, hidden]    */
+#define ORION_W_V 6          /* self_attn.v_proj.weight       [Hkv*d, hidden]    */
+#define ORION_W_O 7          /* self_attn.o_proj.weight       [hidden, Hq*d]     */
+#define ORION_W_Q_BIAS 8     /* self_attn.q_proj.bias         [Hq*d]   (Qwen2)   */
+#define ORION_W_K_BIAS 9     /* self_attn.k_proj.bias         [Hkv*d]  (Qwen2)   */
+#define ORION_W_V_BIAS 10    /* self_attn.v_proj.bias         [Hkv*d]  (Qwen2)   */
+#define ORION_W_POST_NORM 11 /* post_attention_layernorm.weight [hidden]         */
+#define ORION_W_GATE 12      /* mlp.gate_proj.weight          [ffn, hidden]      */
+#define ORION_W_UP 13        /* mlp.up_proj.weight            [ffn, hidden]      */
+#define ORION_W_DOWN 14      /* mlp.down_proj.weight          [hidden, ffn]      */
+
+/* Creates a model with zeroed weights and a zeroed KV arena
+ * (TransformerModel::new, transformer.rs:148-177; KvStore::new, attention.rs:45-62).
+ * The RoPE table is built on the host with the reference formula
+ * (tensor.rs:228-253) and kept on the device. */
+int orion_hip_model_create(orion_hip_device* dev, const orion_hip_model_desc* desc,
+                           orion_hip_model** out);
+void orion_hip_model_destroy(orion_hip_model* model);
+
+/* Uploads one weight (ModelWeights::load, transformer.rs:62-120).  `dtype` is
+ * the host data's type (F32, F16 or BF16); `count` elements.  Matrices are
+ * stored as bf16 on the device (f32 input is rounded to nearest even), norm
+ * gains and biases as f32. */
+int orion_hip_model_upload_weight(orion_hip_model* model, int which, int layer,
+                                  const void* host, int dtype, size_t count);
+
+/* Fills every weight with a seeded synthetic initialisation (no checkpoint):
+ * matrices ~ N(0, std) (integer Irwin-Hall sum of four 16-bit uniforms, then
+ * rounded to bf16), norm gains 1, biases ~ N(0, std).  Bit-reproducible on any
+ * host with orion_hip_synthetic_value(). */
+int orion_hip_model_init_synthetic(orion_hip_model* model, uint64_t seed, float std);
+
+/* The value orion_hip_model_init_synthetic() gives element `index` of weight
+ * (`which`, `layer`), as f32 (for matrices: already rounded to bf16). */
+float orion_hip_synthetic_value(uint64_t seed, int which, int layer, uint64_t index, float std);
+
+/* Reads one weight back as f32 (count elements).  Test hook. */
+int orion_hip_model_download_weight(orion_hip_model* model, int which, int layer, float* host,
+                                    size_t count);
+
+/* ForwardBatch (traits.rs:193-210) in CSR form.  Block table of sequence s is
+ * block_table_ids[block_table_offsets[s] .. block_table_offsets[s+1]]. */
+typedef struct orion_hip_batch {
+  int64_t num_tokens;
+  int64_t num_seqs;
+  const uint32_t* tokens;              /* [num_tokens] */
+  const uint32_t* positions;           /* [num_tokens] */
+  const int64_t* slot_token_counts;    /* [num_seqs], sums to num_tokens */
+  const int64_t* context_lens;         /* [num_seqs] (carried, not used; as the reference) */
+  const int64_t* block_table_offsets;  /* [num_seqs + 1] */
+  const uint32_t* block_table_ids;
+  int32_t has_prefill;
+} orion_hip_batch;
+
+/* LanguageModel::forward (transformer.rs:359-442): validates the batch
+ * (traits.rs:232-261), writes this batch's K/V into the paged arena, runs all
+ * layers and returns last-row logits [num_seqs, vocab] f32 into host memory.
+ * `logits` may be NULL when only `argmax_out` is wanted.  `argmax_out`
+ * (optional, [num_seqs]) receives the greedy token of each row with the
+ * reference's tie rule (runtime/src/sampling.rs:196-207); -1 where no logit
+ * exceeds -inf. */
+int orion_hip_model_forward(orion_hip_model* model, const orion_hip_batch* batch, float* logits,
+                            int64_t* argmax_out);
+
+/* KvStore::read / write (attention.rs:107-134) for one (layer, block, slot,
+ * head) vector of head_dim f32 values; bounds errors as the reference. */
+int orion_hip_model_kv_read(orion_hip_model* model, int64_t layer, uint32_t block, int64_t slot,
+                            int64_t head, int is_value, float* out);
+int orion_hip_model_kv_write(orion_hip_model* model, int64_t layer, uint32_t block, int64_t slot,
+                             int64_t head, int is_value, const float* vec, int64_t len);
+
+/* Device address and byte size of the model's KV arena, layout
+ * [layer][block][k|v][slot][kv_head][head_dim] (attention.rs:11-22). */
+int orion_hip_model_kv_arena(orion_hip_model* model, void** d_arena, size_t* bytes);
+
+/* ---------------------------------------------------------------------------
+ * Op-level entry points (device pointers, enqueued on the device stream).
+ * These are the per-kernel validation gate of docs/cuda.md:80-116.
+ * ------------------------------------------------------------------------- */
+
+/* Geometry of a paged KV arena (KvStore, attention.rs:34-62). */
+typedef struct orion_hip_kv_layout {
+  int64_t num_layers;
+  int64_t num_blocks;
+  int64_t block_size;
+  int64_t num_kv_heads;
+  int64_t head_dim;
+  int32_t dtype; /* ORION_DTYPE_F32 or ORION_DTYPE_BF16 */
+} orion_hip_kv_layout;
+
+/* paged_attention (attention.rs:219-295) for `num_rows` independent query
+ * rows: row r attends positions 0..=d_positions[r] of the sequence
+ * d_row_seq[r] through that sequence's block table (CSR d_bt_offsets /
+ * d_bt_ids).  d_q and d_out are [num_rows, num_q_heads, head_dim] f32.
+ * max_position bounds every d_positions entry (it sizes the split-K grid).
+ * Block ids and table lengths are not re-checked on the device: the caller
+ * guarantees every (position / block_size) < table length and every id
+ * < num_blocks (orion_hip_model_forward checks this on the host). */
+int orion_hip_paged_attention_decode(orion_hip_device* dev, const orion_hip_kv_layout* kv,
+                                     const void* d_arena, int64_t layer, const float* d_q,
+                                     int64_t num_rows, int64_t num_q_heads,
+                                     const uint32_t* d_positions, const int32_t* d_row_seq,
+                                     const int64_t* d_bt_offsets, const uint32_t* d_bt_ids,
+                                     int64_t max_position, float* d_out);
+
+/* Causal attention for prefill chunks on MFMA: sequence s contributes query
+ * rows d_q[d_row_start[s] .. d_row_start[s] + d_row_count[s]) whose positions
+ * are consecutive from d_first_pos[s]; each attends 0..=its position.  Same
+ * result as paged_attention per row.  `max_rows` bounds d_row_count,
+ * `max_position` bounds every position. */
+int orion_hip_paged_attention_prefill(orion_hip_device* dev, const orion_hip_kv_layout* kv,
+                                      const void* d_arena, int64_t layer, const float* d_q,
+                                      int64_t num_q_heads, int64_t num_seqs,
+                                      const int32_t* d_row_start, const int32_t* d_row_count,
+                                      const uint32_t* d_first_pos, const int64_t* d_bt_offsets,
+                                      const uint32_t* d_bt_ids, int64_t max_rows,
+                                      int64_t max_position, float* d_out);
+
+/* Slot mapping + KV write (transformer.rs:371-387 and :283-297) fused with
+ * RoPE (tensor.rs:283-298): for each row, rotates its Q heads from d_q_in
+ * (row stride q_stride elements) into d_q_out [rows, Hq*d] (must not alias
+ * d_q_in), rotates its K heads from d_k, and writes K and V (d_v) into the
+ * arena at (table[pos / bs], pos % bs).  Row strides are in elements, so the
+ * three parts of one fused QKV buffer can be passed directly.  d_cos / d_sin
+ * are the RoPE table [max_positions, head_dim/2] (tensor.rs:228-253).  As for
+ * attention, table lengths and block ids are the caller's guarantee. */
+int orion_hip_rope_and_cache(orion_hip_device* dev, const orion_hip_kv_layout* kv, void* d_arena,
+                             int64_t layer, int64_t num_rows, int64_t num_q_heads,
+                             const float* d_q_in, int64_t q_stride, float* d_q_out,
+                             const float* d_k, int64_t k_stride, const float* d_v,
+                             int64_t v_stride, const uint32_t* d_positions,
+                             const int32_t* d_row_seq, const int64_t* d_bt_offsets,
+                             const uint32_t* d_bt_ids, const float* d_cos, const float* d_sin);
+
+/* rms_norm (tensor.rs:143-163): d_out[r] = d_x[r] * (1/sqrt(mean(x^2)+eps)) * w.
+ * d_out may equal d_x. */
+int orion_hip_rmsnorm(orion_hip_device* dev, const float* d_x, const float* d_weight,
+                      int64_t rows, int64_t cols, float eps, float* d_out);
+
+/* linear (tensor.rs:96-130): d_out[M,N] = d_x[M,K] * W[N,K]^T (+ bias[N]),
+ * W bf16 row-major, x/out f32, f32 accumulation on bf16 MFMA (x is split
+ * into two bf16 terms so its f32 value is kept to ~16 mantissa bits).
+ * accumulate != 0 adds into d_out (residual connection, transformer.rs:328-332). */
+int orion_hip_gemm(orion_hip_device* dev, const float* d_x, const uint16_t* d_w,
+                   const float* d_bias, int64_t M, int64_t N, int64_t K, int accumulate,
+                   float* d_out);
+
+/* swiglu (tensor.rs:175-189): d_gate = silu(d_gate) * d_up, elementwise. */
+int orion_hip_silu_mul(orion_hip_device* dev, float* d_gate, const float* d_up, int64_t count);
+
+/* Greedy argmax per row (runtime/src/sampling.rs:196-207). */
+int orion_hip_argmax(orion_hip_device* dev, const float* d_logits, int64_t rows, int64_t cols,
+                     int64_t* d_out);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* ORION_HIP_H */

@@ -1,0 +1,89 @@
+// Shared device helpers for the gfx950 kernels (wave64, CDNA4).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <cstdint>
+
+namespace orion {
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef uint16_t u16x8 __attribute__((ext_vector_type(8)));
+
+constexpr int kWave = 64;
+
+// bf16 bits -> f32 is an exact widening (the reference's `half` crate does
+// the same, crates/orion-models/src/loader.rs:85-92).
+__device__ __host__ inline float bf16_to_f32(uint16_t b) {
+  uint32_t u = (uint32_t)b << 16;
+  float f;
+  __builtin_memcpy(&f, &u, 4);
+  return f;
+}
+
+// f32 -> bf16, round to nearest even; NaN stays a quiet NaN.
+__device__ __host__ inline uint16_t f32_to_bf16(float f) {
+  uint32_t u;
+  __builtin_memcpy(&u, &f, 4);
+  if ((u & 0x7f800000u) == 0x7f800000u && (u & 0x007fffffu)) return (uint16_t)((u >> 16) | 0x40);
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return (uint16_t)(u >> 16);
+}
+
+// The two bf16 halves of a packed dword, widened exactly.
+__device__ inline float bf16lo(uint32_t w) { return __uint_as_float(w << 16); }
+__device__ inline float bf16hi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
+
+// DPP lane exchange inside a row of 16 lanes.  Controls: quad_perm [1,0,3,2]
+// (xor 1), quad_perm [2,3,0,1] (xor 2), row_half_mirror (i <-> 7-i within 8),
+// row_mirror (i <-> 15-i within 16).  After the xor-1/xor-2 steps a quad holds
+// one value, so the mirrors pair each lane with a lane of the other half.
+template <int CTRL>
+__device__ inline float dpp(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, true));
+}
+constexpr int kDppXor1 = 0xB1;
+constexpr int kDppXor2 = 0x4E;
+constexpr int kDppHalfMirror = 0x141;
+constexpr int kDppMirror = 0x140;
+
+// Sum over groups of N consecutive lanes (N in 1..64, power of two); every
+// lane of a group ends with the group total.
+template <int N>
+__device__ inline float group_sum(float v) {
+  if constexpr (N >= 2) v += dpp<kDppXor1>(v);
+  if constexpr (N >= 4) v += dpp<kDppXor2>(v);
+  if constexpr (N >= 8) v += dpp<kDppHalfMirror>(v);
+  if constexpr (N >= 16) v += dpp<kDppMirror>(v);
+  if constexpr (N >= 32) v += __shfl_xor(v, 16);
+  if constexpr (N >= 64) v += __shfl_xor(v, 32);
+  return v;
+}
+
+template <int N>
+__device__ inline float group_max(float v) {
+  if constexpr (N >= 2) v = fmaxf(v, dpp<kDppXor1>(v));
+  if constexpr (N >= 4) v = fmaxf(v, dpp<kDppXor2>(v));
+  if constexpr (N >= 8) v = fmaxf(v, dpp<kDppHalfMirror>(v));
+  if constexpr (N >= 16) v = fmaxf(v, dpp<kDppMirror>(v));
+  if constexpr (N >= 32) v = fmaxf(v, __shfl_xor(v, 16));
+  if constexpr (N >= 64) v = fmaxf(v, __shfl_xor(v, 32));
+  return v;
+}
+
+__device__ inline float wave_sum(float v) { return group_sum<64>(v); }
+__device__ inline float wave_max(float v) { return group_max<64>(v); }
+
+__device__ inline double wave_sum_f64(double v) {
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
+  return v;
+}
+
+// Split an f32 into hi + lo bf16 terms: hi = rne(x), lo = rne(x - hi).
+// x - hi is exact in f32, so hi + lo carries ~16 significant bits of x.
+__device__ inline void split_bf16(float x, uint16_t& hi, uint16_t& lo) {
+  hi = f32_to_bf16(x);
+  lo = f32_to_bf16(x - bf16_to_f32(hi));
+}
+
+}  // namespace orion

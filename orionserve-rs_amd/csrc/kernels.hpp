@@ -1,0 +1,86 @@
+// Host-side launch wrappers for the gfx950 kernels (internal interface of
+// liborion_hip.so; the public C ABI lives in include/orion_hip.h).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <cstddef>
+#include <cstdint>
+
+namespace orion {
+
+// Geometry of a paged KV arena [layer][block][k|v][slot][kv_head][head_dim].
+struct KvGeom {
+  int64_t num_layers, num_blocks, block_size, num_kv_heads, head_dim;
+  bool dtype_bf16;
+};
+
+// ---- attention --------------------------------------------------------------
+int decode_partition_for(int64_t num_items, int64_t max_len, int64_t block_size);
+int64_t decode_max_splits(int64_t rows, int64_t hkv, int64_t max_position, int64_t block_size);
+size_t decode_workspace_bytes(int64_t rows, int64_t hq, int64_t D, int64_t max_splits);
+hipError_t launch_paged_decode(hipStream_t st, const KvGeom& kv, const void* arena, int64_t layer,
+                               const float* q, int64_t rows, int64_t hq,
+                               const uint32_t* positions, const int32_t* row_seq,
+                               const int64_t* bt_off, const uint32_t* bt_ids, int64_t max_position,
+                               float* out, float* ws, size_t ws_bytes);
+
+hipError_t launch_paged_prefill(hipStream_t st, const KvGeom& kv, const void* arena,
+                                int64_t layer, const float* q, int64_t hq, int64_t num_seqs,
+                                const int32_t* row_start, const int32_t* row_count,
+                                const uint32_t* first_pos, const int64_t* bt_off,
+                                const uint32_t* bt_ids, int64_t max_rows, int64_t max_position,
+                                float* out);
+
+// ---- GEMM -------------------------------------------------------------------
+enum class Epilogue : int {
+  kStore = 0,       // out = x W^T (+ bias)
+  kAccumulate = 1,  // out += x W^T
+  kSwiGLU = 2,      // W rows interleaved in groups of 8 gate / 8 up rows;
+                    // out[:, N/2] = silu(gate) * up
+};
+hipError_t launch_gemm(hipStream_t st, const float* x, const uint16_t* w, const float* bias,
+                       int64_t M, int64_t N, int64_t K, Epilogue ep, float* out);
+
+// ---- elementwise / normalisation -------------------------------------------
+hipError_t launch_embed(hipStream_t st, const uint32_t* tokens, int64_t n, const uint16_t* table,
+                        int64_t hidden, float* out);
+// rows selected by `row_index` (nullptr = identity)
+hipError_t launch_rmsnorm(hipStream_t st, const float* x, const int32_t* row_index,
+                          const float* weight, int64_t rows, int64_t cols, float eps, float* out);
+hipError_t launch_rope_and_cache(hipStream_t st, const KvGeom& kv, void* arena, int64_t layer,
+                                 int64_t rows, int64_t hq, const float* q_in, int64_t q_stride,
+                                 float* q_out, const float* k, int64_t k_stride, const float* v,
+                                 int64_t v_stride, const uint32_t* positions,
+                                 const int32_t* row_seq, const int64_t* bt_off,
+                                 const uint32_t* bt_ids, const float* cos_t, const float* sin_t);
+hipError_t launch_silu_mul(hipStream_t st, float* gate, const float* up, int64_t count);
+hipError_t launch_argmax(hipStream_t st, const float* logits, int64_t rows, int64_t cols,
+                         int64_t* out);
+hipError_t launch_f32_to_bf16(hipStream_t st, const float* in, uint16_t* out, int64_t count);
+hipError_t launch_synthetic_bf16(hipStream_t st, uint16_t* out, int64_t count, uint64_t key,
+                                 float mul);
+hipError_t launch_synthetic_f32(hipStream_t st, float* out, int64_t count, uint64_t key,
+                                float mul);
+hipError_t launch_fill_f32(hipStream_t st, float* out, int64_t count, float value);
+
+// Synthetic-weight generator shared by host and device: splitmix64 of a
+// per-tensor key plus the element index; the sum of the hash's four 16-bit
+// fields (Irwin-Hall, mean 131070, sd 65536/sqrt(3)) centred and scaled.
+__host__ __device__ inline uint64_t splitmix64(uint64_t x) {
+  x += 0x9E3779B97F4A7C15ull;
+  x = (x ^ (x >> 30)) * 0xBF58476D1CE4E5B9ull;
+  x = (x ^ (x >> 27)) * 0x94D049BB133111EBull;
+  return x ^ (x >> 31);
+}
+__host__ __device__ inline float synthetic_normal(uint64_t key, uint64_t index, float mul) {
+  const uint64_t h = splitmix64(key + index);
+  const int32_t s = (int32_t)(h & 0xffff) + (int32_t)((h >> 16) & 0xffff) +
+                    (int32_t)((h >> 32) & 0xffff) + (int32_t)(h >> 48);
+  return (float)(s - 131070) * mul;
+}
+inline uint64_t synthetic_key(uint64_t seed, int which, int layer) {
+  return splitmix64(seed ^ ((uint64_t)(which + 1) << 48) ^ ((uint64_t)(layer + 1) << 24));
+}
+constexpr float kIrwinHallSd = 37837.2265625f;  // 65536 / sqrt(3), rounded to f32
+
+}  // namespace orion

@@ -1,0 +1,991 @@
+// Host runtime behind the C ABI (include/orion_hip.h): device handles,
+// model weights and KV arena in HBM, batch validation/upload and the forward
+// pass orchestration.  Mirrors the reference's CpuBackend/TransformerModel
+// (crates/orion-models/src/backend.rs, transformer.rs) with every tensor
+// operation running as a gfx950 kernel on the device's stream.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cmath>
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <memory>
+#include <string>
+#include <vector>
+
+#include "../../include/orion_hip.h"
+#include "kernels.hpp"
+
+#define ORION_EXPORT extern "C" __attribute__((visibility("default")))
+
+using namespace orion;
+
+namespace {
+
+thread_local std::string g_err;
+thread_local std::string g_stage;
+
+int set_err(int code, const char* stage, const char* fmt, ...) {
+  char buf[1024];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof(buf), fmt, ap);
+  va_end(ap);
+  g_err = buf;
+  g_stage = stage;
+  return code;
+}
+
+int internal(const char* stage, const char* fmt, ...) {
+  char buf[1024];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof(buf), fmt, ap);
+  va_end(ap);
+  g_err = buf;
+  g_stage = stage;
+  return ORION_HIP_ERR_INTERNAL;
+}
+
+#define HIP_TRY(stage, expr)                                                               \
+  do {                                                                                     \
+    hipError_t _e = (expr);                                                                \
+    if (_e != hipSuccess)                                                                  \
+      return set_err(ORION_HIP_ERR_BACKEND, stage, "%s: %s", #expr, hipGetErrorString(_e)); \
+  } while (0)
+
+// A device allocation that grows on demand (never shrinks).
+struct DevBuf {
+  void* ptr = nullptr;
+  size_t bytes = 0;
+  hipError_t reserve(size_t want) {
+    if (want <= bytes) return hipSuccess;
+    if (ptr) {
+      // The old buffer may still be in use by queued work.
+      hipError_t e = hipDeviceSynchronize();
+      if (e != hipSuccess) return e;
+      e = hipFree(ptr);
+      if (e != hipSuccess) return e;
+      ptr = nullptr;
+      bytes = 0;
+    }
+    size_t rounded = std::max<size_t>(want, 256);
+    rounded = (rounded + (1 << 20) - 1) & ~((size_t)(1 << 20) - 1);
+    hipError_t e = hipMalloc(&ptr, rounded);
+    if (e != hipSuccess) {
+      ptr = nullptr;
+      return e;
+    }
+    bytes = rounded;
+    return hipSuccess;
+  }
+  void release() {
+    if (ptr) (void)hipFree(ptr);
+    ptr = nullptr;
+    bytes = 0;
+  }
+  template <typename T>
+  T* as() const {
+    return static_cast<T*>(ptr);
+  }
+};
+
+uint16_t host_f32_to_bf16(float f) {
+  uint32_t u;
+  std::memcpy(&u, &f, 4);
+  if ((u & 0x7f800000u) == 0x7f800000u && (u & 0x007fffffu)) return (uint16_t)((u >> 16) | 0x40);
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return (uint16_t)(u >> 16);
+}
+
+float host_bf16_to_f32(uint16_t b) {
+  uint32_t u = (uint32_t)b << 16;
+  float f;
+  std::memcpy(&f, &u, 4);
+  return f;
+}
+
+float host_f16_to_f32(uint16_t h) {
+  const uint32_t sign = (uint32_t)(h & 0x8000) << 16;
+  uint32_t exp = (h >> 10) & 0x1f;
+  uint32_t mant = h & 0x3ff;
+  uint32_t bits;
+  if (exp == 0) {
+    if (mant == 0) {
+      bits = sign;
+    } else {  // subnormal: renormalise
+      exp = 127 - 15 + 1;
+      while (!(mant & 0x400)) {
+        mant <<= 1;
+        --exp;
+      }
+      mant &= 0x3ff;
+      bits = sign | (exp << 23) | (mant << 13);
+    }
+  } else if (exp == 31) {
+    bits = sign | 0x7f800000u | (mant << 13);
+  } else {
+    bits = sign | ((exp + 127 - 15) << 23) | (mant << 13);
+  }
+  float f;
+  std::memcpy(&f, &bits, 4);
+  return f;
+}
+
+}  // namespace
+
+struct orion_hip_device {
+  int ordinal = 0;
+  hipStream_t stream = nullptr;
+  hipEvent_t ev_start = nullptr, ev_stop = nullptr;
+  std::string name;
+  DevBuf attn_ws;  // split-K workspace for the op-level attention entry point
+};
+
+struct LayerDev {
+  float* input_norm = nullptr;
+  float* post_norm = nullptr;
+  uint16_t* w_qkv = nullptr;  // [Hq*d + 2*Hkv*d, hidden]
+  float* b_qkv = nullptr;     // [Hq*d + 2*Hkv*d] or null
+  uint16_t* w_o = nullptr;    // [hidden, Hq*d]
+  uint16_t* w_gu = nullptr;   // [2*ffn, hidden], gate/up rows interleaved by 8
+  uint16_t* w_down = nullptr; // [hidden, ffn]
+};
+
+struct orion_hip_model {
+  orion_hip_device* dev = nullptr;
+  orion_hip_model_desc desc{};
+  int64_t qd = 0, kvd = 0, qkvd = 0;
+  KvGeom kv{};
+  std::vector<void*> allocations;
+  std::vector<size_t> alloc_bytes;
+  uint16_t* w_embed = nullptr;
+  uint16_t* w_lm = nullptr;  // null when tied
+  float* final_norm = nullptr;
+  std::vector<LayerDev> layers;
+  float* rope_cos = nullptr;
+  float* rope_sin = nullptr;
+  void* arena = nullptr;
+  size_t arena_bytes = 0;
+
+  // activations / batch buffers (grown on demand)
+  DevBuf hidden, xn, qkv, qrot, attn, act, logits, argmax, ws;
+  DevBuf b_tokens, b_positions, b_rowseq, b_btoff, b_btids, b_last;
+  void* pinned = nullptr;
+  size_t pinned_bytes = 0;
+
+  ~orion_hip_model() {
+    for (void* p : allocations) (void)hipFree(p);
+    for (DevBuf* b : {&hidden, &xn, &qkv, &qrot, &attn, &act, &logits, &argmax, &ws, &b_tokens,
+                      &b_positions, &b_rowseq, &b_btoff, &b_btids, &b_last})
+      b->release();
+    if (pinned) (void)hipHostFree(pinned);
+  }
+
+  template <typename T>
+  hipError_t alloc(T** out, size_t count) {
+    void* p = nullptr;
+    const size_t bytes = std::max<size_t>(count * sizeof(T), 256);
+    hipError_t e = hipMalloc(&p, bytes);
+    if (e != hipSuccess) return e;
+    allocations.push_back(p);
+    alloc_bytes.push_back(bytes);
+    *out = static_cast<T*>(p);
+    return hipSuccess;
+  }
+};
+
+// ---------------------------------------------------------------------------
+// Errors
+// ---------------------------------------------------------------------------
+
+ORION_EXPORT const char* orion_hip_last_error(void) { return g_err.c_str(); }
+ORION_EXPORT const char* orion_hip_last_error_stage(void) { return g_stage.c_str(); }
+
+// ---------------------------------------------------------------------------
+// Backend
+// ---------------------------------------------------------------------------
+
+ORION_EXPORT int orion_hip_device_count(int* count) {
+  int n = 0;
+  hipError_t e = hipGetDeviceCount(&n);
+  if (e != hipSuccess) n = 0;  // no driver / no GPU: zero devices, not an error
+  *count = n;
+  return ORION_HIP_OK;
+}
+
+ORION_EXPORT int orion_hip_device_open(int ordinal, orion_hip_device** out) {
+  *out = nullptr;
+  int n = 0;
+  orion_hip_device_count(&n);
+  if (n == 0) return set_err(ORION_HIP_ERR_BACKEND, "device_open", "no HIP devices are visible");
+  if (ordinal < 0 || ordinal >= n)
+    return set_err(ORION_HIP_ERR_BACKEND, "device_open", "device %d requested, %d available",
+                   ordinal, n);
+  HIP_TRY("device_open", hipSetDevice(ordinal));
+  hipDeviceProp_t prop;
+  HIP_TRY("device_open", hipGetDeviceProperties(&prop, ordinal));
+  if (std::strncmp(prop.gcnArchName, "gfx950", 6) != 0)
+    return set_err(ORION_HIP_ERR_BACKEND, "device_open",
+                   "device %d is %s; this library is built for gfx950 (MI355X) only", ordinal,
+                   prop.gcnArchName);
+  auto dev = std::make_unique<orion_hip_device>();
+  dev->ordinal = ordinal;
+  dev->name = prop.name;
+  HIP_TRY("device_open", hipStreamCreateWithFlags(&dev->stream, hipStreamNonBlocking));
+  HIP_TRY("device_open", hipEventCreate(&dev->ev_start));
+  HIP_TRY("device_open", hipEventCreate(&dev->ev_stop));
+  *out = dev.release();
+  return ORION_HIP_OK;
+}
+
+ORION_EXPORT void orion_hip_device_close(orion_hip_device* dev) {
+  if (!dev) return;
+  (void)hipSetDevice(dev->ordinal);
+  (void)hipStreamSynchronize(dev->stream);
+  dev->attn_ws.release();
+  (void)hipEventDestroy(dev->ev_start);
+  (void)hipEventDestroy(dev->ev_stop);
+  (void)hipStreamDestroy(dev->stream);
+  delete dev;
+}
+
+ORION_EXPORT int orion_hip_device_name(orion_hip_device* dev, char* buf, size_t len) {
+  if (!buf || len == 0) return internal("device_name", "empty buffer");
+  std::snprintf(buf, len, "%s", dev->name.c_str());
+  return ORION_HIP_OK;
+}
+
+ORION_EXPORT int orion_hip_mem_info(orion_hip_device* dev, uint64_t* total, uint64_t* free_bytes) {
+  HIP_TRY("mem_info", hipSetDevice(dev->ordinal));
+  size_t f = 0, t = 0;
+  HIP_TRY("mem_info", hipMemGetInfo(&f, &t));
+  *total = t;
+  *free_bytes = f;
+  return ORION_HIP_OK;
+}
+
+ORION_EXPORT int orion_hip_synchronize(orion_hip_device* dev) {
+  HIP_TRY("synchronize", hipStreamSynchronize(dev->stream));
+  return ORION_HIP_OK;
+}
+
+ORION_EXPORT int orion_hip_supports_dtype(orion_hip_device* dev, int dtype) {
+  (void)dev;
+  return dtype == ORION_DTYPE_F32 || dtype == ORION_DTYPE_F16 || dtype == ORION_DTYPE_BF16;
+}
+
+ORION_EXPORT int orion_hip_alloc(orion_hip_device* dev, size_t bytes, void** d_ptr) {
+  HIP_TRY("alloc", hipSetDevice(dev->ordinal));
+  HIP_TRY("alloc", hipMalloc(d_ptr, std::max<size_t>(bytes, 256)));
+  return ORION_HIP_OK;
+}
+
+ORION_EXPORT int orion_hip_free(orion_hip_device* dev, void* d_ptr) {
+  HIP_TRY("free", hipStreamSynchronize(dev->stream));
+  HIP_TRY("free", hipFree(d_ptr));
+  return ORION_HIP_OK;
+}
+
+ORION_EXPORT int orion_hip_memcpy_h2d(orion_hip_device* dev, void* d_dst, const void* src,
+                                      size_t bytes) {
+  HIP_TRY("memcpy_h2d", hipMemcpyAsync(d_dst, src, bytes, hipMemcpyHostToDevice, dev->stream));
+  HIP_TRY("memcpy_h2d", hipStreamSynchronize(dev->stream));
+  return ORION_HIP_OK;
+}
+
+ORION_EXPORT int orion_hip_memcpy_d2h(orion_hip_device* dev, void* dst, const void* d_src,
+                                      size_t bytes) {
+  HIP_TRY("memcpy_d2h", hipMemcpyAsync(dst, d_src, bytes, hipMemcpyDeviceToHost, dev->stream));
+  HIP_TRY("memcpy_d2h", hipStreamSynchronize(dev->stream));
+  return ORION_HIP_OK;
+}
+
+ORION_EXPORT int orion_hip_memcpy_d2d(orion_hip_device* dev, void* d_dst, const void* d_src,
+                                      size_t bytes) {
+  HIP_TRY("memcpy_d2d", hipMemcpyAsync(d_dst, d_src, bytes, hipMemcpyDeviceToDevice, dev->stream));
+  return ORION_HIP_OK;
+}
+
+ORION_EXPORT int orion_hip_memset(orion_hip_device* dev, void* d_dst, int value, size_t bytes) {
+  HIP_TRY("memset", hipMemsetAsync(d_dst, value, bytes, dev->stream));
+  return ORION_HIP_OK;
+}
+
+ORION_EXPORT int orion_hip_timer_start(orion_hip_device* dev) {
+  HIP_TRY("timer", hipEventRecord(dev->ev_start, dev->stream));
+  return ORION_HIP_OK;
+}
+
+ORION_EXPORT int orion_hip_timer_stop(orion_hip_device* dev, float* ms) {
+  HIP_TRY("timer", hipEventRecord(dev->ev_stop, dev->stream));
+  HIP_TRY("timer", hipEventSynchronize(dev->ev_stop));
+  HIP_TRY("timer", hipEventElapsedTime(ms, dev->ev_start, dev->ev_stop));
+  return ORION_HIP_OK;
+}
+
+// ---------------------------------------------------------------------------
+// Model
+// ---------------------------------------------------------------------------
+
+static int check_desc(const orion_hip_model_desc* d) {
+  const char* st = "model_create";
+  if (d->num_layers <= 0 || d->hidden_size <= 0 || d->num_attention_heads <= 0 ||
+      d->num_kv_heads <= 0 || d->head_dim <= 0 || d->intermediate_size <= 0 ||
+      d->vocab_size <= 0 || d->max_position_embeddings <= 0 || d->num_blocks <= 0)
+    return internal(st, "model dimensions must be positive");
+  if (d->num_attention_heads % d->num_kv_heads != 0)
+    return internal(st, "%d query heads cannot be grouped over %d kv heads",
+                    d->num_attention_heads, d->num_kv_heads);
+  if (d->block_size < 4 || d->block_size > 256 || (d->block_size & (d->block_size - 1)))
+    return internal(st, "block_size must be a power of two in [4, 256], got %d", d->block_size);
+  if (d->head_dim != 64 && d->head_dim != 128)
+    return set_err(ORION_HIP_ERR_BACKEND, st, "head_dim %d unsupported (64 or 128)", d->head_dim);
+  if (d->num_attention_heads / d->num_kv_heads > 8)
+    return set_err(ORION_HIP_ERR_BACKEND, st, "GQA group %d unsupported (at most 8)",
+                   d->num_attention_heads / d->num_kv_heads);
+  if (d->hidden_size % 32 || d->intermediate_size % 32 ||
+      (d->num_attention_heads * d->head_dim) % 32)
+    return set_err(ORION_HIP_ERR_BACKEND, st,
+                   "hidden, intermediate and Hq*head_dim must be multiples of 32");
+  if (d->kv_dtype != ORION_DTYPE_F32 && d->kv_dtype != ORION_DTYPE_BF16)
+    return set_err(ORION_HIP_ERR_BACKEND, st, "kv_dtype must be F32 or BF16");
+  return ORION_HIP_OK;
+}
+
+ORION_EXPORT int orion_hip_model_create(orion_hip_device* dev, const orion_hip_model_desc* desc,
+                                        orion_hip_model** out) {
+  *out = nullptr;
+  if (int rc = check_desc(desc)) return rc;
+  HIP_TRY("model_create", hipSetDevice(dev->ordinal));
+  auto m = std::make_unique<orion_hip_model>();
+  m->dev = dev;
+  m->desc = *desc;
+  const auto& d = *desc;
+  m->qd = (int64_t)d.num_attention_heads * d.head_dim;
+  m->kvd = (int64_t)d.num_kv_heads * d.head_dim;
+  m->qkvd = m->qd + 2 * m->kvd;
+  m->kv = KvGeom{d.num_layers, d.num_blocks, d.block_size, d.num_kv_heads, d.head_dim,
+                 d.kv_dtype == ORION_DTYPE_BF16};
+  const int64_t H = d.hidden_size, F = d.intermediate_size, V = d.vocab_size;
+  const char* st = "model_create";
+  HIP_TRY(st, m->alloc(&m->w_embed, (size_t)(V * H)));
+  if (!d.tied_lm_head) HIP_TRY(st, m->alloc(&m->w_lm, (size_t)(V * H)));
+  HIP_TRY(st, m->alloc(&m->final_norm, (size_t)H));
+  m->layers.resize(d.num_layers);
+  for (auto& L : m->layers) {
+    HIP_TRY(st, m->alloc(&L.input_norm, (size_t)H));
+    HIP_TRY(st, m->alloc(&L.post_norm, (size_t)H));
+    HIP_TRY(st, m->alloc(&L.w_qkv, (size_t)(m->qkvd * H)));
+    if (d.has_qkv_bias) HIP_TRY(st, m->alloc(&L.b_qkv, (size_t)m->qkvd));
+    HIP_TRY(st, m->alloc(&L.w_o, (size_t)(H * m->qd)));
+    HIP_TRY(st, m->alloc(&L.w_gu, (size_t)(2 * F * H)));
+    HIP_TRY(st, m->alloc(&L.w_down, (size_t)(H * F)));
+  }
+  // Zero every weight so an un-uploaded tensor is deterministic.
+  for (size_t i = 0; i < m->allocations.size(); ++i)
+    HIP_TRY(st, hipMemsetAsync(m->allocations[i], 0, m->alloc_bytes[i], dev->stream));
+  const int64_t half = d.head_dim / 2;
+  const int64_t tab = (int64_t)d.max_position_embeddings * half;
+  HIP_TRY(st, m->alloc(&m->rope_cos, (size_t)tab));
+  HIP_TRY(st, m->alloc(&m->rope_sin, (size_t)tab));
+  {
+    // RopeTable::new (tensor.rs:228-253), computed on the host with the same
+    // f32 libm calls as the reference and uploaded once.
+    std::vector<float> c(tab), s(tab);
+    for (int64_t pos = 0; pos < d.max_position_embeddings; ++pos)
+      for (int64_t i = 0; i < half; ++i) {
+        const float inv_freq =
+            1.0f / std::pow(d.rope_theta, 2.0f * (float)i / (float)d.head_dim);
+        const float angle = (float)pos * inv_freq;
+        c[pos * half + i] = std::cos(angle);
+        s[pos * half + i] = std::sin(angle);
+      }
+    HIP_TRY(st, hipMemcpy(m->rope_cos, c.data(), tab * 4, hipMemcpyHostToDevice));
+    HIP_TRY(st, hipMemcpy(m->rope_sin, s.data(), tab * 4, hipMemcpyHostToDevice));
+  }
+  // KvStore::new (attention.rs:45-62): zero-filled arena.
+  const size_t esz = m->kv.dtype_bf16 ? 2 : 4;
+  m->arena_bytes = (size_t)d.num_layers * d.num_blocks * 2 * d.block_size * d.num_kv_heads *
+                   d.head_dim * esz;
+  HIP_TRY(st, hipMalloc(&m->arena, m->arena_bytes));
+  m->allocations.push_back(m->arena);
+  m->alloc_bytes.push_back(m->arena_bytes);
+  HIP_TRY(st, hipMemsetAsync(m->arena, 0, m->arena_bytes, dev->stream));
+  HIP_TRY(st, hipStreamSynchronize(dev->stream));
+  *out = m.release();
+  return ORION_HIP_OK;
+}
+
+ORION_EXPORT void orion_hip_model_destroy(orion_hip_model* model) {
+  if (!model) return;
+  (void)hipSetDevice(model->dev->ordinal);
+  (void)hipStreamSynchronize(model->dev->stream);
+  delete model;
+}
+
+// Where a weight lives on the device: base pointer, element type, and the
+// row mapping used by the fused layouts.
+struct WeightSlot {
+  void* base = nullptr;
+  bool bf16 = true;
+  int64_t rows = 0, cols = 0;
+  // destination row of source row r: (r / group) * stride + offset + r % group
+  int64_t group = 0, stride = 0, offset = 0;
+};
+
+static int weight_slot(orion_hip_model* m, int which, int layer, WeightSlot* s) {
+  const auto& d = m->desc;
+  const int64_t H = d.hidden_size, F = d.intermediate_size, V = d.vocab_size;
+  if (which >= ORION_W_INPUT_NORM && (layer < 0 || layer >= d.num_layers))
+    return internal("upload_weight", "layer %d out of range (have %d)", layer, d.num_layers);
+  LayerDev* L = which >= ORION_W_INPUT_NORM ? &m->layers[layer] : nullptr;
+  *s = WeightSlot{};
+  switch (which) {
+    case ORION_W_EMBED: *s = {m->w_embed, true, V, H}; break;
+    case ORION_W_LM_HEAD:
+      if (!m->w_lm) return internal("upload_weight", "model has a tied LM head");
+      *s = {m->w_lm, true, V, H};
+      break;
+    case ORION_W_FINAL_NORM: *s = {m->final_norm, false, 1, H}; break;
+    case ORION_W_INPUT_NORM: *s = {L->input_norm, false, 1, H}; break;
+    case ORION_W_POST_NORM: *s = {L->post_norm, false, 1, H}; break;
+    case ORION_W_Q: *s = {L->w_qkv, true, m->qd, H}; break;
+    case ORION_W_K: *s = {L->w_qkv + m->qd * H, true, m->kvd, H}; break;
+    case ORION_W_V: *s = {L->w_qkv + (m->qd + m->kvd) * H, true, m->kvd, H}; break;
+    case ORION_W_O: *s = {L->w_o, true, H, m->qd}; break;
+    case ORION_W_Q_BIAS:
+    case ORION_W_K_BIAS:
+    case ORION_W_V_BIAS: {
+      if (!L->b_qkv) return internal("upload_weight", "model has no QKV bias");
+      const int64_t off = which == ORION_W_Q_BIAS ? 0 : which == ORION_W_K_BIAS ? m->qd : m->qd + m->kvd;
+      *s = {L->b_qkv + off, false, 1, which == ORION_W_Q_BIAS ? m->qd : m->kvd};
+      break;
+    }
+    case ORION_W_GATE: *s = {L->w_gu, true, F, H, 8, 16, 0}; break;
+    case ORION_W_UP: *s = {L->w_gu, true, F, H, 8, 16, 8}; break;
+    case ORION_W_DOWN: *s = {L->w_down, true, H, F}; break;
+    default: return internal("upload_weight", "unknown weight id %d", which);
+  }
+  return ORION_HIP_OK;
+}
+
+static int upload_rows(orion_hip_model* m, const WeightSlot& s, const void* host_conv,
+                       size_t esz, const char* st) {
+  hipStream_t stream = m->dev->stream;
+  if (s.group == 0) {
+    HIP_TRY(st, hipMemcpyAsync(s.base, host_conv, (size_t)(s.rows * s.cols) * esz,
+                               hipMemcpyHostToDevice, stream));
+  } else {
+    // rows come in groups of `group`; group g lands at row g*stride + offset.
+    const size_t row_bytes = (size_t)s.cols * esz;
+    HIP_TRY(st, hipMemcpy2DAsync(static_cast<char*>(s.base) + s.offset * row_bytes,
+                                 s.stride * row_bytes, host_conv, s.group * row_bytes,
+                                 s.group * row_bytes, (size_t)(s.rows / s.group),
+                                 hipMemcpyHostToDevice, stream));
+  }
+  HIP_TRY(st, hipStreamSynchronize(stream));
+  return ORION_HIP_OK;
+}
+
+ORION_EXPORT int orion_hip_model_upload_weight(orion_hip_model* model, int which, int layer,
+                                               const void* host, int dtype, size_t count) {
+  const char* st = "upload_weight";
+  WeightSlot s;
+  if (int rc = weight_slot(model, which, layer, &s)) return rc;
+  if ((int64_t)count != s.rows * s.cols)
+    return internal(st, "weight %d has %zu elements, expected %lld", which, count,
+                    (long long)(s.rows * s.cols));
+  if (dtype != ORION_DTYPE_F32 && dtype != ORION_DTYPE_F16 && dtype != ORION_DTYPE_BF16)
+    return set_err(ORION_HIP_ERR_BACKEND, st, "unsupported host dtype %d", dtype);
+  HIP_TRY(st, hipSetDevice(model->dev->ordinal));
+  // Convert on the host (loader.rs:74-98 widens to f32; device matrices are bf16).
+  if (s.bf16) {
+    std::vector<uint16_t> conv(count);
+    if (dtype == ORION_DTYPE_BF16) {
+      std::memcpy(conv.data(), host, count * 2);
+    } else if (dtype == ORION_DTYPE_F32) {
+      const float* f = static_cast<const float*>(host);
+      for (size_t i = 0; i < count; ++i) conv[i] = host_f32_to_bf16(f[i]);
+    } else {
+      const uint16_t* h = static_cast<const uint16_t*>(host);
+      for (size_t i = 0; i < count; ++i) conv[i] = host_f32_to_bf16(host_f16_to_f32(h[i]));
+    }
+    return upload_rows(model, s, conv.data(), 2, st);
+  }
+  std::vector<float> conv(count);
+  if (dtype == ORION_DTYPE_F32) {
+    std::memcpy(conv.data(), host, count * 4);
+  } else if (dtype == ORION_DTYPE_BF16) {
+    const uint16_t* h = static_cast<const uint16_t*>(host);
+    for (size_t i = 0; i < count; ++i) conv[i] = host_bf16_to_f32(h[i]);
+  } else {
+    const uint16_t* h = static_cast<const uint16_t*>(host);
+    for (size_t i = 0; i < count; ++i) conv[i] = host_f16_to_f32(h[i]);
+  }
+  return upload_rows(model, s, conv.data(), 4, st);
+}
+
+ORION_EXPORT int orion_hip_model_download_weight(orion_hip_model* model, int which, int layer,
+                                                 float* host, size_t count) {
+  const char* st = "download_weight";
+  WeightSlot s;
+  if (int rc = weight_slot(model, which, layer, &s)) return rc;
+  if ((int64_t)count != s.rows * s.cols)
+    return internal(st, "weight %d has %lld elements, asked for %zu", which,
+                    (long long)(s.rows * s.cols), count);
+  HIP_TRY(st, hipSetDevice(model->dev->ordinal));
+  hipStream_t stream = model->dev->stream;
+  const size_t esz = s.bf16 ? 2 : 4;
+  std::vector<char> raw(count * esz);
+  if (s.group == 0) {
+    HIP_TRY(st, hipMemcpyAsync(raw.data(), s.base, count * esz, hipMemcpyDeviceToHost, stream));
+  } else {
+    const size_t row_bytes = (size_t)s.cols * esz;
+    HIP_TRY(st, hipMemcpy2DAsync(raw.data(), s.group * row_bytes,
+                                 static_cast<char*>(s.base) + s.offset * row_bytes,
+                                 s.stride * row_bytes, s.group * row_bytes,
+                                 (size_t)(s.rows / s.group), hipMemcpyDeviceToHost, stream));
+  }
+  HIP_TRY(st, hipStreamSynchronize(stream));
+  if (s.bf16) {
+    const uint16_t* b = reinterpret_cast<const uint16_t*>(raw.data());
+    for (size_t i = 0; i < count; ++i) host[i] = host_bf16_to_f32(b[i]);
+  } else {
+    std::memcpy(host, raw.data(), count * 4);
+  }
+  return ORION_HIP_OK;
+}
+
+ORION_EXPORT float orion_hip_synthetic_value(uint64_t seed, int which, int layer, uint64_t index,
+                                             float std_) {
+  const bool is_norm =
+      which == ORION_W_FINAL_NORM || which == ORION_W_INPUT_NORM || which == ORION_W_POST_NORM;
+  if (is_norm) return 1.0f;
+  const float mul = std_ / kIrwinHallSd;
+  const uint64_t key = synthetic_key(seed, which, which >= ORION_W_INPUT_NORM ? layer : -1);
+  return host_bf16_to_f32(host_f32_to_bf16(synthetic_normal(key, index, mul)));
+}
+
+static int init_one(orion_hip_model* m, int which, int layer, uint64_t seed, float std_) {
+  const char* st = "init_synthetic";
+  WeightSlot s;
+  if (int rc = weight_slot(m, which, layer, &s)) return rc;
+  hipStream_t stream = m->dev->stream;
+  const float mul = std_ / kIrwinHallSd;
+  const uint64_t key = synthetic_key(seed, which, which >= ORION_W_INPUT_NORM ? layer : -1);
+  const int64_t count = s.rows * s.cols;
+  const bool is_norm =
+      which == ORION_W_FINAL_NORM || which == ORION_W_INPUT_NORM || which == ORION_W_POST_NORM;
+  if (is_norm) {
+    HIP_TRY(st, launch_fill_f32(stream, static_cast<float*>(s.base), count, 1.0f));
+    return ORION_HIP_OK;
+  }
+  if (!s.bf16) {
+    HIP_TRY(st, launch_synthetic_f32(stream, static_cast<float*>(s.base), count, key, mul));
+    return ORION_HIP_OK;
+  }
+  if (s.group == 0) {
+    HIP_TRY(st, launch_synthetic_bf16(stream, static_cast<uint16_t*>(s.base), count, key, mul));
+    return ORION_HIP_OK;
+  }
+  // Interleaved gate/up: generate in logical order into a scratch buffer,
+  // then scatter the row groups.
+  DevBuf tmp;
+  HIP_TRY(st, tmp.reserve((size_t)count * 2));
+  HIP_TRY(st, launch_synthetic_bf16(stream, tmp.as<uint16_t>(), count, key, mul));
+  const size_t row_bytes = (size_t)s.cols * 2;
+  HIP_TRY(st, hipMemcpy2DAsync(static_cast<char*>(s.base) + s.offset * row_bytes,
+                               s.stride * row_bytes, tmp.ptr, s.group * row_bytes,
+                               s.group * row_bytes, (size_t)(s.rows / s.group),
+                               hipMemcpyDeviceToDevice, stream));
+  HIP_TRY(st, hipStreamSynchronize(stream));
+  tmp.release();
+  return ORION_HIP_OK;
+}
+
+ORION_EXPORT int orion_hip_model_init_synthetic(orion_hip_model* model, uint64_t seed, float std_) {
+  HIP_TRY("init_synthetic", hipSetDevice(model->dev->ordinal));
+  const auto& d = model->desc;
+  if (int rc = init_one(model, ORION_W_EMBED, -1, seed, std_)) return rc;
+  if (!d.tied_lm_head)
+    if (int rc = init_one(model, ORION_W_LM_HEAD, -1, seed, std_)) return rc;
+  if (int rc = init_one(model, ORION_W_FINAL_NORM, -1, seed, std_)) return rc;
+  for (int l = 0; l < d.num_layers; ++l) {
+    for (int w = ORION_W_INPUT_NORM; w <= ORION_W_DOWN; ++w) {
+      if ((w == ORION_W_Q_BIAS || w == ORION_W_K_BIAS || w == ORION_W_V_BIAS) && !d.has_qkv_bias)
+        continue;
+      if (int rc = init_one(model, w, l, seed, std_)) return rc;
+    }
+  }
+  HIP_TRY("init_synthetic", hipStreamSynchronize(model->dev->stream));
+  return ORION_HIP_OK;
+}
+
+// ---------------------------------------------------------------------------
+// KV arena access (KvStore::read/write, attention.rs:107-175)
+// ---------------------------------------------------------------------------
+
+static int kv_bounds(orion_hip_model* m, int64_t layer, uint32_t block, int64_t slot,
+                     int64_t head, int64_t vec_len, const char* st) {
+  const auto& d = m->desc;
+  if (layer < 0 || layer >= d.num_layers)
+    return internal(st, "layer %lld out of range (have %d)", (long long)layer, d.num_layers);
+  if ((int64_t)block >= d.num_blocks)
+    return internal(st, "block %u out of range (have %d)", block, d.num_blocks);
+  if (slot < 0 || slot >= d.block_size)
+    return internal(st, "slot %lld out of range (block holds %d)", (long long)slot, d.block_size);
+  if (head < 0 || head >= d.num_kv_heads)
+    return internal(st, "kv head %lld out of range (have %d)", (long long)head, d.num_kv_heads);
+  if (vec_len != d.head_dim)
+    return internal(st, "vector length %lld does not match head_dim %d", (long long)vec_len,
+                    d.head_dim);
+  return ORION_HIP_OK;
+}
+
+static size_t kv_offset_elems(orion_hip_model* m, int64_t layer, uint32_t block, int is_value,
+                              int64_t slot, int64_t head) {
+  const auto& d = m->desc;
+  const int64_t stride = (int64_t)d.block_size * d.num_kv_heads * d.head_dim;
+  const int64_t per_block = 2 * stride;
+  const int64_t per_layer = (int64_t)d.num_blocks * per_block;
+  return (size_t)(layer * per_layer + (int64_t)block * per_block + (is_value ? stride : 0) +
+                  (slot * d.num_kv_heads + head) * d.head_dim);
+}
+
+ORION_EXPORT int orion_hip_model_kv_read(orion_hip_model* model, int64_t layer, uint32_t block,
+                                         int64_t slot, int64_t head, int is_value, float* out) {
+  const char* st = "kv_read";
+  if (int rc = kv_bounds(model, layer, block, slot, head, model->desc.head_dim, st)) return rc;
+  const size_t off = kv_offset_elems(model, layer, block, is_value, slot, head);
+  const int64_t d = model->desc.head_dim;
+  hipStream_t stream = model->dev->stream;
+  if (model->kv.dtype_bf16) {
+    std::vector<uint16_t> tmp(d);
+    HIP_TRY(st, hipMemcpyAsync(tmp.data(), static_cast<uint16_t*>(model->arena) + off, d * 2,
+                               hipMemcpyDeviceToHost, stream));
+    HIP_TRY(st, hipStreamSynchronize(stream));
+    for (int64_t i = 0; i < d; ++i) out[i] = host_bf16_to_f32(tmp[i]);
+  } else {
+    HIP_TRY(st, hipMemcpyAsync(out, static_cast<float*>(model->arena) + off, d * 4,
+                               hipMemcpyDeviceToHost, stream));
+    HIP_TRY(st, hipStreamSynchronize(stream));
+  }
+  return ORION_HIP_OK;
+}
+
+ORION_EXPORT int orion_hip_model_kv_write(orion_hip_model* model, int64_t layer, uint32_t block,
+                                          int64_t slot, int64_t head, int is_value,
+                                          const float* vec, int64_t len) {
+  const char* st = "kv_write";
+  if (int rc = kv_bounds(model, layer, block, slot, head, len, st)) return rc;
+  const size_t off = kv_offset_elems(model, layer, block, is_value, slot, head);
+  hipStream_t stream = model->dev->stream;
+  if (model->kv.dtype_bf16) {
+    std::vector<uint16_t> tmp(len);
+    for (int64_t i = 0; i < len; ++i) tmp[i] = host_f32_to_bf16(vec[i]);
+    HIP_TRY(st, hipMemcpyAsync(static_cast<uint16_t*>(model->arena) + off, tmp.data(), len * 2,
+                               hipMemcpyHostToDevice, stream));
+    HIP_TRY(st, hipStreamSynchronize(stream));
+  } else {
+    HIP_TRY(st, hipMemcpyAsync(static_cast<float*>(model->arena) + off, vec, len * 4,
+                               hipMemcpyHostToDevice, stream));
+    HIP_TRY(st, hipStreamSynchronize(stream));
+  }
+  return ORION_HIP_OK;
+}
+
+ORION_EXPORT int orion_hip_model_kv_arena(orion_hip_model* model, void** d_arena, size_t* bytes) {
+  *d_arena = model->arena;
+  *bytes = model->arena_bytes;
+  return ORION_HIP_OK;
+}
+
+// ---------------------------------------------------------------------------
+// Forward (transformer.rs:359-442)
+// ---------------------------------------------------------------------------
+
+namespace {
+
+struct HostBatch {
+  std::vector<int32_t> row_seq;
+  std::vector<int32_t> last_rows;
+  int64_t max_position = 0;
+};
+
+// ForwardBatch::validate (traits.rs:232-261) plus every check the reference
+// performs while computing (transformer.rs:212-217, :257-262, :376-385,
+// attention.rs:136-175, :411-419), done once on the host before launch.
+int validate_batch(orion_hip_model* m, const orion_hip_batch* b, HostBatch* hb) {
+  const char* st = "forward";
+  const auto& d = m->desc;
+  const int64_t n = b->num_tokens, S = b->num_seqs;
+  if (n < 0 || S < 0) return internal(st, "negative batch sizes");
+  int64_t summed = 0;
+  for (int64_t s = 0; s < S; ++s) {
+    if (b->slot_token_counts[s] < 0) return internal(st, "negative slot token count");
+    summed += b->slot_token_counts[s];
+  }
+  if (summed != n)
+    return internal(st, "ForwardBatch slot token counts sum to %lld but there are %lld tokens",
+                    (long long)summed, (long long)n);
+  if (n == 0) return ORION_HIP_OK;
+  if (b->block_table_offsets[0] != 0) return internal(st, "block table offsets must start at 0");
+  for (int64_t s = 0; s < S; ++s) {
+    if (b->block_table_offsets[s + 1] < b->block_table_offsets[s])
+      return internal(st, "block table offsets must be non-decreasing");
+    if (b->slot_token_counts[s] == 0)
+      return internal(st, "a scheduled sequence contributed zero tokens");
+  }
+  hb->row_seq.resize(n);
+  hb->last_rows.resize(S);
+  std::vector<int64_t> seq_max_pos(S, -1);
+  int64_t row = 0;
+  for (int64_t s = 0; s < S; ++s) {
+    for (int64_t c = 0; c < b->slot_token_counts[s]; ++c, ++row) {
+      hb->row_seq[row] = (int32_t)s;
+      const uint32_t tok = b->tokens[row];
+      const int64_t pos = b->positions[row];
+      if ((int64_t)tok >= d.vocab_size)
+        return internal(st, "token id %u is outside the vocabulary of %d", tok, d.vocab_size);
+      const int64_t tlen = b->block_table_offsets[s + 1] - b->block_table_offsets[s];
+      if (pos / d.block_size >= tlen)
+        return internal(st, "position %lld has no block in the table for sequence %lld",
+                        (long long)pos, (long long)s);
+      if (pos >= d.max_position_embeddings)
+        return internal(st, "position %lld exceeds the RoPE table (%d entries)", (long long)pos,
+                        d.max_position_embeddings);
+      seq_max_pos[s] = std::max(seq_max_pos[s], pos);
+      hb->max_position = std::max(hb->max_position, pos);
+    }
+    hb->last_rows[s] = (int32_t)(row - 1);
+  }
+  // Every block a row can attend to (positions 0..=pos) must exist in the arena.
+  for (int64_t s = 0; s < S; ++s) {
+    const int64_t used = seq_max_pos[s] / d.block_size + 1;
+    const uint32_t* tbl = b->block_table_ids + b->block_table_offsets[s];
+    for (int64_t i = 0; i < used; ++i)
+      if ((int64_t)tbl[i] >= d.num_blocks)
+        return internal(st, "block %u out of range (have %d)", tbl[i], d.num_blocks);
+  }
+  return ORION_HIP_OK;
+}
+
+}  // namespace
+
+ORION_EXPORT int orion_hip_model_forward(orion_hip_model* m, const orion_hip_batch* b,
+                                         float* logits_out, int64_t* argmax_out) {
+  const char* st = "forward";
+  HostBatch hb;
+  if (int rc = validate_batch(m, b, &hb)) return rc;
+  const int64_t n = b->num_tokens, S = b->num_seqs;
+  if (n == 0) return ORION_HIP_OK;
+  const auto& d = m->desc;
+  const int64_t H = d.hidden_size, F = d.intermediate_size, V = d.vocab_size;
+  const int64_t Hq = d.num_attention_heads;
+  hipStream_t stream = m->dev->stream;
+  HIP_TRY(st, hipSetDevice(m->dev->ordinal));
+
+  // ---- capacity ----
+  const int64_t nbt = b->block_table_offsets[S];
+  HIP_TRY(st, m->hidden.reserve(n * H * 4));
+  HIP_TRY(st, m->xn.reserve(n * H * 4));
+  HIP_TRY(st, m->qkv.reserve(n * m->qkvd * 4));
+  HIP_TRY(st, m->qrot.reserve(n * m->qd * 4));
+  HIP_TRY(st, m->attn.reserve(n * m->qd * 4));
+  HIP_TRY(st, m->act.reserve(n * F * 4));
+  HIP_TRY(st, m->logits.reserve(S * V * 4));
+  HIP_TRY(st, m->argmax.reserve(S * 8));
+  const int64_t splits = decode_max_splits(n, d.num_kv_heads, hb.max_position, d.block_size);
+  HIP_TRY(st, m->ws.reserve(decode_workspace_bytes(n, Hq, d.head_dim, splits)));
+
+  // ---- upload the batch: one pinned staging area, one copy ----
+  const size_t o_tok = 0;
+  const size_t o_pos = o_tok + n * 4;
+  const size_t o_rs = o_pos + n * 4;
+  const size_t o_last = o_rs + n * 4;
+  const size_t o_btoff = (o_last + S * 4 + 7) & ~(size_t)7;
+  const size_t o_btids = o_btoff + (S + 1) * 8;
+  const size_t total = o_btids + nbt * 4;
+  if (total > m->pinned_bytes) {
+    if (m->pinned) {
+      HIP_TRY(st, hipStreamSynchronize(stream));
+      HIP_TRY(st, hipHostFree(m->pinned));
+      m->pinned = nullptr;
+    }
+    const size_t cap = std::max<size_t>(total * 2, 1 << 16);
+    HIP_TRY(st, hipHostMalloc(&m->pinned, cap, hipHostMallocDefault));
+    m->pinned_bytes = cap;
+  }
+  HIP_TRY(st, m->b_tokens.reserve(total));
+  char* hp = static_cast<char*>(m->pinned);
+  // The previous forward's copy out of the staging area completed at its sync.
+  std::memcpy(hp + o_tok, b->tokens, n * 4);
+  std::memcpy(hp + o_pos, b->positions, n * 4);
+  std::memcpy(hp + o_rs, hb.row_seq.data(), n * 4);
+  std::memcpy(hp + o_last, hb.last_rows.data(), S * 4);
+  std::memcpy(hp + o_btoff, b->block_table_offsets, (S + 1) * 8);
+  std::memcpy(hp + o_btids, b->block_table_ids, nbt * 4);
+  char* dp = m->b_tokens.as<char>();
+  HIP_TRY(st, hipMemcpyAsync(dp, hp, total, hipMemcpyHostToDevice, stream));
+  const uint32_t* d_tok = reinterpret_cast<const uint32_t*>(dp + o_tok);
+  const uint32_t* d_pos = reinterpret_cast<const uint32_t*>(dp + o_pos);
+  const int32_t* d_rs = reinterpret_cast<const int32_t*>(dp + o_rs);
+  const int32_t* d_last = reinterpret_cast<const int32_t*>(dp + o_last);
+  const int64_t* d_btoff = reinterpret_cast<const int64_t*>(dp + o_btoff);
+  const uint32_t* d_btids = reinterpret_cast<const uint32_t*>(dp + o_btids);
+
+  float* hidden = m->hidden.as<float>();
+  float* xn = m->xn.as<float>();
+  float* qkv = m->qkv.as<float>();
+  float* qrot = m->qrot.as<float>();
+  float* attn = m->attn.as<float>();
+  float* act = m->act.as<float>();
+
+  HIP_TRY(st, launch_embed(stream, d_tok, n, m->w_embed, H, hidden));
+  for (int64_t l = 0; l < d.num_layers; ++l) {
+    const LayerDev& L = m->layers[l];
+    HIP_TRY(st, launch_rmsnorm(stream, hidden, nullptr, L.input_norm, n, H, d.rms_norm_eps, xn));
+    HIP_TRY(st, launch_gemm(stream, xn, L.w_qkv, L.b_qkv, n, m->qkvd, H, Epilogue::kStore, qkv));
+    HIP_TRY(st, launch_rope_and_cache(stream, m->kv, m->arena, l, n, Hq, qkv, m->qkvd, qrot,
+                                      qkv + m->qd, m->qkvd, qkv + m->qd + m->kvd, m->qkvd, d_pos,
+                                      d_rs, d_btoff, d_btids, m->rope_cos, m->rope_sin));
+    HIP_TRY(st, launch_paged_decode(stream, m->kv, m->arena, l, qrot, n, Hq, d_pos, d_rs, d_btoff,
+                                    d_btids, hb.max_position, attn, m->ws.as<float>(),
+                                    m->ws.bytes));
+    HIP_TRY(st, launch_gemm(stream, attn, L.w_o, nullptr, n, H, m->qd, Epilogue::kAccumulate,
+                            hidden));
+    HIP_TRY(st, launch_rmsnorm(stream, hidden, nullptr, L.post_norm, n, H, d.rms_norm_eps, xn));
+    HIP_TRY(st, launch_gemm(stream, xn, L.w_gu, nullptr, n, 2 * F, H, Epilogue::kSwiGLU, act));
+    HIP_TRY(st, launch_gemm(stream, act, L.w_down, nullptr, n, H, F, Epilogue::kAccumulate,
+                            hidden));
+  }
+  // Final norm on the last row of each sequence only (norm is row-wise, so
+  // this equals norming all rows and then gathering), then the LM head.
+  HIP_TRY(st, launch_rmsnorm(stream, hidden, d_last, m->final_norm, S, H, d.rms_norm_eps, xn));
+  const uint16_t* head = m->w_lm ? m->w_lm : m->w_embed;
+  float* logits = m->logits.as<float>();
+  HIP_TRY(st, launch_gemm(stream, xn, head, nullptr, S, V, H, Epilogue::kStore, logits));
+  if (argmax_out) {
+    HIP_TRY(st, launch_argmax(stream, logits, S, V, m->argmax.as<int64_t>()));
+    HIP_TRY(st, hipMemcpyAsync(argmax_out, m->argmax.ptr, S * 8, hipMemcpyDeviceToHost, stream));
+  }
+  if (logits_out)
+    HIP_TRY(st, hipMemcpyAsync(logits_out, logits, S * V * 4, hipMemcpyDeviceToHost, stream));
+  HIP_TRY(st, hipStreamSynchronize(stream));
+  return ORION_HIP_OK;
+}
+
+// ---------------------------------------------------------------------------
+// Op-level entry points
+// ---------------------------------------------------------------------------
+
+static int kv_geom_from(const orion_hip_kv_layout* kv, KvGeom* g, const char* st) {
+  if (kv->dtype != ORION_DTYPE_F32 && kv->dtype != ORION_DTYPE_BF16)
+    return set_err(ORION_HIP_ERR_BACKEND, st, "kv dtype must be F32 or BF16");
+  if (kv->block_size < 1 || (kv->block_size & (kv->block_size - 1)) || kv->block_size > 256)
+    return internal(st, "block_size must be a power of two <= 256");
+  if (kv->head_dim != 64 && kv->head_dim != 128)
+    return set_err(ORION_HIP_ERR_BACKEND, st, "head_dim %lld unsupported (64 or 128)",
+                   (long long)kv->head_dim);
+  *g = KvGeom{kv->num_layers, kv->num_blocks, kv->block_size, kv->num_kv_heads, kv->head_dim,
+              kv->dtype == ORION_DTYPE_BF16};
+  return ORION_HIP_OK;
+}
+
+ORION_EXPORT int orion_hip_paged_attention_decode(
+    orion_hip_device* dev, const orion_hip_kv_layout* kv, const void* d_arena, int64_t layer,
+    const float* d_q, int64_t num_rows, int64_t num_q_heads, const uint32_t* d_positions,
+    const int32_t* d_row_seq, const int64_t* d_bt_offsets, const uint32_t* d_bt_ids,
+    int64_t max_position, float* d_out) {
+  const char* st = "paged_attention_decode";
+  KvGeom g;
+  if (int rc = kv_geom_from(kv, &g, st)) return rc;
+  if (g.num_kv_heads <= 0 || num_q_heads % g.num_kv_heads)
+    return internal(st, "%lld query heads cannot be grouped over %lld kv heads",
+                    (long long)num_q_heads, (long long)g.num_kv_heads);
+  if (num_q_heads / g.num_kv_heads > 8)
+    return set_err(ORION_HIP_ERR_BACKEND, st, "GQA group above 8 unsupported");
+  if (layer < 0 || layer >= g.num_layers)
+    return internal(st, "layer %lld out of range (have %lld)", (long long)layer,
+                    (long long)g.num_layers);
+  HIP_TRY(st, hipSetDevice(dev->ordinal));
+  const int64_t splits = decode_max_splits(num_rows, g.num_kv_heads, max_position, g.block_size);
+  HIP_TRY(st, dev->attn_ws.reserve(decode_workspace_bytes(num_rows, num_q_heads, g.head_dim, splits)));
+  HIP_TRY(st, launch_paged_decode(dev->stream, g, d_arena, layer, d_q, num_rows, num_q_heads,
+                                  d_positions, d_row_seq, d_bt_offsets, d_bt_ids, max_position,
+                                  d_out, dev->attn_ws.as<float>(), dev->attn_ws.bytes));
+  return ORION_HIP_OK;
+}
+
+ORION_EXPORT int orion_hip_paged_attention_prefill(
+    orion_hip_device* dev, const orion_hip_kv_layout* kv, const void* d_arena, int64_t layer,
+    const float* d_q, int64_t num_q_heads, int64_t num_seqs, const int32_t* d_row_start,
+    const int32_t* d_row_count, const uint32_t* d_first_pos, const int64_t* d_bt_offsets,
+    const uint32_t* d_bt_ids, int64_t max_rows, int64_t max_position, float* d_out) {
+  const char* st = "paged_attention_prefill";
+  KvGeom g;
+  if (int rc = kv_geom_from(kv, &g, st)) return rc;
+  if (g.num_kv_heads <= 0 || num_q_heads % g.num_kv_heads)
+    return internal(st, "query heads cannot be grouped over kv heads");
+  HIP_TRY(st, hipSetDevice(dev->ordinal));
+  HIP_TRY(st, launch_paged_prefill(dev->stream, g, d_arena, layer, d_q, num_q_heads, num_seqs,
+                                   d_row_start, d_row_count, d_first_pos, d_bt_offsets, d_bt_ids,
+                                   max_rows, max_position, d_out));
+  return ORION_HIP_OK;
+}
+
+ORION_EXPORT int orion_hip_rope_and_cache(orion_hip_device* dev, const orion_hip_kv_layout* kv,
+                                          void* d_arena, int64_t layer, int64_t num_rows,
+                                          int64_t num_q_heads, const float* d_q_in,
+                                          int64_t q_stride, float* d_q_out, const float* d_k,
+                                          int64_t k_stride, const float* d_v, int64_t v_stride,
+                                          const uint32_t* d_positions, const int32_t* d_row_seq,
+                                          const int64_t* d_bt_offsets, const uint32_t* d_bt_ids,
+                                          const float* d_cos, const float* d_sin) {
+  const char* st = "rope_and_cache";
+  KvGeom g;
+  if (int rc = kv_geom_from(kv, &g, st)) return rc;
+  if (layer < 0 || layer >= g.num_layers) return internal(st, "layer out of range");
+  HIP_TRY(st, hipSetDevice(dev->ordinal));
+  HIP_TRY(st, launch_rope_and_cache(dev->stream, g, d_arena, layer, num_rows, num_q_heads, d_q_in,
+                                    q_stride, d_q_out, d_k, k_stride, d_v, v_stride, d_positions,
+                                    d_row_seq, d_bt_offsets, d_bt_ids, d_cos, d_sin));
+  return ORION_HIP_OK;
+}
+
+ORION_EXPORT int orion_hip_rmsnorm(orion_hip_device* dev, const float* d_x, const float* d_weight,
+                                   int64_t rows, int64_t cols, float eps, float* d_out) {
+  HIP_TRY("rmsnorm", hipSetDevice(dev->ordinal));
+  HIP_TRY("rmsnorm", launch_rmsnorm(dev->stream, d_x, nullptr, d_weight, rows, cols, eps, d_out));
+  return ORION_HIP_OK;
+}
+
+ORION_EXPORT int orion_hip_gemm(orion_hip_device* dev, const float* d_x, const uint16_t* d_w,
+                                const float* d_bias, int64_t M, int64_t N, int64_t K,
+                                int accumulate, float* d_out) {
+  const char* st = "gemm";
+  if (K % 32 != 0 || K <= 0)
+    return set_err(ORION_HIP_ERR_BACKEND, st, "K must be a positive multiple of 32, got %lld",
+                   (long long)K);
+  if (accumulate && d_bias) return internal(st, "bias is not supported with accumulate");
+  HIP_TRY(st, hipSetDevice(dev->ordinal));
+  HIP_TRY(st, launch_gemm(dev->stream, d_x, d_w, d_bias, M, N, K,
+                          accumulate ? Epilogue::kAccumulate : Epilogue::kStore, d_out));
+  return ORION_HIP_OK;
+}
+
+ORION_EXPORT int orion_hip_silu_mul(orion_hip_device* dev, float* d_gate, const float* d_up,
+                                    int64_t count) {
+  HIP_TRY("silu_mul", hipSetDevice(dev->ordinal));
+  HIP_TRY("silu_mul", launch_silu_mul(dev->stream, d_gate, d_up, count));
+  return ORION_HIP_OK;
+}
+
+ORION_EXPORT int orion_hip_argmax(orion_hip_device* dev, const float* d_logits, int64_t rows,
+                                  int64_t cols, int64_t* d_out) {
+  HIP_TRY("argmax", hipSetDevice(dev->ordinal));
+  HIP_TRY("argmax", launch_argmax(dev->stream, d_logits, rows, cols, d_out));
+  return ORION_HIP_OK;
+}

@@ -1,0 +1,77 @@
+"""Seeded paged-attention workloads (BASELINE configs 1 and 2 and edge cases)
+shared by the GPU parity tests, the golden-fixture generator and bench.py."""
+import numpy as np
+
+
+class PagedCase:
+    """Sequences with context lengths `ctxs`, block tables drawn from a
+    seeded permutation of a pool of `num_blocks`, and one query row per
+    sequence at position ctx - 1 (decode).  K/V pool entries are N(0, 1)
+    (also the never-referenced blocks), stored in `dtype` ('f32' | 'bf16')."""
+
+    def __init__(self, seed, ctxs, hq, hkv, d, block_size, num_blocks=None, dtype="f32",
+                 pool_factor=1.25, disjoint=True):
+        rng = np.random.default_rng(seed)
+        self.ctxs = np.asarray(ctxs, dtype=np.int64)
+        self.S = len(ctxs)
+        self.hq, self.hkv, self.d, self.bs = hq, hkv, d, block_size
+        self.dtype = dtype
+        need = [-(-int(c) // block_size) for c in self.ctxs]
+        total = sum(need)
+        self.num_blocks = int(num_blocks or int(np.ceil(pool_factor * total)) or 1)
+        perm = rng.permutation(self.num_blocks)
+        tables, cur = [], 0
+        for nb in need:
+            if disjoint:
+                tables.append(perm[cur:cur + nb].astype(np.uint32))
+                cur += nb
+            else:
+                tables.append(rng.integers(0, self.num_blocks, nb).astype(np.uint32))
+        self.tables = tables
+        self.bt_offsets = np.zeros(self.S + 1, np.int64)
+        self.bt_offsets[1:] = np.cumsum(need)
+        self.bt_ids = np.concatenate(tables) if total else np.zeros(1, np.uint32)
+        n_el = self.num_blocks * 2 * block_size * hkv * d
+        arena = rng.standard_normal(n_el, dtype=np.float32)
+        if dtype == "bf16":
+            from model_fixtures import bf16_round
+            arena = bf16_round(arena)
+        self.arena_f32 = arena  # exact values the device holds, widened to f32
+        self.q = rng.standard_normal((self.S, hq * d), dtype=np.float32)
+        self.positions = (self.ctxs - 1).astype(np.uint32)
+        self.row_seq = np.arange(self.S, dtype=np.int32)
+
+    def dims(self):
+        return (1, self.num_blocks, self.bs, self.hkv, self.d)
+
+    def arena_device_bytes(self):
+        if self.dtype == "bf16":
+            import orion_hip
+            return orion_hip.f32_to_bf16_bits(self.arena_f32)
+        return self.arena_f32
+
+    def kv_bytes_read(self):
+        esz = 2 if self.dtype == "bf16" else 4
+        return int(self.ctxs.sum()) * 2 * self.hkv * self.d * esz
+
+    def oracle(self, positions=None, row_seq=None, q=None):
+        import oracle as orc
+        return orc.paged_attention_rows(
+            self.arena_f32, self.dims(), 0, self.hq, self.q if q is None else q,
+            self.positions if positions is None else positions,
+            self.row_seq if row_seq is None else row_seq, self.bt_offsets, self.bt_ids)
+
+
+def cfg1(seed=20261201):
+    """4 seqs, ctx U[1,512], bs 16, 8q/2kv, d 64, f32, 256-block pool."""
+    rng = np.random.default_rng(seed)
+    ctxs = rng.integers(1, 513, size=4)
+    return PagedCase(seed + 1, ctxs, 8, 2, 64, 16, num_blocks=256, dtype="f32")
+
+
+def cfg2(seed=20261202, num_seqs=64):
+    """64 seqs, ctx U[128,4096], bs 16, 32q/8kv, d 128, bf16 KV,
+    pool 1.25x the blocks needed, scattered tables."""
+    rng = np.random.default_rng(seed)
+    ctxs = rng.integers(128, 4097, size=num_seqs)
+    return PagedCase(seed + 1, ctxs, 32, 8, 128, 16, dtype="bf16", pool_factor=1.25)

@@ -1,0 +1,62 @@
+"""The C-ABI library loads and exports every symbol include/orion_hip.h
+declares (no GPU needed: no compute call is made)."""
+import os
+import re
+import subprocess
+
+import numpy as np
+
+from conftest import ROOT
+
+import orion_hip
+
+HEADER = os.path.join(ROOT, "include", "orion_hip.h")
+
+
+def declared_symbols():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(orion_hip_\w+)\s*\(", text)))
+
+
+def test_header_and_binding_list_agree():
+    assert declared_symbols() == sorted(orion_hip.EXPORTED)
+
+
+def test_library_exports_every_declared_symbol():
+    lib = orion_hip.load_library()
+    for name in declared_symbols():
+        assert hasattr(lib, name), name
+    out = subprocess.run(["nm", "-D", "--defined-only", orion_hip.LIB_PATH], capture_output=True,
+                         text=True, check=True).stdout
+    exported = set(re.findall(r"\b(orion_hip_\w+)\b", out))
+    assert set(declared_symbols()) <= exported
+
+
+def test_library_is_built_for_gfx950_only():
+    out = subprocess.run(["/opt/rocm/llvm/bin/clang-offload-bundler", "--list", "--type=o",
+                          f"--input={orion_hip.LIB_PATH}"], capture_output=True, text=True)
+    if out.returncode == 0 and out.stdout.strip():
+        targets = [t for t in out.stdout.split() if "gfx" in t]
+        assert targets and all("gfx950" in t for t in targets), targets
+
+
+def test_synthetic_generator_statistics_and_determinism():
+    # Host-side generator (no GPU call): zero mean, requested sd, bf16 values,
+    # different tensors/layers give different streams.
+    v = np.array([orion_hip.synthetic_value(3, orion_hip.W_Q, 0, i, 0.02) for i in range(20000)])
+    assert abs(v.mean()) < 1e-3 and abs(v.std() - 0.02) < 1e-3
+    assert np.array_equal(orion_hip.f32_to_bf16_bits(v.astype(np.float32)).astype(np.uint32) << 16,
+                          v.astype(np.float32).view(np.uint32))
+    w = np.array([orion_hip.synthetic_value(3, orion_hip.W_Q, 1, i, 0.02) for i in range(64)])
+    assert not np.array_equal(v[:64], w)
+    assert orion_hip.synthetic_value(3, orion_hip.W_INPUT_NORM, 0, 5, 0.02) == 1.0
+
+
+def test_bf16_helpers_round_to_nearest_even():
+    x = np.array([1.0, 1.00390625, 1.01171875, -2.5, 3.4e38, np.inf], np.float32)
+    b = orion_hip.f32_to_bf16_bits(x)
+    back = orion_hip.bf16_bits_to_f32(b)
+    # 1 + 2^-8 is a tie -> even (1.0); 1 + 3*2^-8 is a tie -> 1 + 2^-6
+    assert back[0] == 1.0 and back[1] == 1.0 and back[2] == np.float32(1.015625)
+    assert back[3] == -2.5 and np.isinf(back[5])

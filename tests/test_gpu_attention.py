@@ -1,0 +1,112 @@
+"""Paged decode attention on the MI355X against the CPU oracle
+(crates/orion-models/src/attention.rs:219-295 restated in oracle/)."""
+import numpy as np
+import pytest
+
+import oracle as orc
+import orion_hip as oh
+from paged_cases import PagedCase, cfg1, cfg2
+
+pytestmark = pytest.mark.gpu
+
+
+def run_decode(be, case, positions=None, row_seq=None, q=None):
+    positions = case.positions if positions is None else np.asarray(positions, np.uint32)
+    row_seq = case.row_seq if row_seq is None else np.asarray(row_seq, np.int32)
+    q = case.q if q is None else q
+    rows = len(positions)
+    kv = oh.kv_layout(1, case.num_blocks, case.bs, case.hkv, case.d,
+                      oh.BF16 if case.dtype == "bf16" else oh.F32)
+    bufs = [be.to_device(case.arena_device_bytes()), be.to_device(q), be.to_device(positions),
+            be.to_device(row_seq), be.to_device(case.bt_offsets), be.to_device(case.bt_ids),
+            be.alloc(rows * case.hq * case.d * 4)]
+    arena, dq, dpos, drs, dbo, dbi, dout = bufs
+    print(f"[decode] rows={rows} hq={case.hq} hkv={case.hkv} d={case.d} bs={case.bs} "
+          f"dtype={case.dtype} maxpos={int(positions.max())}", flush=True)
+    oh.paged_attention_decode(be, kv, arena.ptr, 0, dq.ptr, rows, case.hq, dpos.ptr, drs.ptr,
+                              dbo.ptr, dbi.ptr, int(positions.max()), dout.ptr)
+    out = dout.download(np.float32, (rows, case.hq * case.d))
+    for b in bufs:
+        b.free()
+    return out
+
+
+def test_cfg1_matches_oracle_f32_tolerance(backend):
+    case = cfg1()
+    got = run_decode(backend, case)
+    want = case.oracle()
+    mm, ma, mr, wi = orc.validate(want, got, orc.Tolerance.F32)
+    assert mm == 0, (ma, mr, wi)
+
+
+def test_cfg2_full_size_bf16_kv(backend):
+    case = cfg2()
+    got = run_decode(backend, case)
+    want = case.oracle()
+    err = np.abs(got - want).max()
+    assert err <= 1e-2, err          # north-star tolerance on attention outputs
+    assert err <= 1e-4, err          # what f32 accumulation over exact bf16 values gives
+
+
+@pytest.mark.parametrize("hq,hkv,d,bs,dtype", [
+    (8, 8, 64, 16, "f32"), (16, 8, 128, 16, "bf16"), (12, 4, 128, 8, "bf16"),
+    (28, 4, 128, 16, "bf16"), (32, 4, 64, 16, "bf16"), (20, 4, 64, 32, "f32"),
+    (10, 2, 128, 4, "f32"), (6, 1, 64, 256, "bf16"), (64, 8, 128, 64, "bf16"),
+])
+def test_shapes_groups_and_block_sizes(backend, hq, hkv, d, bs, dtype):
+    ctxs = [1, 2, 15, 16, 17, 63, 64, 65, 255, 256, 257, 511, 512, 513, 1000, 2049]
+    case = PagedCase(hq * 1000 + d + bs, ctxs, hq, hkv, d, bs, dtype=dtype)
+    got = run_decode(backend, case)
+    want = case.oracle()
+    tol = orc.Tolerance.F32 if dtype == "f32" else orc.Tolerance(1e-4, 1e-4)
+    mm, ma, mr, wi = orc.validate(want, got, tol)
+    assert mm == 0, (ma, mr, wi)
+
+
+def test_ragged_positions_and_shared_sequences(backend):
+    # Several query rows per sequence at arbitrary positions (what a chunked
+    # prefill batch looks like to the decode kernel) and sequences sharing
+    # leading blocks (prefix sharing, non-disjoint tables).
+    case = PagedCase(11, [300, 1200, 40], 16, 4, 128, 16, dtype="bf16", disjoint=False,
+                     num_blocks=40)
+    rng = np.random.default_rng(5)
+    row_seq = np.array([0, 0, 0, 1, 1, 2, 1, 0], np.int32)
+    positions = np.array([0, 299, 150, 1199, 17, 39, 640, 31], np.uint32)
+    q = rng.standard_normal((len(row_seq), case.hq * case.d), dtype=np.float32)
+    got = run_decode(backend, case, positions, row_seq, q)
+    want = case.oracle(positions, row_seq, q)
+    assert np.abs(got - want).max() <= 1e-4
+
+
+def test_single_position_returns_value_exactly(backend):
+    # attention.rs:375-403 at a supported head_dim: one position -> softmax 1.0 -> V.
+    case = PagedCase(3, [1, 1, 1], 8, 2, 64, 16, dtype="f32")
+    got = run_decode(backend, case)
+    for s in range(3):
+        b = int(case.tables[s][0])
+        for h in range(8):
+            off = (b * 2 + 1) * 16 * 2 * 64 + (h // 4) * 64
+            v = case.arena_f32[off:off + 64]
+            assert np.array_equal(got[s, h * 64:(h + 1) * 64], v)
+
+
+def test_uniform_keys_give_the_mean_of_values(backend):
+    # attention.rs:479-510: identical keys -> uniform weights -> mean of V.
+    case = PagedCase(9, [777], 4, 1, 128, 16, dtype="f32")
+    a = case.arena_f32.reshape(case.num_blocks, 2, 16, 1, 128)
+    a[:, 0] = 0.25
+    got = run_decode(backend, case)
+    vals = np.stack([a[case.tables[0][p // 16], 1, p % 16, 0] for p in range(777)])
+    np.testing.assert_allclose(got.reshape(4, 128), np.broadcast_to(vals.mean(0), (4, 128)),
+                               rtol=1e-5, atol=1e-6)
+
+
+def test_golden_cfg1_fixture(backend):
+    # Committed golden output of the oracle on config 1 (tests/golden/).
+    import os
+    g = np.load(os.path.join(os.path.dirname(__file__), "golden", "cfg1_decode.npz"))
+    case = cfg1()
+    assert np.array_equal(case.ctxs, g["ctxs"])
+    got = run_decode(backend, case)
+    mm, ma, mr, wi = orc.validate(g["out"], got, orc.Tolerance.F32)
+    assert mm == 0, (ma, mr, wi)

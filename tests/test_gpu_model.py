@@ -1,0 +1,221 @@
+"""LanguageModel::forward on the MI355X against the CPU oracle, plus the
+reference's model invariants (crates/orion-models/src/transformer.rs:590-746)
+checked GPU against GPU."""
+import numpy as np
+import pytest
+
+import oracle as orc
+import orion_hip as oh
+from model_fixtures import Spec, oracle_model, random_weights
+
+pytestmark = pytest.mark.gpu
+
+KEYS = [("input_norm", oh.W_INPUT_NORM), ("q", oh.W_Q), ("k", oh.W_K), ("v", oh.W_V),
+        ("o", oh.W_O), ("post_norm", oh.W_POST_NORM), ("gate", oh.W_GATE), ("up", oh.W_UP),
+        ("down", oh.W_DOWN), ("q_bias", oh.W_Q_BIAS), ("k_bias", oh.W_K_BIAS),
+        ("v_bias", oh.W_V_BIAS)]
+
+
+def meta_of(spec):
+    return oh.ModelMetadata(hidden_size=spec.H, num_layers=spec.L, num_attention_heads=spec.hq,
+                            num_kv_heads=spec.hkv, head_dim=spec.d, vocab_size=spec.V,
+                            intermediate_size=spec.F, max_position_embeddings=spec.max_pos,
+                            rope_theta=spec.theta, rms_norm_eps=spec.eps,
+                            architecture="qwen2" if spec.bias else "llama",
+                            tied_lm_head=spec.tied)
+
+
+def gpu_model(be, spec, W, kv_dtype=oh.F32):
+    m = oh.HipTransformerModel(meta_of(spec), spec.num_blocks, spec.block_size, be, kv_dtype)
+    m.upload_weight(oh.W_EMBED, -1, W["embed"])
+    m.upload_weight(oh.W_FINAL_NORM, -1, W["final_norm"])
+    if W["lm_head"] is not None:
+        m.upload_weight(oh.W_LM_HEAD, -1, W["lm_head"])
+    for l, w in enumerate(W["layers"]):
+        for key, wid in KEYS:
+            if w[key] is not None:
+                m.upload_weight(wid, l, w[key])
+    return m
+
+
+def small_spec(bias=False, tied=True, L=2):
+    return Spec(L, 256, 4, 2, 64, 512, 1000, max_pos=1024, bias=bias, tied=tied,
+                num_blocks=96, block_size=16)
+
+
+def batch(tokens, positions, counts, tables, ctx=None):
+    return oh.ForwardBatch(list(tokens), list(positions), list(range(1, len(counts) + 1)),
+                           list(counts), list(ctx or counts), [list(t) for t in tables], True)
+
+
+def rel_err(a, b):
+    return float(np.abs(a - b).max() / max(np.abs(b).max(), 1e-30))
+
+
+@pytest.mark.parametrize("bias,tied,kv", [(False, True, oh.F32), (True, False, oh.F32),
+                                          (False, False, oh.BF16)])
+def test_forward_matches_oracle(backend, bias, tied, kv):
+    rng = np.random.default_rng(31)
+    spec = small_spec(bias, tied)
+    W = random_weights(spec, rng, std=0.05)
+    gm = gpu_model(backend, spec, W, kv)
+    om = oracle_model(spec, W)
+    perm = rng.permutation(spec.num_blocks)
+    # step 1: a mixed prefill batch of three prompts
+    lens = [37, 1, 70]
+    tables = [perm[0:8], perm[8:16], perm[16:24]]
+    toks = rng.integers(0, spec.V, sum(lens))
+    pos = np.concatenate([np.arange(n) for n in lens])
+    b = batch(toks, pos, lens, tables)
+    print(f"[model] bias={bias} tied={tied} kv={kv} prefill", flush=True)
+    g = gm.forward(b, want_argmax=True)
+    o = om.forward(toks, pos, lens, lens, tables)
+    tol = 1e-4 if kv == oh.F32 else 2e-2
+    assert rel_err(g.logits, o) <= tol, rel_err(g.logits, o)
+    assert g.argmax.tolist() == [orc.argmax(r) for r in g.logits]
+    # step 2: one decode token per sequence on top of the cache
+    toks2 = rng.integers(0, spec.V, 3)
+    b2 = batch(toks2, lens, [1, 1, 1], tables, [n + 1 for n in lens])
+    g2 = gm.forward(b2)
+    o2 = om.forward(toks2, lens, [1, 1, 1], [n + 1 for n in lens], tables)
+    assert rel_err(g2.logits, o2) <= tol, rel_err(g2.logits, o2)
+    gm.close()
+
+
+def test_kv_cache_contents_match_oracle(backend):
+    rng = np.random.default_rng(32)
+    spec = small_spec()
+    W = random_weights(spec, rng, std=0.05)
+    gm, om = gpu_model(backend, spec, W), oracle_model(spec, W)
+    tables = [rng.permutation(spec.num_blocks)[:4]]
+    toks = rng.integers(0, spec.V, 50)
+    gm.forward(batch(toks, range(50), [50], tables))
+    om.forward(toks, np.arange(50), [50], [50], tables)
+    okv = om.kv()
+    store_dims = (spec.L, spec.num_blocks, spec.block_size, spec.hkv, spec.d)
+    for layer in range(spec.L):
+        for p in (0, 15, 16, 49):
+            blk, slot = orc.locate(tables[0], p, spec.block_size)
+            for h in range(spec.hkv):
+                for isv in (False, True):
+                    off = orc.lib().oracle_kv_offset(*store_dims, layer, blk, int(isv), slot, h)
+                    want = okv[off:off + spec.d]
+                    got = gm.kv_read(layer, blk, slot, h, isv)
+                    assert np.abs(got - want).max() <= 1e-4 * np.abs(want).max()
+    # an untouched slot is still zero, and bounds errors are Internal
+    unused = [b for b in range(spec.num_blocks) if b not in tables[0]][0]
+    assert np.all(gm.kv_read(0, unused, 0, 0, False) == 0)
+    with pytest.raises(oh.InternalError):
+        gm.kv_read(0, spec.num_blocks, 0, 0, False)
+    with pytest.raises(oh.InternalError):
+        gm.kv_read(0, 0, spec.block_size, 0, False)
+    gm.close()
+
+
+def test_model_invariants_gpu(backend):
+    rng = np.random.default_rng(33)
+    spec = small_spec(L=2)
+    W = random_weights(spec, rng, std=0.05)
+
+    def fresh():
+        return gpu_model(backend, spec, W)
+
+    t = rng.integers(0, spec.V, 40).tolist()
+    # batching independence (transformer.rs:590-638)
+    m = fresh()
+    alone = m.forward(batch(t[:20], range(20), [20], [[0, 1]])).logits[0]
+    together = m.forward(batch(t[:20] + t[20:40], list(range(20)) * 2, [20, 20],
+                               [[0, 1], [5, 6]])).logits[0]
+    assert rel_err(together, alone) <= 1e-5
+    m.close()
+    # incremental decode == full prefill (:640-677)
+    m = fresh()
+    full = m.forward(batch(t[:33], range(33), [33], [[0, 1, 2]])).logits[0]
+    m.close()
+    m = fresh()
+    m.forward(batch(t[:32], range(32), [32], [[0, 1, 2]]))
+    inc = m.forward(batch([t[32]], [32], [1], [[0, 1, 2]], [33])).logits[0]
+    assert rel_err(inc, full) <= 1e-4
+    m.close()
+    # chunked prefill == one pass (:679-713)
+    m = fresh()
+    m.forward(batch(t[:17], range(17), [17], [[0, 1, 2]]))
+    chunk = m.forward(batch(t[17:33], range(17, 33), [16], [[0, 1, 2]], [33])).logits[0]
+    assert rel_err(chunk, full) <= 1e-4
+    m.close()
+    # scattered table == contiguous (:715-746)
+    m = fresh()
+    scat = m.forward(batch(t[:33], range(33), [33], [[77, 3, 41]])).logits[0]
+    assert rel_err(scat, full) <= 1e-6
+    m.close()
+
+
+def test_forward_errors_are_internal(backend):
+    spec = small_spec(L=1)
+    m = gpu_model(backend, spec, random_weights(spec, np.random.default_rng(0)))
+    with pytest.raises(oh.InternalError):  # OOV token (transformer.rs:769-776)
+        m.forward(batch([spec.V + 5], [0], [1], [[0]]))
+    with pytest.raises(oh.InternalError):  # beyond RoPE table (:778-793)
+        m.forward(batch([1], [spec.max_pos + 1], [1], [list(range(80))]))
+    with pytest.raises(oh.InternalError):  # position outside the block table
+        m.forward(batch([1], [40], [1], [[0]]))
+    with pytest.raises(oh.InternalError):  # block id beyond the arena
+        m.forward(batch([1], [0], [1], [[spec.num_blocks]]))
+    with pytest.raises(oh.InternalError):  # inconsistent batch (:795-801)
+        bad = batch([1, 2], [0, 1], [2], [[0]])
+        bad.slot_token_counts = [5]
+        m.forward(bad)
+    out = m.forward(oh.ForwardBatch([], [], [], [], [], []))  # empty batch (:551-566)
+    assert out.logits.shape == (0, spec.V)
+    m.close()
+
+
+def test_weight_upload_roundtrip_and_synthetic_init(backend):
+    rng = np.random.default_rng(4)
+    spec = small_spec(bias=True, tied=False, L=1)
+    W = random_weights(spec, rng)
+    m = gpu_model(backend, spec, W)
+    for key, wid in KEYS:
+        got = m.download_weight(wid, 0, W["layers"][0][key].size)
+        assert np.array_equal(got, W["layers"][0][key].ravel()), key
+    m.init_synthetic(seed=99, std=0.02)
+    for wid, layer, n in [(oh.W_EMBED, -1, spec.V * spec.H), (oh.W_GATE, 0, spec.F * spec.H),
+                          (oh.W_UP, 0, spec.F * spec.H), (oh.W_K, 0, spec.hkv * spec.d * spec.H),
+                          (oh.W_V_BIAS, 0, spec.hkv * spec.d)]:
+        got = m.download_weight(wid, layer, n)
+        idx = rng.integers(0, n, 200)
+        want = [oh.synthetic_value(99, wid, layer, int(i), 0.02) for i in idx]
+        assert np.array_equal(got[idx], np.array(want, np.float32)), wid
+    assert np.all(m.download_weight(oh.W_INPUT_NORM, 0, spec.H) == 1.0)
+    m.close()
+
+
+def test_greedy_decode_matches_oracle(backend):
+    # Teacher-forced greedy decoding: both sides consume the oracle's token
+    # stream; per-step argmax must agree except where the oracle's top-2
+    # margin is below the measured logit error.
+    rng = np.random.default_rng(35)
+    spec = small_spec(L=2)
+    W = random_weights(spec, rng, std=0.08)
+    gm, om = gpu_model(backend, spec, W), oracle_model(spec, W)
+    S = 4
+    lens = [5, 17, 33, 60]
+    tables = [list(range(8 * s, 8 * s + 8)) for s in range(S)]
+    toks = rng.integers(0, spec.V, sum(lens))
+    pos = np.concatenate([np.arange(n) for n in lens])
+    g = gm.forward(batch(toks, pos, lens, tables)).logits
+    o = om.forward(toks, pos, lens, lens, tables)
+    mismatches = 0
+    for step in range(12):
+        err = np.abs(g - o).max()
+        og = [orc.argmax(r) for r in o]
+        gg = [int(np.argmax(r)) for r in g]
+        for s in range(S):
+            top2 = np.sort(o[s])[-2:]
+            if og[s] != gg[s]:
+                assert top2[1] - top2[0] <= 2 * err, (step, s)
+                mismatches += 1
+        cur = [lens[s] + step for s in range(S)]
+        g = gm.forward(batch(og, cur, [1] * S, tables, [c + 1 for c in cur])).logits
+        o = om.forward(og, cur, [1] * S, [c + 1 for c in cur], tables)
+    assert mismatches <= 1
