@@ -220,12 +220,28 @@ typedef struct orion_hip_kv_layout {
   int32_t dtype; /* ORION_DTYPE_F32 or ORION_DTYPE_BF16 */
 } orion_hip_kv_layout;
 
+/* Work plan for paged decode attention over one batch of query rows.  Built
+ * on the host from the rows' positions (host copy): each row's context is cut
+ * into chunks and the (row, chunk) items are ordered longest first, which keeps
+ * the chip evenly loaded on ragged batches.  A plan depends only on the
+ * positions, so one plan serves every layer of a forward pass.  The plan also
+ * owns the split-K workspace. */
+typedef struct orion_hip_decode_plan orion_hip_decode_plan;
+int orion_hip_decode_plan_create(orion_hip_device* dev, const uint32_t* positions,
+                                 int64_t num_rows, int64_t num_q_heads, int64_t num_kv_heads,
+                                 int64_t head_dim, int64_t block_size,
+                                 orion_hip_decode_plan** out);
+void orion_hip_decode_plan_destroy(orion_hip_decode_plan* plan);
+/* Chunk length in tokens, number of work items, chunks of the longest row. */
+int orion_hip_decode_plan_info(const orion_hip_decode_plan* plan, int64_t* chunk,
+                               int64_t* num_work, int64_t* max_splits);
+
 /* paged_attention (attention.rs:219-295) for `num_rows` independent query
  * rows: row r attends positions 0..=d_positions[r] of the sequence
  * d_row_seq[r] through that sequence's block table (CSR d_bt_offsets /
  * d_bt_ids).  d_q and d_out are [num_rows, num_q_heads, head_dim] f32.
- * max_position bounds every d_positions entry (it sizes the split-K grid).
- * Block ids and table lengths are not re-checked on the device: the caller
+ * `plan` must come from the same positions (host copy) and geometry.  Block
+ * ids and table lengths are not re-checked on the device: the caller
  * guarantees every (position / block_size) < table length and every id
  * < num_blocks (orion_hip_model_forward checks this on the host). */
 int orion_hip_paged_attention_decode(orion_hip_device* dev, const orion_hip_kv_layout* kv,
@@ -233,7 +249,7 @@ int orion_hip_paged_attention_decode(orion_hip_device* dev, const orion_hip_kv_l
                                      int64_t num_rows, int64_t num_q_heads,
                                      const uint32_t* d_positions, const int32_t* d_row_seq,
                                      const int64_t* d_bt_offsets, const uint32_t* d_bt_ids,
-                                     int64_t max_position, float* d_out);
+                                     const orion_hip_decode_plan* plan, float* d_out);
 
 /* Causal attention for prefill chunks on MFMA: sequence s contributes query
  * rows d_q[d_row_start[s] .. d_row_start[s] + d_row_count[s]) whose positions

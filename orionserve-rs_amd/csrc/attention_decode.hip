@@ -26,6 +26,12 @@
 #include "common.hpp"
 #include "kernels.hpp"
 
+#include <algorithm>
+#include <cstdlib>
+#include <functional>
+#include <queue>
+#include <vector>
+
 namespace orion {
 
 template <typename T>
@@ -60,14 +66,12 @@ struct KvVec<uint16_t> {
 };
 
 template <typename T, int D, int G>
-__global__ void __launch_bounds__(256)
-    paged_decode_kernel(const T* __restrict__ kv_layer, int64_t blk_stride, int64_t v_off,
-                        int64_t slot_stride, int bs_log2, int num_kv_heads, int num_q_heads,
-                        int num_items, const float* __restrict__ q,
-                        const uint32_t* __restrict__ positions, const int32_t* __restrict__ row_seq,
-                        const int64_t* __restrict__ bt_off, const uint32_t* __restrict__ bt_ids,
-                        int partition, int max_splits, float scale, float* __restrict__ out,
-                        float* __restrict__ ws_o, float* __restrict__ ws_ml) {
+__device__ __forceinline__ void decode_wave_valu(
+    const T* __restrict__ kv_layer, int64_t blk_stride, int64_t v_off, int64_t slot_stride,
+    int bs_log2, int num_q_heads, const float* __restrict__ q, const int32_t* __restrict__ row_seq,
+    const int64_t* __restrict__ bt_off, const uint32_t* __restrict__ bt_ids, int max_splits,
+    float scale, float* __restrict__ out, float* __restrict__ ws_o, float* __restrict__ ws_ml,
+    int row, int kvh, int start, int end, int split, int nsplit) {
   constexpr int EPL = KvVec<T>::EPL;
   constexpr int CH = D / EPL;   // lanes per token vector
   constexpr int TPW = 64 / CH;  // tokens per wave load
@@ -75,16 +79,6 @@ __global__ void __launch_bounds__(256)
   static_assert(TPW >= 1 && TPW <= 16 && R * TPW == 16, "unsupported head_dim/dtype");
 
   const int lane = threadIdx.x & 63;
-  const int item = blockIdx.x * 4 + (threadIdx.x >> 6);
-  if (item >= num_items) return;
-  const int row = item / num_kv_heads;
-  const int kvh = item - row * num_kv_heads;
-  const int split = blockIdx.y;
-  const int len = (int)positions[row] + 1;
-  const int start = split * partition;
-  if (start >= len) return;
-  const int end = min(len, start + partition);
-  const int nsplit = (len + partition - 1) / partition;
 
   const int t = lane / CH;  // token slot within a wave load
   const int c = lane % CH;  // chunk of the head vector
@@ -228,6 +222,313 @@ __global__ void __launch_bounds__(256)
   }
 }
 
+// One wave per work item (row, KV head, context chunk), four items per
+// workgroup; the work list is ordered longest chunk first.
+template <typename T, int D, int G>
+__global__ void __launch_bounds__(256)
+    paged_decode_kernel(const T* __restrict__ kv_layer, int64_t blk_stride, int64_t v_off,
+                        int64_t slot_stride, int bs_log2, int num_kv_heads, int num_q_heads,
+                        const int2* __restrict__ work, int num_work, const float* __restrict__ q,
+                        const uint32_t* __restrict__ positions, const int32_t* __restrict__ row_seq,
+                        const int64_t* __restrict__ bt_off, const uint32_t* __restrict__ bt_ids,
+                        int chunk, int max_splits, float scale, float* __restrict__ out,
+                        float* __restrict__ ws_o, float* __restrict__ ws_ml) {
+  const int w = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (w >= num_work) return;
+  const int2 wk = work[w];
+  const int row = wk.x / num_kv_heads, kvh = wk.x - row * num_kv_heads, start = wk.y;
+  const int len = (int)positions[row] + 1;
+  const int end = min(len, start + chunk);
+  const int nsplit = (len + chunk - 1) / chunk;
+  decode_wave_valu<T, D, G>(kv_layer, blk_stride, v_off, slot_stride, bs_log2, num_q_heads, q,
+                            row_seq, bt_off, bt_ids, max_splits, scale, out, ws_o, ws_ml, row, kvh,
+                            start, end, start / chunk, nsplit);
+}
+
+// bf16-KV decode kernel with Q.K^T on MFMA.
+//
+// Each iteration covers NT tiles of 16 tokens.  Per tile a wave computes
+// S^T[head, token] = Q[G, D] . K^T[D, 16] with v_mfma_f32_16x16x32_bf16: the A
+// operand is the query group (rows = heads, zero rows past G) split into hi +
+// lo bf16 terms, so the product keeps ~16 bits of each f32 query element; the
+// B operand is the K tile itself, lane l holding token l%16, dims
+// (l/16)*8 + 32j .. +8, i.e. one 16-byte load straight from the cache.  The NT
+// tiles use independent accumulators.  Scores land as lane l: token l%16,
+// heads 4*(l/16)+i; the running max is wave-uniform per head (reduced over the
+// 16 token lanes once per iteration), and the softmax weights reach the P.V
+// lanes through a (16*NT) x G LDS tile.  P.V runs on VALU with lane (t, c) =
+// (token group, 8-dim chunk), the layout in which a V load is one coalesced
+// 16-byte access.
+//
+// Software pipeline: the next iteration's K loads are issued as soon as this
+// iteration's MFMAs have consumed K, and the next V loads as soon as P.V has
+// consumed V, so K(i+1) streams in under the softmax and P.V of step i and
+// V(i+1) under the next Q.K^T.
+template <int D, int G, int NT, bool BIG_BLOCKS>
+__device__ __forceinline__ void decode_wave_mfma(
+    const uint16_t* __restrict__ kv_layer, uint32_t blk_stride, uint32_t v_off,
+    uint32_t slot_stride, int bs_log2, int num_q_heads, const float* __restrict__ q,
+    const int32_t* __restrict__ row_seq, const int64_t* __restrict__ bt_off,
+    const uint32_t* __restrict__ bt_ids, int max_splits, float scale, float* __restrict__ out,
+    float* __restrict__ ws_o, float* __restrict__ ws_ml, float* P, float* A, float* Lr, int row, int kvh, int start, int end, int split, int nsplit) {
+  constexpr int KCH = D / 32;       // MFMA k-steps over the head dim
+  constexpr int CH = D / 8;         // P.V lanes per token (8 bf16 each)
+  constexpr int TPW = 64 / CH;      // tokens per V wave load
+  constexpr int T = 16 * NT;        // tokens per iteration
+  constexpr int RV = T / TPW;       // V loads per lane per iteration
+  constexpr int GP = (G + 3) & ~3;  // heads padded to the MFMA row quad
+  static_assert(G <= 16 && TPW <= 16 && (16 % TPW) == 0, "unsupported shape");
+
+  const int lane = threadIdx.x & 63;
+  const int bs_mask = (1 << bs_log2) - 1;
+
+  // ---- block-table slice of this split, one entry per lane ----
+  const int seq = row_seq[row];
+  const uint32_t* tbl = bt_ids + bt_off[seq];
+  const int first_blk = start >> bs_log2;
+  const int nblk = ((end - 1) >> bs_log2) - first_blk + 1;
+  const int my_blk = lane < nblk ? (int)tbl[first_blk + lane] : 0;
+
+  const uint16_t* base_k = kv_layer + (uint32_t)kvh * D;
+  const int kt = lane & 15;        // K token within a tile (MFMA column)
+  const int kd = (lane >> 4) * 8;  // K dims chunk
+  const int vt = lane / CH;        // V token group
+  const int vc = lane % CH;        // V dims chunk
+
+  uint4 kr[NT][KCH], vr[RV];
+  // Tokens past `end` are clamped to the last valid one; their weight is 0.
+  auto issue_k = [&](int b) {
+#pragma unroll
+    for (int t = 0; t < NT; ++t) {
+      const int j = min(b + 16 * t + kt, end - 1);
+      int blk;
+      if constexpr (BIG_BLOCKS)  // a 16-token tile lies inside one block
+        blk = __builtin_amdgcn_readlane(my_blk, (min(b + 16 * t, end - 1) >> bs_log2) - first_blk);
+      else
+        blk = __shfl(my_blk, (j >> bs_log2) - first_blk);
+      const uint16_t* kp =
+          base_k + (uint32_t)blk * blk_stride + (uint32_t)(j & bs_mask) * slot_stride + kd;
+#pragma unroll
+      for (int c = 0; c < KCH; ++c) kr[t][c] = *reinterpret_cast<const uint4*>(kp + 32 * c);
+    }
+  };
+  auto issue_v = [&](int b) {
+#pragma unroll
+    for (int r = 0; r < RV; ++r) {
+      const int j = min(b + r * TPW + vt, end - 1);
+      int blk;
+      if constexpr (BIG_BLOCKS)
+        blk = __builtin_amdgcn_readlane(
+            my_blk, (min(b + (r * TPW / 16) * 16, end - 1) >> bs_log2) - first_blk);
+      else
+        blk = __shfl(my_blk, (j >> bs_log2) - first_blk);
+      vr[r] = *reinterpret_cast<const uint4*>(base_k + (uint32_t)blk * blk_stride +
+                                              (uint32_t)(j & bs_mask) * slot_stride + v_off +
+                                              vc * 8);
+    }
+  };
+  issue_k(start);
+  issue_v(start);
+
+  // ---- query group as the MFMA A operand (hi/lo bf16) ----
+  bf16x8 qa_hi[KCH], qa_lo[KCH];
+  {
+    const int h = lane & 15;
+    const float* qp = q + ((int64_t)row * num_q_heads + (int64_t)kvh * G + h) * D + kd;
+#pragma unroll
+    for (int j = 0; j < KCH; ++j) {
+      float a[8];
+      if (h < G) {
+        const float4 x0 = *reinterpret_cast<const float4*>(qp + 32 * j);
+        const float4 x1 = *reinterpret_cast<const float4*>(qp + 32 * j + 4);
+        a[0] = x0.x; a[1] = x0.y; a[2] = x0.z; a[3] = x0.w;
+        a[4] = x1.x; a[5] = x1.y; a[6] = x1.z; a[7] = x1.w;
+      } else {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) a[e] = 0.f;
+      }
+      uint16_t hb[8], lb[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) split_bf16(a[e], hb[e], lb[e]);
+      uint4 hv, lv;
+      hv.x = hb[0] | ((uint32_t)hb[1] << 16); hv.y = hb[2] | ((uint32_t)hb[3] << 16);
+      hv.z = hb[4] | ((uint32_t)hb[5] << 16); hv.w = hb[6] | ((uint32_t)hb[7] << 16);
+      lv.x = lb[0] | ((uint32_t)lb[1] << 16); lv.y = lb[2] | ((uint32_t)lb[3] << 16);
+      lv.z = lb[4] | ((uint32_t)lb[5] << 16); lv.w = lb[6] | ((uint32_t)lb[7] << 16);
+      qa_hi[j] = __builtin_bit_cast(bf16x8, hv);
+      qa_lo[j] = __builtin_bit_cast(bf16x8, lv);
+    }
+  }
+
+  float m[4], lsum[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    m[i] = -INFINITY;
+    lsum[i] = 0.f;
+  }
+  float o[G][8];
+#pragma unroll
+  for (int g = 0; g < G; ++g)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) o[g][e] = 0.f;
+
+  const int hrow = (lane >> 4) * 4;  // first head of this lane's score quad
+
+  for (int b = start; b < end; b += T) {
+    const bool more = b + T < end;
+    // ---- S^T = Q . K^T, NT independent tiles ----
+    f32x4 acc[NT];
+#pragma unroll
+    for (int t = 0; t < NT; ++t) acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int c = 0; c < KCH; ++c)
+#pragma unroll
+      for (int t = 0; t < NT; ++t) {
+        const bf16x8 kb = __builtin_bit_cast(bf16x8, kr[t][c]);
+        acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(qa_hi[c], kb, acc[t], 0, 0, 0);
+        acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(qa_lo[c], kb, acc[t], 0, 0, 0);
+      }
+    if (more) issue_k(b + T);
+
+    // ---- online softmax, max wave-uniform per head ----
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      float s[NT];
+      float mx = -INFINITY;
+#pragma unroll
+      for (int t = 0; t < NT; ++t) {
+        s[t] = (b + 16 * t + kt < end) ? acc[t][i] * scale : -INFINITY;
+        mx = fmaxf(mx, s[t]);
+      }
+      mx = group_max<16>(mx);
+      const float m_new = fmaxf(m[i], mx);
+      const float alpha = __expf(m[i] - m_new);
+      float ps = 0.f;
+#pragma unroll
+      for (int t = 0; t < NT; ++t) {
+        s[t] = __expf(s[t] - m_new);
+        ps += s[t];
+        acc[t][i] = s[t];
+      }
+      lsum[i] = lsum[i] * alpha + ps;
+      m[i] = m_new;
+      if (kt == 0 && hrow < GP) A[hrow + i] = alpha;
+    }
+    if (hrow < GP) {
+#pragma unroll
+      for (int t = 0; t < NT; ++t)
+        *reinterpret_cast<float4*>(P + (16 * t + kt) * GP + hrow) =
+            make_float4(acc[t][0], acc[t][1], acc[t][2], acc[t][3]);
+    }
+    wave_lds_sync();
+
+    // ---- P.V on VALU ----
+    float al[GP];
+#pragma unroll
+    for (int g4 = 0; g4 < GP; g4 += 4) {
+      const float4 a4 = *reinterpret_cast<const float4*>(A + g4);
+      al[g4] = a4.x; al[g4 + 1] = a4.y; al[g4 + 2] = a4.z; al[g4 + 3] = a4.w;
+    }
+    bool rescale = false;
+#pragma unroll
+    for (int g = 0; g < G; ++g) rescale |= al[g] != 1.0f;
+    if (rescale) {
+#pragma unroll
+      for (int g = 0; g < G; ++g)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) o[g][e] *= al[g];
+    }
+#pragma unroll
+    for (int r = 0; r < RV; ++r) {
+      float pw[GP];
+      const float* pr = P + (r * TPW + vt) * GP;
+#pragma unroll
+      for (int g4 = 0; g4 < GP; g4 += 4) {
+        const float4 p4 = *reinterpret_cast<const float4*>(pr + g4);
+        pw[g4] = p4.x; pw[g4 + 1] = p4.y; pw[g4 + 2] = p4.z; pw[g4 + 3] = p4.w;
+      }
+      const uint4 v = vr[r];
+      const float vf[8] = {bf16lo(v.x), bf16hi(v.x), bf16lo(v.y), bf16hi(v.y),
+                           bf16lo(v.z), bf16hi(v.z), bf16lo(v.w), bf16hi(v.w)};
+#pragma unroll
+      for (int g = 0; g < G; ++g)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) o[g][e] += pw[g] * vf[e];
+    }
+    if (more) issue_v(b + T);
+    wave_lds_sync();
+  }
+
+  // Row sums over the 16 token lanes; publish (m, l) per head through LDS.
+#pragma unroll
+  for (int i = 0; i < 4; ++i) lsum[i] = group_sum<16>(lsum[i]);
+  if (hrow < GP && kt == 0) {
+    *reinterpret_cast<float4*>(Lr + hrow) = make_float4(lsum[0], lsum[1], lsum[2], lsum[3]);
+    *reinterpret_cast<float4*>(A + hrow) = make_float4(m[0], m[1], m[2], m[3]);
+  }
+  // Sum the token groups of P.V (lanes vc, vc + CH, ...).
+#pragma unroll
+  for (int g = 0; g < G; ++g)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      float v = o[g][e];
+#pragma unroll
+      for (int off = CH; off < 64; off <<= 1) v += __shfl_xor(v, off);
+      o[g][e] = v;
+    }
+  wave_lds_sync();
+  if (vt != 0) return;
+  const int64_t head0 = (int64_t)row * num_q_heads + (int64_t)kvh * G;
+  if (nsplit == 1) {
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      const float inv = 1.f / Lr[g];
+      float* op = out + (head0 + g) * D + vc * 8;
+      *reinterpret_cast<float4*>(op) =
+          make_float4(o[g][0] * inv, o[g][1] * inv, o[g][2] * inv, o[g][3] * inv);
+      *reinterpret_cast<float4*>(op + 4) =
+          make_float4(o[g][4] * inv, o[g][5] * inv, o[g][6] * inv, o[g][7] * inv);
+    }
+  } else {
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      const int64_t slot = (head0 + g) * max_splits + split;
+      float* op = ws_o + slot * D + vc * 8;
+      *reinterpret_cast<float4*>(op) = make_float4(o[g][0], o[g][1], o[g][2], o[g][3]);
+      *reinterpret_cast<float4*>(op + 4) = make_float4(o[g][4], o[g][5], o[g][6], o[g][7]);
+      if (vc == 0) *reinterpret_cast<float2*>(ws_ml + slot * 2) = make_float2(A[g], Lr[g]);
+    }
+  }
+}
+
+template <int D, int G, int NT, bool BIG_BLOCKS>
+__global__ void __launch_bounds__(256)
+    paged_decode_mfma_kernel(const uint16_t* __restrict__ kv_layer, uint32_t blk_stride,
+                             uint32_t v_off, uint32_t slot_stride, int bs_log2, int num_kv_heads,
+                             int num_q_heads, const int2* __restrict__ work, int num_work,
+                             const float* __restrict__ q, const uint32_t* __restrict__ positions,
+                             const int32_t* __restrict__ row_seq,
+                             const int64_t* __restrict__ bt_off, const uint32_t* __restrict__ bt_ids,
+                             int chunk, int max_splits, float scale, float* __restrict__ out,
+                             float* __restrict__ ws_o, float* __restrict__ ws_ml) {
+  constexpr int GP = (G + 3) & ~3;
+  __shared__ float lds_p[4][16 * NT * GP];
+  __shared__ float lds_a[4][GP];
+  __shared__ float lds_l[4][GP];
+  const int wv = threadIdx.x >> 6;
+  const int w = blockIdx.x * 4 + wv;
+  if (w >= num_work) return;
+  const int2 wk = work[w];
+  const int row = wk.x / num_kv_heads, kvh = wk.x - row * num_kv_heads, start = wk.y;
+  const int len = (int)positions[row] + 1;
+  const int end = min(len, start + chunk);
+  const int nsplit = (len + chunk - 1) / chunk;
+  decode_wave_mfma<D, G, NT, BIG_BLOCKS>(kv_layer, blk_stride, v_off, slot_stride, bs_log2,
+                                         num_q_heads, q, row_seq, bt_off, bt_ids, max_splits, scale,
+                                         out, ws_o, ws_ml, lds_p[wv], lds_a[wv], lds_l[wv], row, kvh,
+                                         start, end, start / chunk, nsplit);
+}
+
 // Merges the per-split states of rows whose context spans several splits.
 // One wave per (row, query head).
 template <int D>
@@ -262,105 +563,97 @@ __global__ void __launch_bounds__(256)
   for (int i = 0; i < PER; ++i) out[item * D + lane + 64 * i] = acc[i] * inv;
 }
 
-template <typename T, int D>
-static hipError_t launch_decode_g(int G, dim3 grid, hipStream_t st, const T* kv, int64_t bstr,
-                                  int64_t voff, int64_t sstr, int bsl, int hkv, int hq, int items,
-                                  const float* q, const uint32_t* pos, const int32_t* rs,
-                                  const int64_t* bo, const uint32_t* bi, int P, int ms, float scale,
-                                  float* out, float* wo, float* wml) {
-#define ORION_DECODE_CASE(GG)                                                                   \
-  case GG:                                                                                      \
-    hipLaunchKernelGGL((paged_decode_kernel<T, D, GG>), grid, dim3(256), 0, st, kv, bstr, voff, \
-                       sstr, bsl, hkv, hq, items, q, pos, rs, bo, bi, P, ms, scale, out, wo,    \
-                       wml);                                                                    \
-    break;
-  switch (G) {
-    ORION_DECODE_CASE(1)
-    ORION_DECODE_CASE(2)
-    ORION_DECODE_CASE(3)
-    ORION_DECODE_CASE(4)
-    ORION_DECODE_CASE(5)
-    ORION_DECODE_CASE(6)
-    ORION_DECODE_CASE(7)
-    ORION_DECODE_CASE(8)
-    default:
-      return hipErrorInvalidValue;
+// ---------------------------------------------------------------------------
+// Host side: decode plans and launch
+// ---------------------------------------------------------------------------
+
+// Decode work decomposition.  A work item is (row, KV head, chunk of the
+// row's context) and runs on one wave.  All full chunks come first and the
+// partial tail chunks last, longest first (LPT list scheduling), so the final
+// waves to be dispatched are the shortest.  The chunk length is chosen by
+// simulating that schedule on the chip's resident wave slots (greedy: each
+// item goes to the slot that frees up first), with a fixed per-item cost
+// for setup and the split-K merge.
+static int64_t simulate_makespan(const std::vector<int>& lens, int64_t hkv, int C,
+                                 int64_t slots) {
+  std::vector<int> sizes;
+  for (int L : lens) {
+    const int full = L / C;
+    for (int64_t h = 0; h < hkv; ++h)
+      for (int s = 0; s < full; ++s) sizes.push_back(C);
   }
-#undef ORION_DECODE_CASE
-  return hipGetLastError();
+  std::vector<int> tails;
+  for (int L : lens)
+    if (L % C)
+      for (int64_t h = 0; h < hkv; ++h) tails.push_back(L % C);
+  std::sort(tails.begin(), tails.end(), std::greater<int>());
+  sizes.insert(sizes.end(), tails.begin(), tails.end());
+  constexpr int kItemOverhead = 48;  // tokens-equivalent per item
+  if ((int64_t)sizes.size() <= slots) {
+    int64_t mx = 0;
+    for (int v : sizes) mx = std::max<int64_t>(mx, v + kItemOverhead);
+    return mx;
+  }
+  std::priority_queue<int64_t, std::vector<int64_t>, std::greater<int64_t>> pq;
+  for (int64_t i = 0; i < slots; ++i) pq.push(0);
+  int64_t mx = 0;
+  for (int v : sizes) {
+    int64_t t = pq.top();
+    pq.pop();
+    t += v + kItemOverhead;
+    mx = std::max(mx, t);
+    pq.push(t);
+  }
+  return mx;
 }
 
-int decode_partition_for(int64_t num_items, int64_t max_len, int64_t block_size) {
-  // Enough (item, split) waves to cover the chip several times over, with
-  // partitions no shorter than 64 tokens.  A partition is a multiple of 16
-  // tokens and of the block size, and spans at most 64 blocks.
-  int P = 512;
-  while (P > 64 && num_items * ((max_len + P - 1) / P) < 4096) P >>= 1;
-  if (P < block_size) P = (int)block_size;
-  if (P / block_size > 64) P = (int)(64 * block_size);
-  return P;
-}
-
-hipError_t launch_paged_decode(hipStream_t st, const KvGeom& kv, const void* arena, int64_t layer,
-                               const float* q, int64_t rows, int64_t hq,
-                               const uint32_t* positions, const int32_t* row_seq,
-                               const int64_t* bt_off, const uint32_t* bt_ids, int64_t max_position,
-                               float* out, float* ws, size_t ws_bytes) {
-  if (rows == 0) return hipSuccess;
-  const int64_t hkv = kv.num_kv_heads, D = kv.head_dim;
-  const int G = (int)(hq / hkv);
-  const int64_t items = rows * hkv;
-  const int P = decode_partition_for(items, max_position + 1, kv.block_size);
-  const int max_splits = (int)((max_position + 1 + P - 1) / P);
-  const size_t need = decode_workspace_bytes(rows, hq, D, max_splits);
-  if (max_splits > 1 && need > ws_bytes) return hipErrorOutOfMemory;
-  float* ws_o = ws;
-  float* ws_ml = ws ? ws + rows * hq * max_splits * D : nullptr;
-  int bs_log2 = 0;
-  while ((1 << bs_log2) < kv.block_size) ++bs_log2;
-  const int64_t slot_stride = hkv * D;
-  const int64_t v_off = kv.block_size * slot_stride;
-  const int64_t blk_stride = 2 * v_off;
-  const int64_t layer_elems = kv.num_blocks * blk_stride;
-  const float scale = 1.0f / sqrtf((float)D);
-  dim3 grid((unsigned)((items + 3) / 4), (unsigned)max_splits);
-  hipError_t e;
-  if (kv.dtype_bf16) {
-    const uint16_t* base = static_cast<const uint16_t*>(arena) + layer * layer_elems;
-    if (D == 128)
-      e = launch_decode_g<uint16_t, 128>(G, grid, st, base, blk_stride, v_off, slot_stride,
-                                         bs_log2, (int)hkv, (int)hq, (int)items, q, positions,
-                                         row_seq, bt_off, bt_ids, P, max_splits, scale, out, ws_o,
-                                         ws_ml);
-    else if (D == 64)
-      e = launch_decode_g<uint16_t, 64>(G, grid, st, base, blk_stride, v_off, slot_stride,
-                                        bs_log2, (int)hkv, (int)hq, (int)items, q, positions,
-                                        row_seq, bt_off, bt_ids, P, max_splits, scale, out, ws_o,
-                                        ws_ml);
-    else
-      return hipErrorInvalidValue;
-  } else {
-    const float* base = static_cast<const float*>(arena) + layer * layer_elems;
-    if (D == 128)
-      e = launch_decode_g<float, 128>(G, grid, st, base, blk_stride, v_off, slot_stride, bs_log2,
-                                      (int)hkv, (int)hq, (int)items, q, positions, row_seq,
-                                      bt_off, bt_ids, P, max_splits, scale, out, ws_o, ws_ml);
-    else if (D == 64)
-      e = launch_decode_g<float, 64>(G, grid, st, base, blk_stride, v_off, slot_stride, bs_log2,
-                                     (int)hkv, (int)hq, (int)items, q, positions, row_seq, bt_off,
-                                     bt_ids, P, max_splits, scale, out, ws_o, ws_ml);
-    else
-      return hipErrorInvalidValue;
+void build_decode_plan(const uint32_t* positions, int64_t rows, int64_t hkv, int64_t block_size,
+                       int64_t wave_slots, DecodePlanHost* plan) {
+  std::vector<int> lens(rows);
+  int max_len = 0;
+  for (int64_t r = 0; r < rows; ++r) {
+    lens[r] = (int)positions[r] + 1;
+    max_len = std::max(max_len, lens[r]);
   }
-  if (e != hipSuccess || max_splits == 1) return e;
-  dim3 cgrid((unsigned)((rows * hq + 3) / 4));
-  if (D == 128)
-    hipLaunchKernelGGL(paged_decode_combine_kernel<128>, cgrid, dim3(256), 0, st, (int)rows,
-                       (int)hq, positions, P, max_splits, ws_o, ws_ml, out);
-  else
-    hipLaunchKernelGGL(paged_decode_combine_kernel<64>, cgrid, dim3(256), 0, st, (int)rows,
-                       (int)hq, positions, P, max_splits, ws_o, ws_ml, out);
-  return hipGetLastError();
+  int best_c = 0;
+  int64_t best_t = 0;
+  for (int C = 64; C <= 2048; C <<= 1) {
+    if (C < block_size || C / block_size > 64) continue;
+    const int64_t t = simulate_makespan(lens, hkv, C, wave_slots);
+    if (best_c == 0 || t < best_t) {
+      best_c = C;
+      best_t = t;
+    }
+  }
+  if (best_c == 0) best_c = (int)std::max<int64_t>(block_size, 64);
+  // ORION_DECODE_CHUNK overrides the choice (measurement knob).
+  static const int forced = [] {
+    const char* e = getenv("ORION_DECODE_CHUNK");
+    return e ? atoi(e) : 0;
+  }();
+  if (forced >= 16 && (forced & (forced - 1)) == 0 && forced >= block_size &&
+      forced / block_size <= 64)
+    best_c = forced;
+  const int C = best_c;
+  plan->chunk = C;
+  plan->max_splits = rows ? (max_len + C - 1) / C : 0;
+  plan->work.clear();
+  std::vector<std::pair<int, int>> tails;  // (tail length, row)
+  for (int64_t r = 0; r < rows; ++r) {
+    const int full = lens[r] / C;
+    for (int s = 0; s < full; ++s)
+      for (int64_t h = 0; h < hkv; ++h)
+        plan->work.push_back({(int32_t)(r * hkv + h), (int32_t)(s * C)});
+    if (lens[r] % C) tails.push_back({lens[r] % C, (int)r});
+  }
+  std::stable_sort(tails.begin(), tails.end(),
+                   [](const std::pair<int, int>& a, const std::pair<int, int>& b) {
+                     return a.first > b.first;
+                   });
+  for (const auto& t : tails)
+    for (int64_t h = 0; h < hkv; ++h)
+      plan->work.push_back(
+          {(int32_t)(t.second * hkv + h), (int32_t)((lens[t.second] / C) * C)});
 }
 
 size_t decode_workspace_bytes(int64_t rows, int64_t hq, int64_t D, int64_t max_splits) {
@@ -368,9 +661,123 @@ size_t decode_workspace_bytes(int64_t rows, int64_t hq, int64_t D, int64_t max_s
   return (size_t)(rows * hq * max_splits) * (size_t)(D + 2) * sizeof(float);
 }
 
-int64_t decode_max_splits(int64_t rows, int64_t hkv, int64_t max_position, int64_t block_size) {
-  const int P = decode_partition_for(rows * hkv, max_position + 1, block_size);
-  return (max_position + 1 + P - 1) / P;
+template <typename T, int D>
+static hipError_t launch_valu(int G, dim3 grid, dim3 block, hipStream_t st, const T* kv,
+                              int64_t bstr, int64_t voff, int64_t sstr, int bsl, int hkv, int hq,
+                              const int2* work, int nwork, const float* q, const uint32_t* pos,
+                              const int32_t* rs, const int64_t* bo, const uint32_t* bi, int C,
+                              int ms, float scale, float* out, float* wo, float* wml) {
+#define ORION_VALU_CASE(GG)                                                                   \
+  case GG:                                                                                    \
+    hipLaunchKernelGGL((paged_decode_kernel<T, D, GG>), grid, block, 0, st, kv, bstr, voff,   \
+                       sstr, bsl, hkv, hq, work, nwork, q, pos, rs, bo, bi, C, ms, scale, out,\
+                       wo, wml);                                                              \
+    break;
+  switch (G) {
+    ORION_VALU_CASE(1)
+    ORION_VALU_CASE(2)
+    ORION_VALU_CASE(3)
+    ORION_VALU_CASE(4)
+    ORION_VALU_CASE(5)
+    ORION_VALU_CASE(6)
+    ORION_VALU_CASE(7)
+    ORION_VALU_CASE(8)
+    default:
+      return hipErrorInvalidValue;
+  }
+#undef ORION_VALU_CASE
+  return hipGetLastError();
+}
+
+template <int D, bool BIG, int NT>
+static hipError_t launch_mfma(int G, dim3 grid, dim3 block, hipStream_t st, const uint16_t* kv,
+                              uint32_t bstr, uint32_t voff, uint32_t sstr, int bsl, int hkv,
+                              int hq, const int2* work, int nwork, const float* q,
+                              const uint32_t* pos,
+                              const int32_t* rs, const int64_t* bo, const uint32_t* bi, int C,
+                              int ms, float scale, float* out, float* wo, float* wml) {
+#define ORION_MFMA_CASE(GG)                                                                   \
+  case GG:                                                                                    \
+    hipLaunchKernelGGL((paged_decode_mfma_kernel<D, GG, NT, BIG>), grid, block, 0, st, kv,    \
+                       bstr, voff, sstr, bsl, hkv, hq, work, nwork, q, pos, rs, bo, bi, C, ms,  \
+                       scale, out, wo, wml);                                                  \
+    break;
+  switch (G) {
+    ORION_MFMA_CASE(1)
+    ORION_MFMA_CASE(2)
+    ORION_MFMA_CASE(3)
+    ORION_MFMA_CASE(4)
+    ORION_MFMA_CASE(5)
+    ORION_MFMA_CASE(6)
+    ORION_MFMA_CASE(7)
+    ORION_MFMA_CASE(8)
+    default:
+      return hipErrorInvalidValue;
+  }
+#undef ORION_MFMA_CASE
+  return hipGetLastError();
+}
+
+hipError_t launch_paged_decode(hipStream_t st, const KvGeom& kv, const void* arena, int64_t layer,
+                               const float* q, int64_t rows, int64_t hq,
+                               const uint32_t* positions, const int32_t* row_seq,
+                               const int64_t* bt_off, const uint32_t* bt_ids,
+                               const DecodePlanDev& plan, float* out) {
+  if (rows == 0 || plan.num_work == 0) return hipSuccess;
+  const int64_t hkv = kv.num_kv_heads, D = kv.head_dim;
+  const int G = (int)(hq / hkv);
+  const int C = plan.chunk, ms = plan.max_splits;
+  if (ms > 1 && plan.ws_bytes < decode_workspace_bytes(rows, hq, D, ms))
+    return hipErrorInvalidValue;
+  float* ws_o = plan.ws;
+  float* ws_ml = ws_o ? ws_o + rows * hq * ms * D : nullptr;
+  int bs_log2 = 0;
+  while ((1 << bs_log2) < kv.block_size) ++bs_log2;
+  const int64_t slot_stride = hkv * D;
+  const int64_t v_off = kv.block_size * slot_stride;
+  const int64_t blk_stride = 2 * v_off;
+  const int64_t layer_elems = kv.num_blocks * blk_stride;
+  const float scale = 1.0f / sqrtf((float)D);
+  const dim3 grid((unsigned)((plan.num_work + 3) / 4));
+  const dim3 block(256);
+  hipError_t e;
+  if (kv.dtype_bf16) {
+    if (layer_elems > (int64_t)UINT32_MAX) return hipErrorInvalidValue;
+    const uint16_t* base = static_cast<const uint16_t*>(arena) + layer * layer_elems;
+    const bool big = kv.block_size >= 16;
+#define ORION_MFMA(DD, BB)                                                                    \
+  launch_mfma<DD, BB, 2>(G, grid, block, st, base, (uint32_t)blk_stride, (uint32_t)v_off,    \
+                         (uint32_t)slot_stride, bs_log2, (int)hkv, (int)hq, plan.work, plan.num_work, q,    \
+                         positions, row_seq, bt_off, bt_ids, C, ms, scale, out, ws_o, ws_ml)
+    if (D == 128)
+      e = big ? ORION_MFMA(128, true) : ORION_MFMA(128, false);
+    else if (D == 64)
+      e = big ? ORION_MFMA(64, true) : ORION_MFMA(64, false);
+    else
+      return hipErrorInvalidValue;
+#undef ORION_MFMA
+  } else {
+    const float* base = static_cast<const float*>(arena) + layer * layer_elems;
+    if (D == 128)
+      e = launch_valu<float, 128>(G, grid, block, st, base, blk_stride, v_off, slot_stride,
+                                  bs_log2, (int)hkv, (int)hq, plan.work, plan.num_work, q, positions, row_seq,
+                                  bt_off, bt_ids, C, ms, scale, out, ws_o, ws_ml);
+    else if (D == 64)
+      e = launch_valu<float, 64>(G, grid, block, st, base, blk_stride, v_off, slot_stride,
+                                 bs_log2, (int)hkv, (int)hq, plan.work, plan.num_work, q, positions, row_seq,
+                                 bt_off, bt_ids, C, ms, scale, out, ws_o, ws_ml);
+    else
+      return hipErrorInvalidValue;
+  }
+  if (e != hipSuccess || ms == 1) return e;
+  dim3 cgrid((unsigned)((rows * hq + 3) / 4));
+  if (D == 128)
+    hipLaunchKernelGGL(paged_decode_combine_kernel<128>, cgrid, dim3(256), 0, st, (int)rows,
+                       (int)hq, positions, C, ms, ws_o, ws_ml, out);
+  else
+    hipLaunchKernelGGL(paged_decode_combine_kernel<64>, cgrid, dim3(256), 0, st, (int)rows,
+                       (int)hq, positions, C, ms, ws_o, ws_ml, out);
+  return hipGetLastError();
 }
 
 }  // namespace orion

@@ -79,6 +79,17 @@ __device__ inline double wave_sum_f64(double v) {
   return v;
 }
 
+// Orders LDS traffic between the lanes of one wave: every LDS write issued
+// before the call is visible to every lane's LDS read after it.  The fences
+// are wavefront-scope (a wave's LDS operations execute in order, so no
+// hardware wait is needed); they stop the compiler from moving memory
+// operations across the exchange point, which wave_barrier alone does not.
+__device__ inline void wave_lds_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
 // Split an f32 into hi + lo bf16 terms: hi = rne(x), lo = rne(x - hi).
 // x - hi is exact in f32, so hi + lo carries ~16 significant bits of x.
 __device__ inline void split_bf16(float x, uint16_t& hi, uint16_t& lo) {

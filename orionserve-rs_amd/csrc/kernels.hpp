@@ -5,6 +5,7 @@
 #include <hip/hip_runtime.h>
 #include <cstddef>
 #include <cstdint>
+#include <vector>
 
 namespace orion {
 
@@ -15,14 +16,30 @@ struct KvGeom {
 };
 
 // ---- attention --------------------------------------------------------------
-int decode_partition_for(int64_t num_items, int64_t max_len, int64_t block_size);
-int64_t decode_max_splits(int64_t rows, int64_t hkv, int64_t max_position, int64_t block_size);
+// Decode work plan: (row * Hkv + kv_head, chunk start) items in longest-first
+// order; built on the host from the query positions, shared by every layer of
+// a forward.
+struct DecodePlanHost {
+  int chunk = 0;       // tokens per chunk (power of two)
+  int max_splits = 0;  // chunks of the longest row
+  std::vector<int2> work;
+};
+struct DecodePlanDev {
+  const int2* work = nullptr;
+  int num_work = 0;
+  int chunk = 0;
+  int max_splits = 0;
+  float* ws = nullptr;  // split-K partials, decode_workspace_bytes()
+  size_t ws_bytes = 0;
+};
+void build_decode_plan(const uint32_t* positions, int64_t rows, int64_t hkv, int64_t block_size,
+                       int64_t wave_slots, DecodePlanHost* plan);
 size_t decode_workspace_bytes(int64_t rows, int64_t hq, int64_t D, int64_t max_splits);
 hipError_t launch_paged_decode(hipStream_t st, const KvGeom& kv, const void* arena, int64_t layer,
                                const float* q, int64_t rows, int64_t hq,
                                const uint32_t* positions, const int32_t* row_seq,
-                               const int64_t* bt_off, const uint32_t* bt_ids, int64_t max_position,
-                               float* out, float* ws, size_t ws_bytes);
+                               const int64_t* bt_off, const uint32_t* bt_ids,
+                               const DecodePlanDev& plan, float* out);
 
 hipError_t launch_paged_prefill(hipStream_t st, const KvGeom& kv, const void* arena,
                                 int64_t layer, const float* q, int64_t hq, int64_t num_seqs,

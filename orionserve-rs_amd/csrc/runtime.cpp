@@ -140,7 +140,28 @@ struct orion_hip_device {
   hipStream_t stream = nullptr;
   hipEvent_t ev_start = nullptr, ev_stop = nullptr;
   std::string name;
-  DevBuf attn_ws;  // split-K workspace for the op-level attention entry point
+  int64_t wave_slots = 2048;  // resident decode waves: CUs x 4 SIMDs x 2
+};
+
+struct orion_hip_decode_plan {
+  orion_hip_device* dev = nullptr;
+  int64_t rows = 0, hq = 0, hkv = 0, head_dim = 0, block_size = 0;
+  DecodePlanHost host;
+  DevBuf work, ws;
+  ~orion_hip_decode_plan() {
+    work.release();
+    ws.release();
+  }
+  DecodePlanDev view() const {
+    DecodePlanDev d;
+    d.work = work.as<const int2>();
+    d.num_work = (int)host.work.size();
+    d.chunk = host.chunk;
+    d.max_splits = host.max_splits;
+    d.ws = ws.as<float>();
+    d.ws_bytes = ws.bytes;
+    return d;
+  }
 };
 
 struct LayerDev {
@@ -233,6 +254,7 @@ ORION_EXPORT int orion_hip_device_open(int ordinal, orion_hip_device** out) {
   auto dev = std::make_unique<orion_hip_device>();
   dev->ordinal = ordinal;
   dev->name = prop.name;
+  dev->wave_slots = (int64_t)prop.multiProcessorCount * 8;
   HIP_TRY("device_open", hipStreamCreateWithFlags(&dev->stream, hipStreamNonBlocking));
   HIP_TRY("device_open", hipEventCreate(&dev->ev_start));
   HIP_TRY("device_open", hipEventCreate(&dev->ev_stop));
@@ -244,7 +266,6 @@ ORION_EXPORT void orion_hip_device_close(orion_hip_device* dev) {
   if (!dev) return;
   (void)hipSetDevice(dev->ordinal);
   (void)hipStreamSynchronize(dev->stream);
-  dev->attn_ws.release();
   (void)hipEventDestroy(dev->ev_start);
   (void)hipEventDestroy(dev->ev_stop);
   (void)hipStreamDestroy(dev->stream);
@@ -797,8 +818,10 @@ ORION_EXPORT int orion_hip_model_forward(orion_hip_model* m, const orion_hip_bat
   HIP_TRY(st, m->act.reserve(n * F * 4));
   HIP_TRY(st, m->logits.reserve(S * V * 4));
   HIP_TRY(st, m->argmax.reserve(S * 8));
-  const int64_t splits = decode_max_splits(n, d.num_kv_heads, hb.max_position, d.block_size);
-  HIP_TRY(st, m->ws.reserve(decode_workspace_bytes(n, Hq, d.head_dim, splits)));
+  // Decode plan (longest-first chunk list), shared by every layer.
+  DecodePlanHost plan;
+  build_decode_plan(b->positions, n, d.num_kv_heads, d.block_size, m->dev->wave_slots, &plan);
+  HIP_TRY(st, m->ws.reserve(decode_workspace_bytes(n, Hq, d.head_dim, plan.max_splits)));
 
   // ---- upload the batch: one pinned staging area, one copy ----
   const size_t o_tok = 0;
@@ -807,7 +830,8 @@ ORION_EXPORT int orion_hip_model_forward(orion_hip_model* m, const orion_hip_bat
   const size_t o_last = o_rs + n * 4;
   const size_t o_btoff = (o_last + S * 4 + 7) & ~(size_t)7;
   const size_t o_btids = o_btoff + (S + 1) * 8;
-  const size_t total = o_btids + nbt * 4;
+  const size_t o_work = (o_btids + nbt * 4 + 7) & ~(size_t)7;
+  const size_t total = o_work + plan.work.size() * sizeof(int2);
   if (total > m->pinned_bytes) {
     if (m->pinned) {
       HIP_TRY(st, hipStreamSynchronize(stream));
@@ -827,6 +851,7 @@ ORION_EXPORT int orion_hip_model_forward(orion_hip_model* m, const orion_hip_bat
   std::memcpy(hp + o_last, hb.last_rows.data(), S * 4);
   std::memcpy(hp + o_btoff, b->block_table_offsets, (S + 1) * 8);
   std::memcpy(hp + o_btids, b->block_table_ids, nbt * 4);
+  std::memcpy(hp + o_work, plan.work.data(), plan.work.size() * sizeof(int2));
   char* dp = m->b_tokens.as<char>();
   HIP_TRY(st, hipMemcpyAsync(dp, hp, total, hipMemcpyHostToDevice, stream));
   const uint32_t* d_tok = reinterpret_cast<const uint32_t*>(dp + o_tok);
@@ -835,6 +860,13 @@ ORION_EXPORT int orion_hip_model_forward(orion_hip_model* m, const orion_hip_bat
   const int32_t* d_last = reinterpret_cast<const int32_t*>(dp + o_last);
   const int64_t* d_btoff = reinterpret_cast<const int64_t*>(dp + o_btoff);
   const uint32_t* d_btids = reinterpret_cast<const uint32_t*>(dp + o_btids);
+  DecodePlanDev dplan;
+  dplan.work = reinterpret_cast<const int2*>(dp + o_work);
+  dplan.num_work = (int)plan.work.size();
+  dplan.chunk = plan.chunk;
+  dplan.max_splits = plan.max_splits;
+  dplan.ws = m->ws.as<float>();
+  dplan.ws_bytes = m->ws.bytes;
 
   float* hidden = m->hidden.as<float>();
   float* xn = m->xn.as<float>();
@@ -852,8 +884,7 @@ ORION_EXPORT int orion_hip_model_forward(orion_hip_model* m, const orion_hip_bat
                                       qkv + m->qd, m->qkvd, qkv + m->qd + m->kvd, m->qkvd, d_pos,
                                       d_rs, d_btoff, d_btids, m->rope_cos, m->rope_sin));
     HIP_TRY(st, launch_paged_decode(stream, m->kv, m->arena, l, qrot, n, Hq, d_pos, d_rs, d_btoff,
-                                    d_btids, hb.max_position, attn, m->ws.as<float>(),
-                                    m->ws.bytes));
+                                    d_btids, dplan, attn));
     HIP_TRY(st, launch_gemm(stream, attn, L.w_o, nullptr, n, H, m->qd, Epilogue::kAccumulate,
                             hidden));
     HIP_TRY(st, launch_rmsnorm(stream, hidden, nullptr, L.post_norm, n, H, d.rms_norm_eps, xn));
@@ -894,11 +925,56 @@ static int kv_geom_from(const orion_hip_kv_layout* kv, KvGeom* g, const char* st
   return ORION_HIP_OK;
 }
 
+ORION_EXPORT int orion_hip_decode_plan_create(orion_hip_device* dev, const uint32_t* positions,
+                                             int64_t num_rows, int64_t num_q_heads,
+                                             int64_t num_kv_heads, int64_t head_dim,
+                                             int64_t block_size, orion_hip_decode_plan** out) {
+  const char* st = "decode_plan";
+  *out = nullptr;
+  if (num_rows < 0 || num_kv_heads <= 0 || num_q_heads % num_kv_heads || head_dim <= 0 ||
+      block_size < 1 || (block_size & (block_size - 1)) || block_size > 256)
+    return internal(st, "invalid plan geometry");
+  HIP_TRY(st, hipSetDevice(dev->ordinal));
+  auto p = std::make_unique<orion_hip_decode_plan>();
+  p->dev = dev;
+  p->rows = num_rows;
+  p->hq = num_q_heads;
+  p->hkv = num_kv_heads;
+  p->head_dim = head_dim;
+  p->block_size = block_size;
+  build_decode_plan(positions, num_rows, num_kv_heads, block_size, dev->wave_slots, &p->host);
+  const size_t wbytes = p->host.work.size() * sizeof(int2);
+  HIP_TRY(st, p->work.reserve(wbytes));
+  if (wbytes)
+    HIP_TRY(st, hipMemcpyAsync(p->work.ptr, p->host.work.data(), wbytes, hipMemcpyHostToDevice,
+                               dev->stream));
+  HIP_TRY(st, p->ws.reserve(
+                  decode_workspace_bytes(num_rows, num_q_heads, head_dim, p->host.max_splits)));
+  HIP_TRY(st, hipStreamSynchronize(dev->stream));
+  *out = p.release();
+  return ORION_HIP_OK;
+}
+
+ORION_EXPORT void orion_hip_decode_plan_destroy(orion_hip_decode_plan* plan) {
+  if (!plan) return;
+  (void)hipSetDevice(plan->dev->ordinal);
+  (void)hipStreamSynchronize(plan->dev->stream);
+  delete plan;
+}
+
+ORION_EXPORT int orion_hip_decode_plan_info(const orion_hip_decode_plan* plan, int64_t* chunk,
+                                            int64_t* num_work, int64_t* max_splits) {
+  *chunk = plan->host.chunk;
+  *num_work = (int64_t)plan->host.work.size();
+  *max_splits = plan->host.max_splits;
+  return ORION_HIP_OK;
+}
+
 ORION_EXPORT int orion_hip_paged_attention_decode(
     orion_hip_device* dev, const orion_hip_kv_layout* kv, const void* d_arena, int64_t layer,
     const float* d_q, int64_t num_rows, int64_t num_q_heads, const uint32_t* d_positions,
     const int32_t* d_row_seq, const int64_t* d_bt_offsets, const uint32_t* d_bt_ids,
-    int64_t max_position, float* d_out) {
+    const orion_hip_decode_plan* plan, float* d_out) {
   const char* st = "paged_attention_decode";
   KvGeom g;
   if (int rc = kv_geom_from(kv, &g, st)) return rc;
@@ -910,12 +986,14 @@ ORION_EXPORT int orion_hip_paged_attention_decode(
   if (layer < 0 || layer >= g.num_layers)
     return internal(st, "layer %lld out of range (have %lld)", (long long)layer,
                     (long long)g.num_layers);
+  if (!plan || plan->rows != num_rows || plan->hq != num_q_heads ||
+      plan->hkv != g.num_kv_heads || plan->head_dim != g.head_dim ||
+      plan->block_size != g.block_size)
+    return internal(st, "decode plan does not match this call's geometry");
   HIP_TRY(st, hipSetDevice(dev->ordinal));
-  const int64_t splits = decode_max_splits(num_rows, g.num_kv_heads, max_position, g.block_size);
-  HIP_TRY(st, dev->attn_ws.reserve(decode_workspace_bytes(num_rows, num_q_heads, g.head_dim, splits)));
   HIP_TRY(st, launch_paged_decode(dev->stream, g, d_arena, layer, d_q, num_rows, num_q_heads,
-                                  d_positions, d_row_seq, d_bt_offsets, d_bt_ids, max_position,
-                                  d_out, dev->attn_ws.as<float>(), dev->attn_ws.bytes));
+                                  d_positions, d_row_seq, d_bt_offsets, d_bt_ids, plan->view(),
+                                  d_out));
   return ORION_HIP_OK;
 }
 

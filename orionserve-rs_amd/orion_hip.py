@@ -42,7 +42,8 @@ EXPORTED = [
     "orion_hip_model_create", "orion_hip_model_destroy", "orion_hip_model_upload_weight",
     "orion_hip_model_init_synthetic", "orion_hip_synthetic_value",
     "orion_hip_model_download_weight", "orion_hip_model_forward", "orion_hip_model_kv_read",
-    "orion_hip_model_kv_write", "orion_hip_model_kv_arena", "orion_hip_paged_attention_decode",
+    "orion_hip_model_kv_write", "orion_hip_model_kv_arena", "orion_hip_decode_plan_create",
+    "orion_hip_decode_plan_destroy", "orion_hip_decode_plan_info", "orion_hip_paged_attention_decode",
     "orion_hip_paged_attention_prefill", "orion_hip_rope_and_cache", "orion_hip_rmsnorm",
     "orion_hip_gemm", "orion_hip_silu_mul", "orion_hip_argmax",
 ]
@@ -138,8 +139,11 @@ def load_library(path: str = LIB_PATH) -> C.CDLL:
         "orion_hip_model_kv_read": ([vp, i64, u32, i64, i64, C.c_int, vp], C.c_int),
         "orion_hip_model_kv_write": ([vp, i64, u32, i64, i64, C.c_int, vp, i64], C.c_int),
         "orion_hip_model_kv_arena": ([vp, P(vp), P(sz)], C.c_int),
+        "orion_hip_decode_plan_create": ([vp, vp, i64, i64, i64, i64, i64, P(vp)], C.c_int),
+        "orion_hip_decode_plan_destroy": ([vp], None),
+        "orion_hip_decode_plan_info": ([vp, P(i64), P(i64), P(i64)], C.c_int),
         "orion_hip_paged_attention_decode": (
-            [vp, P(KvLayout), vp, i64, vp, i64, i64, vp, vp, vp, vp, i64, vp], C.c_int),
+            [vp, P(KvLayout), vp, i64, vp, i64, i64, vp, vp, vp, vp, vp, vp], C.c_int),
         "orion_hip_paged_attention_prefill": (
             [vp, P(KvLayout), vp, i64, vp, i64, i64, vp, vp, vp, vp, vp, i64, i64, vp], C.c_int),
         "orion_hip_rope_and_cache": (
@@ -484,13 +488,39 @@ def kv_layout(num_layers, num_blocks, block_size, num_kv_heads, head_dim, dtype)
     return KvLayout(num_layers, num_blocks, block_size, num_kv_heads, head_dim, dtype)
 
 
+class DecodePlan:
+    """orion_hip_decode_plan: the longest-first (row, chunk) work list for one
+    batch of decode rows, built from the rows' positions (host copy)."""
+
+    def __init__(self, be: HipBackend, positions, num_q_heads: int, num_kv_heads: int,
+                 head_dim: int, block_size: int):
+        pos = np.ascontiguousarray(positions, dtype=np.uint32)
+        h = C.c_void_p()
+        _check(be.lib.orion_hip_decode_plan_create(be.handle, pos.ctypes.data, pos.size,
+                                                   num_q_heads, num_kv_heads, head_dim,
+                                                   block_size, C.byref(h)))
+        self.be = be
+        self.handle = h.value
+
+    def info(self):
+        c, n, m = C.c_int64(), C.c_int64(), C.c_int64()
+        _check(self.be.lib.orion_hip_decode_plan_info(self.handle, C.byref(c), C.byref(n),
+                                                      C.byref(m)))
+        return {"chunk": c.value, "num_work": n.value, "max_splits": m.value}
+
+    def close(self) -> None:
+        if self.handle:
+            self.be.lib.orion_hip_decode_plan_destroy(self.handle)
+            self.handle = None
+
+
 def paged_attention_decode(be: HipBackend, kv: KvLayout, arena_ptr: int, layer: int, q_ptr: int,
                            num_rows: int, num_q_heads: int, pos_ptr: int, row_seq_ptr: int,
-                           bt_off_ptr: int, bt_ids_ptr: int, max_position: int,
+                           bt_off_ptr: int, bt_ids_ptr: int, plan: DecodePlan,
                            out_ptr: int) -> None:
     _check(be.lib.orion_hip_paged_attention_decode(
         be.handle, C.byref(kv), arena_ptr, layer, q_ptr, num_rows, num_q_heads, pos_ptr,
-        row_seq_ptr, bt_off_ptr, bt_ids_ptr, max_position, out_ptr))
+        row_seq_ptr, bt_off_ptr, bt_ids_ptr, plan.handle, out_ptr))
 
 
 def paged_attention_prefill(be: HipBackend, kv: KvLayout, arena_ptr: int, layer: int, q_ptr: int,
