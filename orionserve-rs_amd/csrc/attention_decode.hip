@@ -264,25 +264,25 @@ __global__ void __launch_bounds__(256)
 // iteration's MFMAs have consumed K, and the next V loads as soon as P.V has
 // consumed V, so K(i+1) streams in under the softmax and P.V of step i and
 // V(i+1) under the next Q.K^T.
-template <int D, int G, int NT, bool BIG_BLOCKS>
+template <int D, int G, int NS, bool BIG_BLOCKS, bool LOADS_ONLY = false>
 __device__ __forceinline__ void decode_wave_mfma(
     const uint16_t* __restrict__ kv_layer, uint32_t blk_stride, uint32_t v_off,
     uint32_t slot_stride, int bs_log2, int num_q_heads, const float* __restrict__ q,
     const int32_t* __restrict__ row_seq, const int64_t* __restrict__ bt_off,
     const uint32_t* __restrict__ bt_ids, int max_splits, float scale, float* __restrict__ out,
-    float* __restrict__ ws_o, float* __restrict__ ws_ml, float* P, float* A, float* Lr, int row, int kvh, int start, int end, int split, int nsplit) {
+    float* __restrict__ ws_o, float* __restrict__ ws_ml, float* P, float* A, float* Lr, int row,
+    int kvh, int start, int end, int split, int nsplit) {
   constexpr int KCH = D / 32;       // MFMA k-steps over the head dim
   constexpr int CH = D / 8;         // P.V lanes per token (8 bf16 each)
   constexpr int TPW = 64 / CH;      // tokens per V wave load
-  constexpr int T = 16 * NT;        // tokens per iteration
-  constexpr int RV = T / TPW;       // V loads per lane per iteration
+  constexpr int RV = 16 / TPW;      // V loads per lane per 16-token step
   constexpr int GP = (G + 3) & ~3;  // heads padded to the MFMA row quad
   static_assert(G <= 16 && TPW <= 16 && (16 % TPW) == 0, "unsupported shape");
 
   const int lane = threadIdx.x & 63;
   const int bs_mask = (1 << bs_log2) - 1;
 
-  // ---- block-table slice of this split, one entry per lane ----
+  // ---- block-table slice of this chunk, one entry per lane ----
   const int seq = row_seq[row];
   const uint32_t* tbl = bt_ids + bt_off[seq];
   const int first_blk = start >> bs_log2;
@@ -290,45 +290,45 @@ __device__ __forceinline__ void decode_wave_mfma(
   const int my_blk = lane < nblk ? (int)tbl[first_blk + lane] : 0;
 
   const uint16_t* base_k = kv_layer + (uint32_t)kvh * D;
-  const int kt = lane & 15;        // K token within a tile (MFMA column)
+  const int kt = lane & 15;        // K token within the step (MFMA column)
   const int kd = (lane >> 4) * 8;  // K dims chunk
   const int vt = lane / CH;        // V token group
   const int vc = lane % CH;        // V dims chunk
 
-  uint4 kr[NT][KCH], vr[RV];
+  // Ring of NS register stages, each one 16-token step of K and V.
+  uint4 kr[NS][KCH], vr[NS][RV];
   // Tokens past `end` are clamped to the last valid one; their weight is 0.
-  auto issue_k = [&](int b) {
+  auto issue = [&](uint4 (&ks)[KCH], uint4 (&vs)[RV], int b) {
+    const int jk = min(b + kt, end - 1);
+    if constexpr (BIG_BLOCKS) {
+      // b is 16-aligned and blocks hold >= 16 tokens: one block per step.
+      const int blk = __builtin_amdgcn_readlane(my_blk, (b >> bs_log2) - first_blk);
+      const uint16_t* bb = base_k + (uint32_t)blk * blk_stride;
+      const uint16_t* kp = bb + (uint32_t)(jk & bs_mask) * slot_stride + kd;
 #pragma unroll
-    for (int t = 0; t < NT; ++t) {
-      const int j = min(b + 16 * t + kt, end - 1);
-      int blk;
-      if constexpr (BIG_BLOCKS)  // a 16-token tile lies inside one block
-        blk = __builtin_amdgcn_readlane(my_blk, (min(b + 16 * t, end - 1) >> bs_log2) - first_blk);
-      else
-        blk = __shfl(my_blk, (j >> bs_log2) - first_blk);
+      for (int c = 0; c < KCH; ++c) ks[c] = *reinterpret_cast<const uint4*>(kp + 32 * c);
+#pragma unroll
+      for (int r = 0; r < RV; ++r) {
+        const int jv = min(b + r * TPW + vt, end - 1);
+        vs[r] = *reinterpret_cast<const uint4*>(bb + (uint32_t)(jv & bs_mask) * slot_stride +
+                                                v_off + vc * 8);
+      }
+    } else {
+      const int bk = __shfl(my_blk, (jk >> bs_log2) - first_blk);
       const uint16_t* kp =
-          base_k + (uint32_t)blk * blk_stride + (uint32_t)(j & bs_mask) * slot_stride + kd;
+          base_k + (uint32_t)bk * blk_stride + (uint32_t)(jk & bs_mask) * slot_stride + kd;
 #pragma unroll
-      for (int c = 0; c < KCH; ++c) kr[t][c] = *reinterpret_cast<const uint4*>(kp + 32 * c);
+      for (int c = 0; c < KCH; ++c) ks[c] = *reinterpret_cast<const uint4*>(kp + 32 * c);
+#pragma unroll
+      for (int r = 0; r < RV; ++r) {
+        const int jv = min(b + r * TPW + vt, end - 1);
+        const int bv = __shfl(my_blk, (jv >> bs_log2) - first_blk);
+        vs[r] = *reinterpret_cast<const uint4*>(base_k + (uint32_t)bv * blk_stride +
+                                                (uint32_t)(jv & bs_mask) * slot_stride + v_off +
+                                                vc * 8);
+      }
     }
   };
-  auto issue_v = [&](int b) {
-#pragma unroll
-    for (int r = 0; r < RV; ++r) {
-      const int j = min(b + r * TPW + vt, end - 1);
-      int blk;
-      if constexpr (BIG_BLOCKS)
-        blk = __builtin_amdgcn_readlane(
-            my_blk, (min(b + (r * TPW / 16) * 16, end - 1) >> bs_log2) - first_blk);
-      else
-        blk = __shfl(my_blk, (j >> bs_log2) - first_blk);
-      vr[r] = *reinterpret_cast<const uint4*>(base_k + (uint32_t)blk * blk_stride +
-                                              (uint32_t)(j & bs_mask) * slot_stride + v_off +
-                                              vc * 8);
-    }
-  };
-  issue_k(start);
-  issue_v(start);
 
   // ---- query group as the MFMA A operand (hi/lo bf16) ----
   bf16x8 qa_hi[KCH], qa_lo[KCH];
@@ -374,69 +374,46 @@ __device__ __forceinline__ void decode_wave_mfma(
 
   const int hrow = (lane >> 4) * 4;  // first head of this lane's score quad
 
-  for (int b = start; b < end; b += T) {
-    const bool more = b + T < end;
-    // ---- S^T = Q . K^T, NT independent tiles ----
-    f32x4 acc[NT];
+  // One 16-token step on stage registers (ks, vs).
+  auto compute = [&](const uint4 (&ks)[KCH], const uint4 (&vs)[RV], int b) {
+    // S^T = Q . K^T; hi and lo terms in independent accumulators.
+    f32x4 ah = {0.f, 0.f, 0.f, 0.f}, al4 = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int t = 0; t < NT; ++t) acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int c = 0; c < KCH; ++c)
-#pragma unroll
-      for (int t = 0; t < NT; ++t) {
-        const bf16x8 kb = __builtin_bit_cast(bf16x8, kr[t][c]);
-        acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(qa_hi[c], kb, acc[t], 0, 0, 0);
-        acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(qa_lo[c], kb, acc[t], 0, 0, 0);
-      }
-    if (more) issue_k(b + T);
-
-    // ---- online softmax, max wave-uniform per head ----
+    for (int c = 0; c < KCH; ++c) {
+      const bf16x8 kb = __builtin_bit_cast(bf16x8, ks[c]);
+      ah = __builtin_amdgcn_mfma_f32_16x16x32_bf16(qa_hi[c], kb, ah, 0, 0, 0);
+      al4 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(qa_lo[c], kb, al4, 0, 0, 0);
+    }
+    const bool kvalid = b + kt < end;
+    float p[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      float s[NT];
-      float mx = -INFINITY;
-#pragma unroll
-      for (int t = 0; t < NT; ++t) {
-        s[t] = (b + 16 * t + kt < end) ? acc[t][i] * scale : -INFINITY;
-        mx = fmaxf(mx, s[t]);
-      }
-      mx = group_max<16>(mx);
-      const float m_new = fmaxf(m[i], mx);
+      const float s = kvalid ? (ah[i] + al4[i]) * scale : -INFINITY;
+      const float m_new = fmaxf(m[i], group_max<16>(s));
       const float alpha = __expf(m[i] - m_new);
-      float ps = 0.f;
-#pragma unroll
-      for (int t = 0; t < NT; ++t) {
-        s[t] = __expf(s[t] - m_new);
-        ps += s[t];
-        acc[t][i] = s[t];
-      }
-      lsum[i] = lsum[i] * alpha + ps;
+      p[i] = __expf(s - m_new);
+      lsum[i] = lsum[i] * alpha + p[i];
       m[i] = m_new;
       if (kt == 0 && hrow < GP) A[hrow + i] = alpha;
     }
-    if (hrow < GP) {
-#pragma unroll
-      for (int t = 0; t < NT; ++t)
-        *reinterpret_cast<float4*>(P + (16 * t + kt) * GP + hrow) =
-            make_float4(acc[t][0], acc[t][1], acc[t][2], acc[t][3]);
-    }
+    if (hrow < GP) *reinterpret_cast<float4*>(P + kt * GP + hrow) = make_float4(p[0], p[1], p[2], p[3]);
     wave_lds_sync();
 
-    // ---- P.V on VALU ----
-    float al[GP];
+    // P.V on VALU.
+    float alv[GP];
 #pragma unroll
     for (int g4 = 0; g4 < GP; g4 += 4) {
       const float4 a4 = *reinterpret_cast<const float4*>(A + g4);
-      al[g4] = a4.x; al[g4 + 1] = a4.y; al[g4 + 2] = a4.z; al[g4 + 3] = a4.w;
+      alv[g4] = a4.x; alv[g4 + 1] = a4.y; alv[g4 + 2] = a4.z; alv[g4 + 3] = a4.w;
     }
     bool rescale = false;
 #pragma unroll
-    for (int g = 0; g < G; ++g) rescale |= al[g] != 1.0f;
+    for (int g = 0; g < G; ++g) rescale |= alv[g] != 1.0f;
     if (rescale) {
 #pragma unroll
       for (int g = 0; g < G; ++g)
 #pragma unroll
-        for (int e = 0; e < 8; ++e) o[g][e] *= al[g];
+        for (int e = 0; e < 8; ++e) o[g][e] *= alv[g];
     }
 #pragma unroll
     for (int r = 0; r < RV; ++r) {
@@ -447,7 +424,7 @@ __device__ __forceinline__ void decode_wave_mfma(
         const float4 p4 = *reinterpret_cast<const float4*>(pr + g4);
         pw[g4] = p4.x; pw[g4 + 1] = p4.y; pw[g4 + 2] = p4.z; pw[g4 + 3] = p4.w;
       }
-      const uint4 v = vr[r];
+      const uint4 v = vs[r];
       const float vf[8] = {bf16lo(v.x), bf16hi(v.x), bf16lo(v.y), bf16hi(v.y),
                            bf16lo(v.z), bf16hi(v.z), bf16lo(v.w), bf16hi(v.w)};
 #pragma unroll
@@ -455,8 +432,46 @@ __device__ __forceinline__ void decode_wave_mfma(
 #pragma unroll
         for (int e = 0; e < 8; ++e) o[g][e] += pw[g] * vf[e];
     }
-    if (more) issue_v(b + T);
     wave_lds_sync();
+  };
+
+  // Software pipeline: stage s is computed while stages s+1 .. s+NS-1 load.
+  // Loads are issued unconditionally, with token indices clamped into the
+  // chunk (steps past the end re-read the last rows, which hit in cache), so
+  // no load sits under a branch and the compiler's wait counts stay exact:
+  // computing a stage waits only for that stage's loads.
+  const int nsteps = (end - start + 15) >> 4;
+  auto step_base = [&](int i) { return min(start + 16 * i, end - 1) & ~15; };
+#pragma unroll
+  for (int s = 0; s < NS - 1; ++s) issue(kr[s], vr[s], step_base(s));
+  uint32_t fold = 0;  // LOADS_ONLY measurement variant: consume the data trivially
+  int i = 0;
+  for (; i + NS <= nsteps; i += NS) {
+#pragma unroll
+    for (int s = 0; s < NS; ++s) {
+      issue(kr[(s + NS - 1) % NS], vr[(s + NS - 1) % NS], step_base(i + s + NS - 1));
+      if constexpr (!LOADS_ONLY) compute(kr[s], vr[s], start + 16 * (i + s));
+    }
+  }
+  for (; i < nsteps; i += NS) {
+#pragma unroll
+    for (int s = 0; s < NS; ++s) {
+      issue(kr[(s + NS - 1) % NS], vr[(s + NS - 1) % NS], step_base(i + s + NS - 1));
+      if (i + s < nsteps) {
+        if constexpr (LOADS_ONLY) {
+#pragma unroll
+          for (int c = 0; c < KCH; ++c) fold ^= kr[s][c].x ^ kr[s][c].y ^ kr[s][c].z ^ kr[s][c].w;
+#pragma unroll
+          for (int r = 0; r < RV; ++r) fold ^= vr[s][r].x ^ vr[s][r].y ^ vr[s][r].z ^ vr[s][r].w;
+        } else {
+          compute(kr[s], vr[s], start + 16 * (i + s));
+        }
+      }
+    }
+  }
+  if constexpr (LOADS_ONLY) {
+    if (fold == 0x9e3779b9u) out[0] = 0.f;
+    return;
   }
 
   // Row sums over the 16 token lanes; publish (m, l) per head through LDS.
@@ -501,7 +516,261 @@ __device__ __forceinline__ void decode_wave_mfma(
   }
 }
 
-template <int D, int G, int NT, bool BIG_BLOCKS>
+// Second-generation bf16 decode wave: both contractions on MFMA.
+//
+//   S = K . Q^T   (v_mfma_f32_16x16x32_bf16, A = K tile straight from HBM,
+//                  B = query group hi/lo; out lane l: token 4*(l/16)+i, head l%16)
+//   O^T = V^T . P^T (v_mfma_f32_16x16x16bf16_1k, K = the step's 16 tokens)
+//
+// The score layout of the first product is exactly the B-operand layout of
+// the second (lane l: head l%16, tokens 4*(l/16)..+4), so the softmax weights
+// never leave registers; they are split into hi + lo bf16 terms.  V arrives
+// row-major ([token][dim], one coalesced 16-byte load per lane), is written to
+// a padded per-wave LDS tile, and read back column-wise with ds_read_tr16_b64,
+// which hands lane i of each 16-lane group element (i%4) of the 8-byte chunk
+// addressed by lane 4r + i/4 as its r-th value.  Every per-head quantity (max,
+// rescale, sum, output) lives in the lanes l with l%16 = head.
+template <int D, int G, int NS, bool BIG_BLOCKS>
+__device__ __forceinline__ void decode_wave_mfma2(
+    const uint16_t* __restrict__ kv_layer, uint32_t blk_stride, uint32_t v_off,
+    uint32_t slot_stride, int bs_log2, int num_q_heads, const float* __restrict__ q,
+    const int32_t* __restrict__ row_seq, const int64_t* __restrict__ bt_off,
+    const uint32_t* __restrict__ bt_ids, int max_splits, float scale, float* __restrict__ out,
+    float* __restrict__ ws_o, float* __restrict__ ws_ml, uint16_t* VL, uint4* QL, int row, int kvh,
+    int start, int end, int split, int nsplit) {
+  constexpr int KCH = D / 32;     // K . Q^T MFMA k-steps
+  constexpr int DT = D / 16;      // output dim tiles of the P.V MFMA
+  constexpr int CH = D / 8;       // lanes per V row (16 bytes each)
+  constexpr int TPW = 64 / CH;    // V rows per wave load
+  constexpr int RV = 16 / TPW;    // V loads per lane per step
+  constexpr int VROW = D + 8;     // padded LDS row, in bf16 elements
+  static_assert(G <= 16 && TPW <= 16 && (16 % TPW) == 0, "unsupported shape");
+
+  const int lane = threadIdx.x & 63;
+  const int bs_mask = (1 << bs_log2) - 1;
+  const int l16 = lane & 15;  // token (K load) / head (scores, output)
+  const int grp = lane >> 4;  // 16-lane group
+
+  const int seq = row_seq[row];
+  const uint32_t* tbl = bt_ids + bt_off[seq];
+  const int first_blk = start >> bs_log2;
+  const int nblk = ((end - 1) >> bs_log2) - first_blk + 1;
+  const int my_blk = lane < nblk ? (int)tbl[first_blk + lane] : 0;
+
+  const uint16_t* base_k = kv_layer + (uint32_t)kvh * D;
+  const int kd = grp * 8;          // K dims chunk
+  const int vt = lane / CH;        // V row within a wave load
+  const int vc = lane % CH;        // V 16-byte chunk
+
+  auto issue = [&](uint4 (&ks)[KCH], uint4 (&vs)[RV], int b) {
+    const int jk = min(b + l16, end - 1);
+    if constexpr (BIG_BLOCKS) {
+      const int blk = __builtin_amdgcn_readlane(my_blk, (b >> bs_log2) - first_blk);
+      const uint16_t* bb = base_k + (uint32_t)blk * blk_stride;
+      const uint16_t* kp = bb + (uint32_t)(jk & bs_mask) * slot_stride + kd;
+#pragma unroll
+      for (int c = 0; c < KCH; ++c) ks[c] = *reinterpret_cast<const uint4*>(kp + 32 * c);
+#pragma unroll
+      for (int r = 0; r < RV; ++r) {
+        const int jv = min(b + r * TPW + vt, end - 1);
+        vs[r] = *reinterpret_cast<const uint4*>(bb + (uint32_t)(jv & bs_mask) * slot_stride +
+                                                v_off + vc * 8);
+      }
+    } else {
+      const int bk = __shfl(my_blk, (jk >> bs_log2) - first_blk);
+      const uint16_t* kp =
+          base_k + (uint32_t)bk * blk_stride + (uint32_t)(jk & bs_mask) * slot_stride + kd;
+#pragma unroll
+      for (int c = 0; c < KCH; ++c) ks[c] = *reinterpret_cast<const uint4*>(kp + 32 * c);
+#pragma unroll
+      for (int r = 0; r < RV; ++r) {
+        const int jv = min(b + r * TPW + vt, end - 1);
+        const int bv = __shfl(my_blk, (jv >> bs_log2) - first_blk);
+        vs[r] = *reinterpret_cast<const uint4*>(base_k + (uint32_t)bv * blk_stride +
+                                                (uint32_t)(jv & bs_mask) * slot_stride + v_off +
+                                                vc * 8);
+      }
+    }
+  };
+
+  // ---- query group as the B operand of S = K . Q^T (hi/lo bf16) ----
+  // Kept in a per-wave LDS tile (lane-major, conflict-free 16-byte reads)
+  // rather than in 32 VGPRs, which keeps the wave at 3 per SIMD.
+  typedef __attribute__((address_space(3))) uint4 lds_q4;
+  const uint32_t ql_base = (uint32_t)(uintptr_t)QL;
+  {
+    const float* qp = q + ((int64_t)row * num_q_heads + (int64_t)kvh * G + l16) * D + kd;
+#pragma unroll
+    for (int j = 0; j < KCH; ++j) {
+      float a[8];
+      if (l16 < G) {
+        const float4 x0 = *reinterpret_cast<const float4*>(qp + 32 * j);
+        const float4 x1 = *reinterpret_cast<const float4*>(qp + 32 * j + 4);
+        a[0] = x0.x; a[1] = x0.y; a[2] = x0.z; a[3] = x0.w;
+        a[4] = x1.x; a[5] = x1.y; a[6] = x1.z; a[7] = x1.w;
+      } else {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) a[e] = 0.f;
+      }
+      uint4 hv, lv;
+      split2_trunc(a[0], a[1], hv.x, lv.x);
+      split2_trunc(a[2], a[3], hv.y, lv.y);
+      split2_trunc(a[4], a[5], hv.z, lv.z);
+      split2_trunc(a[6], a[7], hv.w, lv.w);
+      QL[(2 * j) * 64 + lane] = hv;
+      QL[(2 * j + 1) * 64 + lane] = lv;
+    }
+  }
+  wave_lds_sync();
+  auto qb = [&](int j, int lo) -> bf16x8 {
+    uint4 v;
+    __builtin_memcpy(&v, (const void*)&QL[(2 * j + lo) * 64 + lane], 16);
+    return __builtin_bit_cast(bf16x8, v);
+  };
+
+  float m = -INFINITY, lsum = 0.f;  // for head l16 (replicated over the groups)
+  f32x4 o[DT];                      // O^T tile dt: dims 16dt + 4*grp + i, head l16
+#pragma unroll
+  for (int t = 0; t < DT; ++t) o[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  // LDS addresses: V row-major write (row vt + TPW*r, chunk vc) and the
+  // transposed read (lane 4r + q of a group addresses row 4*grp + r, dims
+  // 4q .. 4q+3 of the tile).
+  const uint32_t vl_base = (uint32_t)(uintptr_t)VL;
+  const uint32_t w_off = (uint32_t)(vt * VROW + vc * 8) * 2;
+  const uint32_t r_off = (uint32_t)((4 * grp + (l16 >> 2)) * VROW + 4 * (l16 & 3)) * 2;
+  typedef short v4s __attribute__((ext_vector_type(4)));
+  typedef __attribute__((address_space(3))) v4s lds_v4s;
+
+  // Softmax reference: m is a per-head value shared by the four lane groups.
+  // Weights are exp(s - m); m is raised (with an exact cross-group max and a
+  // rescale) only when some score exceeds it by more than kLazy, so weights
+  // stay <= e^kLazy and the cross-lane exchange is rare after the first step.
+  constexpr float kLazy = 8.0f;
+  typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+  typedef __attribute__((address_space(3))) u32x4 lds_u4;
+  auto compute = [&](const uint4 (&ks)[KCH], const uint4 (&vs)[RV], int b, int buf) {
+    // Stage V into LDS (row-major, padded rows).  One buffer per wave: its
+    // LDS operations execute in order, and the fence at the end of the step
+    // keeps the compiler from moving this write above the previous reads.
+    (void)buf;
+    const uint32_t wb = vl_base + w_off;
+#pragma unroll
+    for (int r = 0; r < RV; ++r)
+      *(lds_u4*)(uintptr_t)(wb + r * TPW * VROW * 2) = __builtin_bit_cast(u32x4, vs[r]);
+    // S = K . Q^T
+    f32x4 sh = {0.f, 0.f, 0.f, 0.f}, sl = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int c = 0; c < KCH; ++c) {
+      const bf16x8 ka = __builtin_bit_cast(bf16x8, ks[c]);
+      sh = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ka, qb(c, 0), sh, 0, 0, 0);
+      sl = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ka, qb(c, 1), sl, 0, 0, 0);
+    }
+    float s[4];
+    float mx = -INFINITY;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      s[i] = (b + 4 * grp + i < end) ? (sh[i] + sl[i]) * scale : -INFINITY;
+      mx = fmaxf(mx, s[i]);
+    }
+    if (__builtin_amdgcn_ballot_w64(mx > m + kLazy) != 0) {
+      mx = fmaxf(mx, __shfl_xor(mx, 16));
+      mx = fmaxf(mx, __shfl_xor(mx, 32));
+      const float m_new = fmaxf(m, mx);
+      const float alpha = __expf(m - m_new);
+      m = m_new;
+      lsum *= alpha;
+#pragma unroll
+      for (int t = 0; t < DT; ++t) o[t] *= alpha;
+    }
+    float pv[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) pv[i] = __expf(s[i] - m);
+    lsum += (pv[0] + pv[1]) + (pv[2] + pv[3]);
+    uint2 hi2, lo2;
+    split2_trunc(pv[0], pv[1], hi2.x, lo2.x);
+    split2_trunc(pv[2], pv[3], hi2.y, lo2.y);
+    const v4s pb_hi = __builtin_bit_cast(v4s, hi2);
+    const v4s pb_lo = __builtin_bit_cast(v4s, lo2);
+    wave_lds_sync();
+    // O^T += V^T . P^T
+    const uint32_t rb = vl_base + r_off;
+#pragma unroll
+    for (int t = 0; t < DT; ++t) {
+      const v4s va = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4s*)(uintptr_t)(rb + t * 32));
+      o[t] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(va, pb_hi, o[t], 0, 0, 0);
+      o[t] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(va, pb_lo, o[t], 0, 0, 0);
+    }
+    wave_lds_sync();
+  };
+
+  // Two register sets in ping-pong: step i computes on one set while the
+  // next step's loads land in the other.  Loads are unconditional (token
+  // indices clamped into the chunk), so the compiler's wait counts are exact,
+  // and a full pair of steps is one basic block, so one step's softmax and
+  // P.V overlap the next step's Q.K^T.  LDS buffer parity = step parity.
+  uint4 ka[KCH], va_[RV], kb[KCH], vb[RV];
+  const int nsteps = (end - start + 15) >> 4;
+  auto step_base = [&](int i) { return min(start + 16 * i, end - 1) & ~15; };
+  issue(ka, va_, step_base(0));
+  int i = 0;
+  for (; i + 2 <= nsteps; i += 2) {
+    issue(kb, vb, step_base(i + 1));
+    compute(ka, va_, start + 16 * i, 0);
+    issue(ka, va_, step_base(i + 2));
+    compute(kb, vb, start + 16 * (i + 1), 1);
+  }
+  if (i < nsteps) compute(ka, va_, start + 16 * i, 0);
+
+  lsum += __shfl_xor(lsum, 16);
+  lsum += __shfl_xor(lsum, 32);
+  if (l16 >= G) return;
+  const int64_t hidx = (int64_t)row * num_q_heads + (int64_t)kvh * G + l16;
+  if (nsplit == 1) {
+    const float inv = 1.f / lsum;
+    float* op = out + hidx * D + 4 * grp;
+#pragma unroll
+    for (int t = 0; t < DT; ++t)
+      *reinterpret_cast<float4*>(op + 16 * t) =
+          make_float4(o[t][0] * inv, o[t][1] * inv, o[t][2] * inv, o[t][3] * inv);
+  } else {
+    const int64_t slot = hidx * max_splits + split;
+    float* op = ws_o + slot * D + 4 * grp;
+#pragma unroll
+    for (int t = 0; t < DT; ++t)
+      *reinterpret_cast<float4*>(op + 16 * t) = make_float4(o[t][0], o[t][1], o[t][2], o[t][3]);
+    if (grp == 0) *reinterpret_cast<float2*>(ws_ml + slot * 2) = make_float2(m, lsum);
+  }
+}
+
+template <int D, int G, int NS, bool BIG_BLOCKS>
+__global__ void __launch_bounds__(256)
+    paged_decode_mfma2_kernel(const uint16_t* __restrict__ kv_layer, uint32_t blk_stride,
+                              uint32_t v_off, uint32_t slot_stride, int bs_log2, int num_kv_heads,
+                              int num_q_heads, const int2* __restrict__ work, int num_work,
+                              const float* __restrict__ q, const uint32_t* __restrict__ positions,
+                              const int32_t* __restrict__ row_seq,
+                              const int64_t* __restrict__ bt_off,
+                              const uint32_t* __restrict__ bt_ids, int chunk, int max_splits,
+                              float scale, float* __restrict__ out, float* __restrict__ ws_o,
+                              float* __restrict__ ws_ml) {
+  __shared__ __attribute__((aligned(16))) uint16_t lds_v[4][16 * (D + 8)];
+  __shared__ uint4 lds_q[4][2 * (D / 32) * 64];
+  const int wv = threadIdx.x >> 6;
+  const int w = blockIdx.x * 4 + wv;
+  if (w >= num_work) return;
+  const int2 wk = work[w];
+  const int row = wk.x / num_kv_heads, kvh = wk.x - row * num_kv_heads, start = wk.y;
+  const int len = (int)positions[row] + 1;
+  const int end = min(len, start + chunk);
+  const int nsplit = (len + chunk - 1) / chunk;
+  decode_wave_mfma2<D, G, NS, BIG_BLOCKS>(kv_layer, blk_stride, v_off, slot_stride, bs_log2,
+                                          num_q_heads, q, row_seq, bt_off, bt_ids, max_splits,
+                                          scale, out, ws_o, ws_ml, lds_v[wv], lds_q[wv], row, kvh, start, end,
+                                          start / chunk, nsplit);
+}
+
+template <int D, int G, int NS, bool BIG_BLOCKS, bool LOADS_ONLY = false>
 __global__ void __launch_bounds__(256)
     paged_decode_mfma_kernel(const uint16_t* __restrict__ kv_layer, uint32_t blk_stride,
                              uint32_t v_off, uint32_t slot_stride, int bs_log2, int num_kv_heads,
@@ -512,7 +781,7 @@ __global__ void __launch_bounds__(256)
                              int chunk, int max_splits, float scale, float* __restrict__ out,
                              float* __restrict__ ws_o, float* __restrict__ ws_ml) {
   constexpr int GP = (G + 3) & ~3;
-  __shared__ float lds_p[4][16 * NT * GP];
+  __shared__ float lds_p[4][16 * GP];
   __shared__ float lds_a[4][GP];
   __shared__ float lds_l[4][GP];
   const int wv = threadIdx.x >> 6;
@@ -523,7 +792,7 @@ __global__ void __launch_bounds__(256)
   const int len = (int)positions[row] + 1;
   const int end = min(len, start + chunk);
   const int nsplit = (len + chunk - 1) / chunk;
-  decode_wave_mfma<D, G, NT, BIG_BLOCKS>(kv_layer, blk_stride, v_off, slot_stride, bs_log2,
+  decode_wave_mfma<D, G, NS, BIG_BLOCKS, LOADS_ONLY>(kv_layer, blk_stride, v_off, slot_stride, bs_log2,
                                          num_q_heads, q, row_seq, bt_off, bt_ids, max_splits, scale,
                                          out, ws_o, ws_ml, lds_p[wv], lds_a[wv], lds_l[wv], row, kvh,
                                          start, end, start / chunk, nsplit);
@@ -689,7 +958,7 @@ static hipError_t launch_valu(int G, dim3 grid, dim3 block, hipStream_t st, cons
   return hipGetLastError();
 }
 
-template <int D, bool BIG, int NT>
+template <int D, bool BIG, int NS>
 static hipError_t launch_mfma(int G, dim3 grid, dim3 block, hipStream_t st, const uint16_t* kv,
                               uint32_t bstr, uint32_t voff, uint32_t sstr, int bsl, int hkv,
                               int hq, const int2* work, int nwork, const float* q,
@@ -698,7 +967,7 @@ static hipError_t launch_mfma(int G, dim3 grid, dim3 block, hipStream_t st, cons
                               int ms, float scale, float* out, float* wo, float* wml) {
 #define ORION_MFMA_CASE(GG)                                                                   \
   case GG:                                                                                    \
-    hipLaunchKernelGGL((paged_decode_mfma_kernel<D, GG, NT, BIG>), grid, block, 0, st, kv,    \
+    hipLaunchKernelGGL((paged_decode_mfma_kernel<D, GG, NS, BIG>), grid, block, 0, st, kv,    \
                        bstr, voff, sstr, bsl, hkv, hq, work, nwork, q, pos, rs, bo, bi, C, ms,  \
                        scale, out, wo, wml);                                                  \
     break;
@@ -715,6 +984,35 @@ static hipError_t launch_mfma(int G, dim3 grid, dim3 block, hipStream_t st, cons
       return hipErrorInvalidValue;
   }
 #undef ORION_MFMA_CASE
+  return hipGetLastError();
+}
+
+template <int D, bool BIG, int NS>
+static hipError_t launch_mfma2(int G, dim3 grid, dim3 block, hipStream_t st, const uint16_t* kv,
+                               uint32_t bstr, uint32_t voff, uint32_t sstr, int bsl, int hkv,
+                               int hq, const int2* work, int nwork, const float* q,
+                               const uint32_t* pos, const int32_t* rs, const int64_t* bo,
+                               const uint32_t* bi, int C, int ms, float scale, float* out,
+                               float* wo, float* wml) {
+#define ORION_MFMA2_CASE(GG)                                                                   \
+  case GG:                                                                                     \
+    hipLaunchKernelGGL((paged_decode_mfma2_kernel<D, GG, NS, BIG>), grid, block, 0, st, kv,    \
+                       bstr, voff, sstr, bsl, hkv, hq, work, nwork, q, pos, rs, bo, bi, C, ms,   \
+                       scale, out, wo, wml);                                                   \
+    break;
+  switch (G) {
+    ORION_MFMA2_CASE(1)
+    ORION_MFMA2_CASE(2)
+    ORION_MFMA2_CASE(3)
+    ORION_MFMA2_CASE(4)
+    ORION_MFMA2_CASE(5)
+    ORION_MFMA2_CASE(6)
+    ORION_MFMA2_CASE(7)
+    ORION_MFMA2_CASE(8)
+    default:
+      return hipErrorInvalidValue;
+  }
+#undef ORION_MFMA2_CASE
   return hipGetLastError();
 }
 
@@ -745,16 +1043,66 @@ hipError_t launch_paged_decode(hipStream_t st, const KvGeom& kv, const void* are
     if (layer_elems > (int64_t)UINT32_MAX) return hipErrorInvalidValue;
     const uint16_t* base = static_cast<const uint16_t*>(arena) + layer * layer_elems;
     const bool big = kv.block_size >= 16;
-#define ORION_MFMA(DD, BB)                                                                    \
-  launch_mfma<DD, BB, 2>(G, grid, block, st, base, (uint32_t)blk_stride, (uint32_t)v_off,    \
-                         (uint32_t)slot_stride, bs_log2, (int)hkv, (int)hq, plan.work, plan.num_work, q,    \
-                         positions, row_seq, bt_off, bt_ids, C, ms, scale, out, ws_o, ws_ml)
+  // ORION_DECODE_STAGES (2..4): register pipeline depth (measurement knob).
+  static const int stages = [] {
+    const char* e = getenv("ORION_DECODE_STAGES");
+    const int v = e ? atoi(e) : 3;
+    return (v >= 2 && v <= 4) ? v : 3;
+  }();
+#define ORION_MFMA_NS(DD, BB, NN)                                                             \
+  launch_mfma<DD, BB, NN>(G, grid, block, st, base, (uint32_t)blk_stride, (uint32_t)v_off,   \
+                          (uint32_t)slot_stride, bs_log2, (int)hkv, (int)hq, plan.work,      \
+                          plan.num_work, q, positions, row_seq, bt_off, bt_ids, C, ms, scale, \
+                          out, ws_o, ws_ml)
+#define ORION_MFMA(DD, BB)                                                                     \
+  (stages == 2 ? ORION_MFMA_NS(DD, BB, 2)                                                      \
+               : stages == 4 ? ORION_MFMA_NS(DD, BB, 4) : ORION_MFMA_NS(DD, BB, 3))
+    static const bool loads_only = getenv("ORION_DECODE_LOADS_ONLY") != nullptr;
+    static const bool gen1 = [] {
+      const char* e = getenv("ORION_DECODE_KERNEL");
+      return e && atoi(e) == 1;
+    }();
+    if (!gen1 && !loads_only) {
+#define ORION_MFMA2_NS(DD, BB, NN)                                                             \
+  launch_mfma2<DD, BB, NN>(G, grid, block, st, base, (uint32_t)blk_stride, (uint32_t)v_off,    \
+                           (uint32_t)slot_stride, bs_log2, (int)hkv, (int)hq, plan.work,      \
+                           plan.num_work, q, positions, row_seq, bt_off, bt_ids, C, ms, scale, \
+                           out, ws_o, ws_ml)
+#define ORION_MFMA2(DD, BB)                                                                     \
+  (stages == 2 ? ORION_MFMA2_NS(DD, BB, 2)                                                      \
+               : stages == 4 ? ORION_MFMA2_NS(DD, BB, 4) : ORION_MFMA2_NS(DD, BB, 3))
+      if (D == 128)
+        e = big ? ORION_MFMA2(128, true) : ORION_MFMA2(128, false);
+      else if (D == 64)
+        e = big ? ORION_MFMA2(64, true) : ORION_MFMA2(64, false);
+      else
+        return hipErrorInvalidValue;
+#undef ORION_MFMA2
+#undef ORION_MFMA2_NS
+      if (e != hipSuccess || ms == 1) return e;
+      dim3 cgrid((unsigned)((rows * hq + 3) / 4));
+      if (D == 128)
+        hipLaunchKernelGGL(paged_decode_combine_kernel<128>, cgrid, dim3(256), 0, st, (int)rows,
+                           (int)hq, positions, C, ms, ws_o, ws_ml, out);
+      else
+        hipLaunchKernelGGL(paged_decode_combine_kernel<64>, cgrid, dim3(256), 0, st, (int)rows,
+                           (int)hq, positions, C, ms, ws_o, ws_ml, out);
+      return hipGetLastError();
+    }
+    if (loads_only && D == 128 && G == 4 && big) {
+      hipLaunchKernelGGL((paged_decode_mfma_kernel<128, 4, 2, true, true>), grid, block, 0, st,
+                         base, (uint32_t)blk_stride, (uint32_t)v_off, (uint32_t)slot_stride,
+                         bs_log2, (int)hkv, (int)hq, plan.work, plan.num_work, q, positions,
+                         row_seq, bt_off, bt_ids, C, ms, scale, out, ws_o, ws_ml);
+      return hipGetLastError();
+    }
     if (D == 128)
       e = big ? ORION_MFMA(128, true) : ORION_MFMA(128, false);
     else if (D == 64)
       e = big ? ORION_MFMA(64, true) : ORION_MFMA(64, false);
     else
       return hipErrorInvalidValue;
+#undef ORION_MFMA_NS
 #undef ORION_MFMA
   } else {
     const float* base = static_cast<const float*>(arena) + layer * layer_elems;
