@@ -90,7 +90,8 @@ def main():
     dout = be.alloc(case.S * case.hq * case.d * 4)
     # The plan depends only on the batch's positions; a forward pass builds it
     # once and reuses it for every layer, so it is built outside the timed loop.
-    plan = oh.DecodePlan(be, case.positions, case.hq, case.hkv, case.d, case.bs)
+    plan = oh.DecodePlan(be, case.positions, case.row_seq, case.bt_offsets, case.bt_ids, case.hq,
+                         case.hkv, case.d, case.bs)
 
     def step():
         oh.paged_attention_decode(be, kv, arena.ptr, 0, dq.ptr, case.S, case.hq, dpos.ptr,

@@ -221,16 +221,19 @@ typedef struct orion_hip_kv_layout {
 } orion_hip_kv_layout;
 
 /* Work plan for paged decode attention over one batch of query rows.  Built
- * on the host from the rows' positions (host copy): each row's context is cut
- * into chunks and the (row, chunk) items are ordered longest first, which keeps
- * the chip evenly loaded on ragged batches.  A plan depends only on the
- * positions, so one plan serves every layer of a forward pass.  The plan also
- * owns the split-K workspace. */
+ * on the host from host copies of the rows' positions, their sequence index
+ * and the CSR block tables: each row's context is cut into chunks and the
+ * (row, kv head, chunk) items are ordered longest first, which keeps the chip
+ * evenly loaded on ragged batches; each item carries its table offset and first
+ * block id.  A plan depends only on the batch, so one plan serves every layer
+ * of a forward pass.  The plan also owns the split-K workspace.  Rows whose
+ * position has no block in their table are rejected (EngineError::Internal). */
 typedef struct orion_hip_decode_plan orion_hip_decode_plan;
 int orion_hip_decode_plan_create(orion_hip_device* dev, const uint32_t* positions,
-                                 int64_t num_rows, int64_t num_q_heads, int64_t num_kv_heads,
-                                 int64_t head_dim, int64_t block_size,
-                                 orion_hip_decode_plan** out);
+                                 const int32_t* row_seq, const int64_t* block_table_offsets,
+                                 const uint32_t* block_table_ids, int64_t num_rows,
+                                 int64_t num_q_heads, int64_t num_kv_heads, int64_t head_dim,
+                                 int64_t block_size, orion_hip_decode_plan** out);
 void orion_hip_decode_plan_destroy(orion_hip_decode_plan* plan);
 /* Chunk length in tokens, number of work items, chunks of the longest row. */
 int orion_hip_decode_plan_info(const orion_hip_decode_plan* plan, int64_t* chunk,

@@ -68,10 +68,9 @@ struct KvVec<uint16_t> {
 template <typename T, int D, int G>
 __device__ __forceinline__ void decode_wave_valu(
     const T* __restrict__ kv_layer, int64_t blk_stride, int64_t v_off, int64_t slot_stride,
-    int bs_log2, int num_q_heads, const float* __restrict__ q, const int32_t* __restrict__ row_seq,
-    const int64_t* __restrict__ bt_off, const uint32_t* __restrict__ bt_ids, int max_splits,
-    float scale, float* __restrict__ out, float* __restrict__ ws_o, float* __restrict__ ws_ml,
-    int row, int kvh, int start, int end, int split, int nsplit) {
+    int bs_log2, int num_q_heads, const float* __restrict__ q, const uint32_t* __restrict__ tbl,
+    int max_splits, float scale, float* __restrict__ out, float* __restrict__ ws_o,
+    float* __restrict__ ws_ml, int row, int kvh, int start, int end, int split, int nsplit) {
   constexpr int EPL = KvVec<T>::EPL;
   constexpr int CH = D / EPL;   // lanes per token vector
   constexpr int TPW = 64 / CH;  // tokens per wave load
@@ -101,12 +100,11 @@ __device__ __forceinline__ void decode_wave_valu(
     }
   }
 
-  // Block-table slice of this split, one entry per lane.
-  const int seq = row_seq[row];
-  const uint32_t* tbl = bt_ids + bt_off[seq];
+  // Block-table slice of this chunk (tbl points at its first entry), one
+  // entry per lane.
   const int first_blk = start >> bs_log2;
   const int nblk = ((end - 1) >> bs_log2) - first_blk + 1;
-  const int my_blk = lane < nblk ? (int)tbl[first_blk + lane] : 0;
+  const int my_blk = lane < nblk ? (int)tbl[lane] : 0;
 
   const T* kbase = kv_layer + (int64_t)kvh * D + c * EPL;
 
@@ -228,21 +226,18 @@ template <typename T, int D, int G>
 __global__ void __launch_bounds__(256)
     paged_decode_kernel(const T* __restrict__ kv_layer, int64_t blk_stride, int64_t v_off,
                         int64_t slot_stride, int bs_log2, int num_kv_heads, int num_q_heads,
-                        const int2* __restrict__ work, int num_work, const float* __restrict__ q,
+                        const DecodeWork* __restrict__ work, int num_work, const float* __restrict__ q,
                         const uint32_t* __restrict__ positions, const int32_t* __restrict__ row_seq,
                         const int64_t* __restrict__ bt_off, const uint32_t* __restrict__ bt_ids,
                         int chunk, int max_splits, float scale, float* __restrict__ out,
                         float* __restrict__ ws_o, float* __restrict__ ws_ml) {
   const int w = blockIdx.x * 4 + (threadIdx.x >> 6);
   if (w >= num_work) return;
-  const int2 wk = work[w];
-  const int row = wk.x / num_kv_heads, kvh = wk.x - row * num_kv_heads, start = wk.y;
-  const int len = (int)positions[row] + 1;
-  const int end = min(len, start + chunk);
-  const int nsplit = (len + chunk - 1) / chunk;
+  const DecodeWork wk = work[w];
+  const int row = wk.item / num_kv_heads, kvh = wk.item - row * num_kv_heads;
   decode_wave_valu<T, D, G>(kv_layer, blk_stride, v_off, slot_stride, bs_log2, num_q_heads, q,
-                            row_seq, bt_off, bt_ids, max_splits, scale, out, ws_o, ws_ml, row, kvh,
-                            start, end, start / chunk, nsplit);
+                            bt_ids + wk.tbl_off, max_splits, scale, out, ws_o, ws_ml, row, kvh,
+                            wk.start, wk.end, wk.start / chunk, wk.nsplit);
 }
 
 // bf16-KV decode kernel with Q.K^T on MFMA.
@@ -268,8 +263,7 @@ template <int D, int G, int NS, bool BIG_BLOCKS, bool LOADS_ONLY = false>
 __device__ __forceinline__ void decode_wave_mfma(
     const uint16_t* __restrict__ kv_layer, uint32_t blk_stride, uint32_t v_off,
     uint32_t slot_stride, int bs_log2, int num_q_heads, const float* __restrict__ q,
-    const int32_t* __restrict__ row_seq, const int64_t* __restrict__ bt_off,
-    const uint32_t* __restrict__ bt_ids, int max_splits, float scale, float* __restrict__ out,
+    const uint32_t* __restrict__ tbl, int max_splits, float scale, float* __restrict__ out,
     float* __restrict__ ws_o, float* __restrict__ ws_ml, float* P, float* A, float* Lr, int row,
     int kvh, int start, int end, int split, int nsplit) {
   constexpr int KCH = D / 32;       // MFMA k-steps over the head dim
@@ -283,11 +277,9 @@ __device__ __forceinline__ void decode_wave_mfma(
   const int bs_mask = (1 << bs_log2) - 1;
 
   // ---- block-table slice of this chunk, one entry per lane ----
-  const int seq = row_seq[row];
-  const uint32_t* tbl = bt_ids + bt_off[seq];
   const int first_blk = start >> bs_log2;
   const int nblk = ((end - 1) >> bs_log2) - first_blk + 1;
-  const int my_blk = lane < nblk ? (int)tbl[first_blk + lane] : 0;
+  const int my_blk = lane < nblk ? (int)tbl[lane] : 0;
 
   const uint16_t* base_k = kv_layer + (uint32_t)kvh * D;
   const int kt = lane & 15;        // K token within the step (MFMA column)
@@ -534,9 +526,9 @@ template <int D, int G, int NS, bool BIG_BLOCKS>
 __device__ __forceinline__ void decode_wave_mfma2(
     const uint16_t* __restrict__ kv_layer, uint32_t blk_stride, uint32_t v_off,
     uint32_t slot_stride, int bs_log2, int num_q_heads, const float* __restrict__ q,
-    const int32_t* __restrict__ row_seq, const int64_t* __restrict__ bt_off,
-    const uint32_t* __restrict__ bt_ids, int max_splits, float scale, float* __restrict__ out,
-    float* __restrict__ ws_o, float* __restrict__ ws_ml, uint16_t* VL, uint4* QL, int row, int kvh,
+    const uint32_t* __restrict__ tbl, int blk0, int max_splits, float scale,
+    float* __restrict__ out, float* __restrict__ ws_o, float* __restrict__ ws_ml, uint16_t* VL,
+    uint4* QL, int row, int kvh,
     int start, int end, int split, int nsplit) {
   constexpr int KCH = D / 32;     // K . Q^T MFMA k-steps
   constexpr int DT = D / 16;      // output dim tiles of the P.V MFMA
@@ -551,21 +543,23 @@ __device__ __forceinline__ void decode_wave_mfma2(
   const int l16 = lane & 15;  // token (K load) / head (scores, output)
   const int grp = lane >> 4;  // 16-lane group
 
-  const int seq = row_seq[row];
-  const uint32_t* tbl = bt_ids + bt_off[seq];
   const int first_blk = start >> bs_log2;
   const int nblk = ((end - 1) >> bs_log2) - first_blk + 1;
-  const int my_blk = lane < nblk ? (int)tbl[first_blk + lane] : 0;
+  const int my_blk = lane < nblk ? (int)tbl[lane] : 0;
 
   const uint16_t* base_k = kv_layer + (uint32_t)kvh * D;
   const int kd = grp * 8;          // K dims chunk
   const int vt = lane / CH;        // V row within a wave load
   const int vc = lane % CH;        // V 16-byte chunk
 
-  auto issue = [&](uint4 (&ks)[KCH], uint4 (&vs)[RV], int b) {
+  // blk_hint >= 0 supplies the step's block id directly (the first step uses
+  // the plan's copy, so its loads need not wait for the table slice).
+  auto issue = [&](uint4 (&ks)[KCH], uint4 (&vs)[RV], int b, int blk_hint) {
     const int jk = min(b + l16, end - 1);
     if constexpr (BIG_BLOCKS) {
-      const int blk = __builtin_amdgcn_readlane(my_blk, (b >> bs_log2) - first_blk);
+      const int blk = blk_hint >= 0
+                          ? blk_hint
+                          : __builtin_amdgcn_readlane(my_blk, (b >> bs_log2) - first_blk);
       const uint16_t* bb = base_k + (uint32_t)blk * blk_stride;
       const uint16_t* kp = bb + (uint32_t)(jk & bs_mask) * slot_stride + kd;
 #pragma unroll
@@ -712,12 +706,12 @@ __device__ __forceinline__ void decode_wave_mfma2(
   uint4 ka[KCH], va_[RV], kb[KCH], vb[RV];
   const int nsteps = (end - start + 15) >> 4;
   auto step_base = [&](int i) { return min(start + 16 * i, end - 1) & ~15; };
-  issue(ka, va_, step_base(0));
+  issue(ka, va_, step_base(0), BIG_BLOCKS ? blk0 : -1);
   int i = 0;
   for (; i + 2 <= nsteps; i += 2) {
-    issue(kb, vb, step_base(i + 1));
+    issue(kb, vb, step_base(i + 1), -1);
     compute(ka, va_, start + 16 * i, 0);
-    issue(ka, va_, step_base(i + 2));
+    issue(ka, va_, step_base(i + 2), -1);
     compute(kb, vb, start + 16 * (i + 1), 1);
   }
   if (i < nsteps) compute(ka, va_, start + 16 * i, 0);
@@ -747,7 +741,7 @@ template <int D, int G, int NS, bool BIG_BLOCKS>
 __global__ void __launch_bounds__(256)
     paged_decode_mfma2_kernel(const uint16_t* __restrict__ kv_layer, uint32_t blk_stride,
                               uint32_t v_off, uint32_t slot_stride, int bs_log2, int num_kv_heads,
-                              int num_q_heads, const int2* __restrict__ work, int num_work,
+                              int num_q_heads, const DecodeWork* __restrict__ work, int num_work,
                               const float* __restrict__ q, const uint32_t* __restrict__ positions,
                               const int32_t* __restrict__ row_seq,
                               const int64_t* __restrict__ bt_off,
@@ -759,22 +753,19 @@ __global__ void __launch_bounds__(256)
   const int wv = threadIdx.x >> 6;
   const int w = blockIdx.x * 4 + wv;
   if (w >= num_work) return;
-  const int2 wk = work[w];
-  const int row = wk.x / num_kv_heads, kvh = wk.x - row * num_kv_heads, start = wk.y;
-  const int len = (int)positions[row] + 1;
-  const int end = min(len, start + chunk);
-  const int nsplit = (len + chunk - 1) / chunk;
+  const DecodeWork wk = work[w];
+  const int row = wk.item / num_kv_heads, kvh = wk.item - row * num_kv_heads;
   decode_wave_mfma2<D, G, NS, BIG_BLOCKS>(kv_layer, blk_stride, v_off, slot_stride, bs_log2,
-                                          num_q_heads, q, row_seq, bt_off, bt_ids, max_splits,
-                                          scale, out, ws_o, ws_ml, lds_v[wv], lds_q[wv], row, kvh, start, end,
-                                          start / chunk, nsplit);
+                                          num_q_heads, q, bt_ids + wk.tbl_off, wk.blk0, max_splits,
+                                          scale, out, ws_o, ws_ml, lds_v[wv], lds_q[wv], row, kvh,
+                                          wk.start, wk.end, wk.start / chunk, wk.nsplit);
 }
 
 template <int D, int G, int NS, bool BIG_BLOCKS, bool LOADS_ONLY = false>
 __global__ void __launch_bounds__(256)
     paged_decode_mfma_kernel(const uint16_t* __restrict__ kv_layer, uint32_t blk_stride,
                              uint32_t v_off, uint32_t slot_stride, int bs_log2, int num_kv_heads,
-                             int num_q_heads, const int2* __restrict__ work, int num_work,
+                             int num_q_heads, const DecodeWork* __restrict__ work, int num_work,
                              const float* __restrict__ q, const uint32_t* __restrict__ positions,
                              const int32_t* __restrict__ row_seq,
                              const int64_t* __restrict__ bt_off, const uint32_t* __restrict__ bt_ids,
@@ -787,24 +778,26 @@ __global__ void __launch_bounds__(256)
   const int wv = threadIdx.x >> 6;
   const int w = blockIdx.x * 4 + wv;
   if (w >= num_work) return;
-  const int2 wk = work[w];
-  const int row = wk.x / num_kv_heads, kvh = wk.x - row * num_kv_heads, start = wk.y;
-  const int len = (int)positions[row] + 1;
-  const int end = min(len, start + chunk);
-  const int nsplit = (len + chunk - 1) / chunk;
-  decode_wave_mfma<D, G, NS, BIG_BLOCKS, LOADS_ONLY>(kv_layer, blk_stride, v_off, slot_stride, bs_log2,
-                                         num_q_heads, q, row_seq, bt_off, bt_ids, max_splits, scale,
-                                         out, ws_o, ws_ml, lds_p[wv], lds_a[wv], lds_l[wv], row, kvh,
-                                         start, end, start / chunk, nsplit);
+  const DecodeWork wk = work[w];
+  const int row = wk.item / num_kv_heads, kvh = wk.item - row * num_kv_heads;
+  decode_wave_mfma<D, G, NS, BIG_BLOCKS, LOADS_ONLY>(kv_layer, blk_stride, v_off, slot_stride,
+                                                     bs_log2, num_q_heads, q, bt_ids + wk.tbl_off,
+                                                     max_splits, scale, out, ws_o, ws_ml, lds_p[wv],
+                                                     lds_a[wv], lds_l[wv], row, kvh, wk.start,
+                                                     wk.end, wk.start / chunk, wk.nsplit);
 }
 
 // Merges the per-split states of rows whose context spans several splits.
-// One wave per (row, query head).
+// One wave per (row, query head).  Fast path (<= 64 splits): lane s holds
+// split s's (max, sum), and the first MAXS splits' partial outputs are loaded
+// before any reduction, so the merge costs one memory round trip.
 template <int D>
 __global__ void __launch_bounds__(256)
     paged_decode_combine_kernel(int num_rows, int num_q_heads, const uint32_t* __restrict__ positions,
                                 int partition, int max_splits, const float* __restrict__ ws_o,
                                 const float* __restrict__ ws_ml, float* __restrict__ out) {
+  constexpr int PER = D / 64;
+  constexpr int MAXS = 8;
   const int lane = threadIdx.x & 63;
   const int64_t item = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
   if (item >= (int64_t)num_rows * num_q_heads) return;
@@ -813,19 +806,46 @@ __global__ void __launch_bounds__(256)
   const int nsplit = (len + partition - 1) / partition;
   if (nsplit <= 1) return;
   const float* ml = ws_ml + item * max_splits * 2;
-  float mx = -INFINITY;
-  for (int s = 0; s < nsplit; ++s) mx = fmaxf(mx, ml[2 * s]);
-  float lsum = 0.f;
-  constexpr int PER = D / 64;
+  const float* ob = ws_o + item * max_splits * D;
   float acc[PER];
 #pragma unroll
   for (int i = 0; i < PER; ++i) acc[i] = 0.f;
-  for (int s = 0; s < nsplit; ++s) {
-    const float w = __expf(ml[2 * s] - mx);
-    lsum += w * ml[2 * s + 1];
-    const float* op = ws_o + (item * max_splits + s) * D;
+  float lsum;
+  if (nsplit <= 64) {
+    const float2 e = lane < nsplit ? *reinterpret_cast<const float2*>(ml + 2 * lane)
+                                   : make_float2(-INFINITY, 0.f);
+    float ov[MAXS][PER];
 #pragma unroll
-    for (int i = 0; i < PER; ++i) acc[i] += w * op[lane + 64 * i];
+    for (int j = 0; j < MAXS; ++j)
+#pragma unroll
+      for (int i = 0; i < PER; ++i)
+        ov[j][i] = j < nsplit ? ob[(int64_t)j * D + lane + 64 * i] : 0.f;
+    const float mx = wave_max(e.x);
+    const float w = lane < nsplit ? __expf(e.x - mx) : 0.f;
+    lsum = wave_sum(w * e.y);
+#pragma unroll
+    for (int j = 0; j < MAXS; ++j) {
+      const float wj = __shfl(w, j);
+#pragma unroll
+      for (int i = 0; i < PER; ++i) acc[i] += wj * ov[j][i];
+    }
+    for (int j = MAXS; j < nsplit; ++j) {
+      const float wj = __shfl(w, j);
+#pragma unroll
+      for (int i = 0; i < PER; ++i) acc[i] += wj * ob[(int64_t)j * D + lane + 64 * i];
+    }
+  } else {
+    float mx = -INFINITY;
+    for (int s = lane; s < nsplit; s += 64) mx = fmaxf(mx, ml[2 * s]);
+    mx = wave_max(mx);
+    float ls = 0.f;
+    for (int s = lane; s < nsplit; s += 64) ls += __expf(ml[2 * s] - mx) * ml[2 * s + 1];
+    lsum = wave_sum(ls);
+    for (int s = 0; s < nsplit; ++s) {
+      const float wj = __expf(ml[2 * s] - mx);
+#pragma unroll
+      for (int i = 0; i < PER; ++i) acc[i] += wj * ob[(int64_t)s * D + lane + 64 * i];
+    }
   }
   const float inv = 1.f / lsum;
 #pragma unroll
@@ -876,8 +896,11 @@ static int64_t simulate_makespan(const std::vector<int>& lens, int64_t hkv, int 
   return mx;
 }
 
-void build_decode_plan(const uint32_t* positions, int64_t rows, int64_t hkv, int64_t block_size,
-                       int64_t wave_slots, DecodePlanHost* plan) {
+void build_decode_plan(const uint32_t* positions, const int32_t* row_seq,
+                       const int64_t* bt_offsets, const uint32_t* bt_ids, int64_t rows,
+                       int64_t hkv, int64_t block_size, int64_t wave_slots, DecodePlanHost* plan) {
+  int bs_log2 = 0;
+  while ((1 << bs_log2) < block_size) ++bs_log2;
   std::vector<int> lens(rows);
   int max_len = 0;
   for (int64_t r = 0; r < rows; ++r) {
@@ -907,22 +930,25 @@ void build_decode_plan(const uint32_t* positions, int64_t rows, int64_t hkv, int
   plan->chunk = C;
   plan->max_splits = rows ? (max_len + C - 1) / C : 0;
   plan->work.clear();
+  auto push = [&](int64_t r, int start) {
+    const int len = lens[r];
+    const int64_t tbl_off = bt_offsets[row_seq[r]] + (start >> bs_log2);
+    const int nsplit = (len + C - 1) / C;
+    for (int64_t h = 0; h < hkv; ++h)
+      plan->work.push_back({(int32_t)(r * hkv + h), start, std::min(len, start + C), nsplit,
+                            (int32_t)tbl_off, (int32_t)bt_ids[tbl_off], 0, 0});
+  };
   std::vector<std::pair<int, int>> tails;  // (tail length, row)
   for (int64_t r = 0; r < rows; ++r) {
     const int full = lens[r] / C;
-    for (int s = 0; s < full; ++s)
-      for (int64_t h = 0; h < hkv; ++h)
-        plan->work.push_back({(int32_t)(r * hkv + h), (int32_t)(s * C)});
+    for (int s = 0; s < full; ++s) push(r, s * C);
     if (lens[r] % C) tails.push_back({lens[r] % C, (int)r});
   }
   std::stable_sort(tails.begin(), tails.end(),
                    [](const std::pair<int, int>& a, const std::pair<int, int>& b) {
                      return a.first > b.first;
                    });
-  for (const auto& t : tails)
-    for (int64_t h = 0; h < hkv; ++h)
-      plan->work.push_back(
-          {(int32_t)(t.second * hkv + h), (int32_t)((lens[t.second] / C) * C)});
+  for (const auto& t : tails) push(t.second, (lens[t.second] / C) * C);
 }
 
 size_t decode_workspace_bytes(int64_t rows, int64_t hq, int64_t D, int64_t max_splits) {
@@ -933,7 +959,7 @@ size_t decode_workspace_bytes(int64_t rows, int64_t hq, int64_t D, int64_t max_s
 template <typename T, int D>
 static hipError_t launch_valu(int G, dim3 grid, dim3 block, hipStream_t st, const T* kv,
                               int64_t bstr, int64_t voff, int64_t sstr, int bsl, int hkv, int hq,
-                              const int2* work, int nwork, const float* q, const uint32_t* pos,
+                              const DecodeWork* work, int nwork, const float* q, const uint32_t* pos,
                               const int32_t* rs, const int64_t* bo, const uint32_t* bi, int C,
                               int ms, float scale, float* out, float* wo, float* wml) {
 #define ORION_VALU_CASE(GG)                                                                   \
@@ -961,7 +987,7 @@ static hipError_t launch_valu(int G, dim3 grid, dim3 block, hipStream_t st, cons
 template <int D, bool BIG, int NS>
 static hipError_t launch_mfma(int G, dim3 grid, dim3 block, hipStream_t st, const uint16_t* kv,
                               uint32_t bstr, uint32_t voff, uint32_t sstr, int bsl, int hkv,
-                              int hq, const int2* work, int nwork, const float* q,
+                              int hq, const DecodeWork* work, int nwork, const float* q,
                               const uint32_t* pos,
                               const int32_t* rs, const int64_t* bo, const uint32_t* bi, int C,
                               int ms, float scale, float* out, float* wo, float* wml) {
@@ -990,7 +1016,7 @@ static hipError_t launch_mfma(int G, dim3 grid, dim3 block, hipStream_t st, cons
 template <int D, bool BIG, int NS>
 static hipError_t launch_mfma2(int G, dim3 grid, dim3 block, hipStream_t st, const uint16_t* kv,
                                uint32_t bstr, uint32_t voff, uint32_t sstr, int bsl, int hkv,
-                               int hq, const int2* work, int nwork, const float* q,
+                               int hq, const DecodeWork* work, int nwork, const float* q,
                                const uint32_t* pos, const int32_t* rs, const int64_t* bo,
                                const uint32_t* bi, int C, int ms, float scale, float* out,
                                float* wo, float* wml) {

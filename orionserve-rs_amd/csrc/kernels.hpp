@@ -16,24 +16,31 @@ struct KvGeom {
 };
 
 // ---- attention --------------------------------------------------------------
-// Decode work plan: (row * Hkv + kv_head, chunk start) items in longest-first
-// order; built on the host from the query positions, shared by every layer of
-// a forward.
+// One decode work item: KV head `item % Hkv` of query row `item / Hkv` over
+// context tokens [start, end).  The block table slice of the chunk starts at
+// block_table_ids[tbl_off]; blk0 is its first entry, so the first step's loads
+// can be issued before the slice arrives.
+struct DecodeWork {
+  int32_t item, start, end, nsplit, tbl_off, blk0, pad0, pad1;
+};
+// Decode work plan: items in longest-first order; built on the host from the
+// query positions and block tables, shared by every layer of a forward.
 struct DecodePlanHost {
   int chunk = 0;       // tokens per chunk (power of two)
   int max_splits = 0;  // chunks of the longest row
-  std::vector<int2> work;
+  std::vector<DecodeWork> work;
 };
 struct DecodePlanDev {
-  const int2* work = nullptr;
+  const DecodeWork* work = nullptr;
   int num_work = 0;
   int chunk = 0;
   int max_splits = 0;
   float* ws = nullptr;  // split-K partials, decode_workspace_bytes()
   size_t ws_bytes = 0;
 };
-void build_decode_plan(const uint32_t* positions, int64_t rows, int64_t hkv, int64_t block_size,
-                       int64_t wave_slots, DecodePlanHost* plan);
+void build_decode_plan(const uint32_t* positions, const int32_t* row_seq,
+                       const int64_t* bt_offsets, const uint32_t* bt_ids, int64_t rows,
+                       int64_t hkv, int64_t block_size, int64_t wave_slots, DecodePlanHost* plan);
 size_t decode_workspace_bytes(int64_t rows, int64_t hq, int64_t D, int64_t max_splits);
 hipError_t launch_paged_decode(hipStream_t st, const KvGeom& kv, const void* arena, int64_t layer,
                                const float* q, int64_t rows, int64_t hq,

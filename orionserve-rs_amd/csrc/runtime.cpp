@@ -154,7 +154,7 @@ struct orion_hip_decode_plan {
   }
   DecodePlanDev view() const {
     DecodePlanDev d;
-    d.work = work.as<const int2>();
+    d.work = work.as<const DecodeWork>();
     d.num_work = (int)host.work.size();
     d.chunk = host.chunk;
     d.max_splits = host.max_splits;
@@ -820,7 +820,8 @@ ORION_EXPORT int orion_hip_model_forward(orion_hip_model* m, const orion_hip_bat
   HIP_TRY(st, m->argmax.reserve(S * 8));
   // Decode plan (longest-first chunk list), shared by every layer.
   DecodePlanHost plan;
-  build_decode_plan(b->positions, n, d.num_kv_heads, d.block_size, m->dev->wave_slots, &plan);
+  build_decode_plan(b->positions, hb.row_seq.data(), b->block_table_offsets, b->block_table_ids, n,
+                    d.num_kv_heads, d.block_size, m->dev->wave_slots, &plan);
   HIP_TRY(st, m->ws.reserve(decode_workspace_bytes(n, Hq, d.head_dim, plan.max_splits)));
 
   // ---- upload the batch: one pinned staging area, one copy ----
@@ -830,8 +831,8 @@ ORION_EXPORT int orion_hip_model_forward(orion_hip_model* m, const orion_hip_bat
   const size_t o_last = o_rs + n * 4;
   const size_t o_btoff = (o_last + S * 4 + 7) & ~(size_t)7;
   const size_t o_btids = o_btoff + (S + 1) * 8;
-  const size_t o_work = (o_btids + nbt * 4 + 7) & ~(size_t)7;
-  const size_t total = o_work + plan.work.size() * sizeof(int2);
+  const size_t o_work = (o_btids + nbt * 4 + 31) & ~(size_t)31;
+  const size_t total = o_work + plan.work.size() * sizeof(DecodeWork);
   if (total > m->pinned_bytes) {
     if (m->pinned) {
       HIP_TRY(st, hipStreamSynchronize(stream));
@@ -851,7 +852,7 @@ ORION_EXPORT int orion_hip_model_forward(orion_hip_model* m, const orion_hip_bat
   std::memcpy(hp + o_last, hb.last_rows.data(), S * 4);
   std::memcpy(hp + o_btoff, b->block_table_offsets, (S + 1) * 8);
   std::memcpy(hp + o_btids, b->block_table_ids, nbt * 4);
-  std::memcpy(hp + o_work, plan.work.data(), plan.work.size() * sizeof(int2));
+  std::memcpy(hp + o_work, plan.work.data(), plan.work.size() * sizeof(DecodeWork));
   char* dp = m->b_tokens.as<char>();
   HIP_TRY(st, hipMemcpyAsync(dp, hp, total, hipMemcpyHostToDevice, stream));
   const uint32_t* d_tok = reinterpret_cast<const uint32_t*>(dp + o_tok);
@@ -861,7 +862,7 @@ ORION_EXPORT int orion_hip_model_forward(orion_hip_model* m, const orion_hip_bat
   const int64_t* d_btoff = reinterpret_cast<const int64_t*>(dp + o_btoff);
   const uint32_t* d_btids = reinterpret_cast<const uint32_t*>(dp + o_btids);
   DecodePlanDev dplan;
-  dplan.work = reinterpret_cast<const int2*>(dp + o_work);
+  dplan.work = reinterpret_cast<const DecodeWork*>(dp + o_work);
   dplan.num_work = (int)plan.work.size();
   dplan.chunk = plan.chunk;
   dplan.max_splits = plan.max_splits;
@@ -926,9 +927,12 @@ static int kv_geom_from(const orion_hip_kv_layout* kv, KvGeom* g, const char* st
 }
 
 ORION_EXPORT int orion_hip_decode_plan_create(orion_hip_device* dev, const uint32_t* positions,
-                                             int64_t num_rows, int64_t num_q_heads,
-                                             int64_t num_kv_heads, int64_t head_dim,
-                                             int64_t block_size, orion_hip_decode_plan** out) {
+                                             const int32_t* row_seq,
+                                             const int64_t* block_table_offsets,
+                                             const uint32_t* block_table_ids, int64_t num_rows,
+                                             int64_t num_q_heads, int64_t num_kv_heads,
+                                             int64_t head_dim, int64_t block_size,
+                                             orion_hip_decode_plan** out) {
   const char* st = "decode_plan";
   *out = nullptr;
   if (num_rows < 0 || num_kv_heads <= 0 || num_q_heads % num_kv_heads || head_dim <= 0 ||
@@ -942,8 +946,16 @@ ORION_EXPORT int orion_hip_decode_plan_create(orion_hip_device* dev, const uint3
   p->hkv = num_kv_heads;
   p->head_dim = head_dim;
   p->block_size = block_size;
-  build_decode_plan(positions, num_rows, num_kv_heads, block_size, dev->wave_slots, &p->host);
-  const size_t wbytes = p->host.work.size() * sizeof(int2);
+  for (int64_t i = 0; i < num_rows; ++i) {
+    const int64_t s = row_seq[i];
+    const int64_t tl = block_table_offsets[s + 1] - block_table_offsets[s];
+    if (s < 0 || (int64_t)positions[i] / block_size >= tl)
+      return internal(st, "row %lld: position %u has no block in its table", (long long)i,
+                      positions[i]);
+  }
+  build_decode_plan(positions, row_seq, block_table_offsets, block_table_ids, num_rows,
+                    num_kv_heads, block_size, dev->wave_slots, &p->host);
+  const size_t wbytes = p->host.work.size() * sizeof(DecodeWork);
   HIP_TRY(st, p->work.reserve(wbytes));
   if (wbytes)
     HIP_TRY(st, hipMemcpyAsync(p->work.ptr, p->host.work.data(), wbytes, hipMemcpyHostToDevice,

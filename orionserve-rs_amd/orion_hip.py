@@ -139,7 +139,8 @@ def load_library(path: str = LIB_PATH) -> C.CDLL:
         "orion_hip_model_kv_read": ([vp, i64, u32, i64, i64, C.c_int, vp], C.c_int),
         "orion_hip_model_kv_write": ([vp, i64, u32, i64, i64, C.c_int, vp, i64], C.c_int),
         "orion_hip_model_kv_arena": ([vp, P(vp), P(sz)], C.c_int),
-        "orion_hip_decode_plan_create": ([vp, vp, i64, i64, i64, i64, i64, P(vp)], C.c_int),
+        "orion_hip_decode_plan_create": ([vp, vp, vp, vp, vp, i64, i64, i64, i64, i64, P(vp)],
+                                         C.c_int),
         "orion_hip_decode_plan_destroy": ([vp], None),
         "orion_hip_decode_plan_info": ([vp, P(i64), P(i64), P(i64)], C.c_int),
         "orion_hip_paged_attention_decode": (
@@ -492,11 +493,15 @@ class DecodePlan:
     """orion_hip_decode_plan: the longest-first (row, chunk) work list for one
     batch of decode rows, built from the rows' positions (host copy)."""
 
-    def __init__(self, be: HipBackend, positions, num_q_heads: int, num_kv_heads: int,
-                 head_dim: int, block_size: int):
+    def __init__(self, be: HipBackend, positions, row_seq, bt_offsets, bt_ids, num_q_heads: int,
+                 num_kv_heads: int, head_dim: int, block_size: int):
         pos = np.ascontiguousarray(positions, dtype=np.uint32)
+        rs = np.ascontiguousarray(row_seq, dtype=np.int32)
+        bo = np.ascontiguousarray(bt_offsets, dtype=np.int64)
+        bi = np.ascontiguousarray(bt_ids, dtype=np.uint32)
         h = C.c_void_p()
-        _check(be.lib.orion_hip_decode_plan_create(be.handle, pos.ctypes.data, pos.size,
+        _check(be.lib.orion_hip_decode_plan_create(be.handle, pos.ctypes.data, rs.ctypes.data,
+                                                   bo.ctypes.data, bi.ctypes.data, pos.size,
                                                    num_q_heads, num_kv_heads, head_dim,
                                                    block_size, C.byref(h)))
         self.be = be

@@ -23,7 +23,8 @@ def run_decode(be, case, positions=None, row_seq=None, q=None):
     arena, dq, dpos, drs, dbo, dbi, dout = bufs
     print(f"[decode] rows={rows} hq={case.hq} hkv={case.hkv} d={case.d} bs={case.bs} "
           f"dtype={case.dtype} maxpos={int(positions.max())}", flush=True)
-    plan = oh.DecodePlan(be, positions, case.hq, case.hkv, case.d, case.bs)
+    plan = oh.DecodePlan(be, positions, row_seq, case.bt_offsets, case.bt_ids, case.hq, case.hkv,
+                         case.d, case.bs)
     oh.paged_attention_decode(be, kv, arena.ptr, 0, dq.ptr, rows, case.hq, dpos.ptr, drs.ptr,
                               dbo.ptr, dbi.ptr, plan, dout.ptr)
     out = dout.download(np.float32, (rows, case.hq * case.d))
