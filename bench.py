@@ -63,12 +63,126 @@ def cpu_baseline(case, seconds_budget=30.0):
     }
 
 
+TINYLLAMA = dict(L=22, H=2048, hq=32, hkv=4, d=64, F=5632, V=32000, eps=1e-5, theta=10000.0,
+                 max_pos=2048)
+
+
+def decode_e2e(steps=64, seqs=32, seed=20261204, cpu=True):
+    """full decode step of a random-init TinyLlama-1.1B-shape
+    model (bf16 weights N(0, 0.02), bf16 KV cache), 32 sequences with prompt
+    lengths U[16, 1024] (random token ids), prefilled in one forward, then
+    `steps` greedy decode steps (device argmax).  Returns a dict of results."""
+    import orion_hip as oh
+
+    cfg = TINYLLAMA
+    rng = np.random.default_rng(seed)
+    lens = rng.integers(16, 1025, size=seqs)
+    bs = 16
+    need = [-(-int(n + steps) // bs) for n in lens]
+    num_blocks = int(sum(need) * 1.1) + 8
+    perm = rng.permutation(num_blocks)
+    tables, cur = [], 0
+    for nb in need:
+        tables.append(perm[cur:cur + nb].tolist())
+        cur += nb
+    meta = oh.ModelMetadata(hidden_size=cfg["H"], num_layers=cfg["L"],
+                            num_attention_heads=cfg["hq"], num_kv_heads=cfg["hkv"],
+                            head_dim=cfg["d"], vocab_size=cfg["V"], intermediate_size=cfg["F"],
+                            max_position_embeddings=cfg["max_pos"], rope_theta=cfg["theta"],
+                            rms_norm_eps=cfg["eps"])
+    be = oh.HipBackend(0)
+    model = oh.HipTransformerModel(meta, num_blocks, bs, be, oh.BF16)
+    model.init_synthetic(seed, 0.02)
+    prompts = [rng.integers(0, cfg["V"], size=int(n)).tolist() for n in lens]
+    toks = [t for p in prompts for t in p]
+    pos = [i for n in lens for i in range(int(n))]
+    t0 = time.perf_counter()
+    out = model.forward(oh.ForwardBatch(toks, pos, list(range(seqs)), [int(n) for n in lens],
+                                        [int(n) for n in lens], tables, True),
+                        want_logits=False, want_argmax=True)
+    be.synchronize()
+    prefill_s = time.perf_counter() - t0
+    last = out.argmax.tolist()
+    ctx = [int(n) for n in lens]
+
+    def step():
+        nonlocal last
+        b = oh.ForwardBatch(last, ctx, list(range(seqs)), [1] * seqs, [c + 1 for c in ctx],
+                            tables, False)
+        o = model.forward(b, want_logits=False, want_argmax=True)
+        last = o.argmax.tolist()
+        for i in range(seqs):
+            ctx[i] += 1
+
+    for _ in range(2):  # warm-up steps (they also extend the sequences)
+        step()
+    be.synchronize()
+    n_steps = steps - 2
+    t0 = time.perf_counter()
+    for _ in range(n_steps):
+        step()
+    be.synchronize()
+    dt = time.perf_counter() - t0
+    res = {
+        "decode_tokens_per_s": round(seqs * n_steps / dt, 1),
+        "decode_ms_per_step": round(dt / n_steps * 1e3, 4),
+        "prefill_tokens": int(sum(lens)),
+        "prefill_s": round(prefill_s, 3),
+        "workload": "TinyLlama-1.1B shape (22L, hidden 2048, 32q/4kv, d 64, ffn 5632, vocab "
+                    "32000), bf16 weights N(0,0.02) synthetic, bf16 KV, 32 seqs, prompts "
+                    "U[16,1024], greedy decode",
+        "weight_bytes_per_step": int((22 * (2048 * (2048 + 512) + 2048 * 2048 + 3 * 2048 * 5632)
+                                      + 32000 * 2048) * 2),
+    }
+    model.close()
+    be.close()
+    if cpu:
+        res["cpu_baseline"] = cpu_decode_step(cfg, lens, tables, num_blocks, seqs)
+        res["speedup_vs_cpu"] = round(res["decode_tokens_per_s"] / res["cpu_baseline"]["value"], 1)
+    return res
+
+
+def cpu_decode_step(cfg, lens, tables, num_blocks, seqs):
+    """The oracle (C++ restatement of the reference CPU TransformerModel) on one
+    decode step of the same shapes.  Weights are a constant (the oracle's
+    scalar loops take the same time for any finite values); the KV arena holds
+    whatever it holds (timing does not depend on it)."""
+    import oracle as orc
+
+    threads = min(16, os.cpu_count() or 1)
+    orc.set_num_threads(threads)
+    m = orc.OracleTransformer(cfg["L"], cfg["H"], cfg["hq"], cfg["hkv"], cfg["d"], cfg["F"],
+                              cfg["V"], cfg["max_pos"], cfg["eps"], cfg["theta"], False, False,
+                              num_blocks, 16)
+    H, F, V = cfg["H"], cfg["F"], cfg["V"]
+    qd, kvd = cfg["hq"] * cfg["d"], cfg["hkv"] * cfg["d"]
+    c = lambda n: np.full(n, 0.01, np.float32)
+    m.set_weight(orc.W_EMBED, -1, c(V * H))
+    m.set_weight(orc.W_LM_HEAD, -1, c(V * H))
+    m.set_weight(orc.W_FINAL_NORM, -1, np.ones(H, np.float32))
+    for l in range(cfg["L"]):
+        for wid, n in [(orc.W_INPUT_NORM, H), (orc.W_POST_NORM, H)]:
+            m.set_weight(wid, l, np.ones(n, np.float32))
+        for wid, n in [(orc.W_Q, qd * H), (orc.W_K, kvd * H), (orc.W_V, kvd * H), (orc.W_O, H * qd),
+                       (orc.W_GATE, F * H), (orc.W_UP, F * H), (orc.W_DOWN, H * F)]:
+            m.set_weight(wid, l, c(n))
+    pos = [int(n) for n in lens]
+    t0 = time.perf_counter()
+    m.forward([1] * seqs, pos, [1] * seqs, [p + 1 for p in pos], tables)
+    dt = time.perf_counter() - t0
+    m.close()
+    return {"value": round(seqs / dt, 3), "unit": "tokens/s", "cores": threads, "kind": "port",
+            "sample": f"one decode step of the same model shape and batch ({seqs} rows), "
+                      f"{dt:.2f} s/step, constant weights, OpenMP over independent outputs"}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU oracle baseline")
+    ap.add_argument("--no-e2e", action="store_true", help="skip the config-4 decode step")
     a = ap.parse_args()
     if a.gpus != 1:
         print(f"bench.py measures one GPU only (this build is single-GPU); --gpus {a.gpus} "
@@ -152,6 +266,8 @@ def main():
     if not a.no_cpu:
         result["cpu_baseline"] = cpu_baseline(case)
     be.close()
+    if not a.no_e2e:
+        result["decode_e2e"] = decode_e2e(cpu=not a.no_cpu)
     print(json.dumps(result))
 
 

@@ -6,58 +6,60 @@
 // one output column with one 16-byte load, straight from HBM into registers.
 //
 // Activations arrive in f32.  Each 8-element A fragment is split on the fly
-// into hi = bf16(x) and lo = bf16(x - hi) and both are multiplied against the
-// bf16 weight (two MFMAs, f32 accumulation), so the product carries ~16
-// mantissa bits of x instead of 8.  Weights are exact (bf16 checkpoints widen
-// exactly in the reference loader), so the only departure from the reference's
-// f32 arithmetic is summation order plus a ~2^-17 relative term per product.
+// into hi = the top 16 bits of x and lo = the top 16 bits of (x - hi) and both
+// are multiplied against the bf16 weight (two MFMAs, f32 accumulation), so the
+// product carries ~16 mantissa bits of x instead of 8.  Weights are exact
+// (bf16 checkpoints widen exactly in the reference loader), so the only
+// departure from the reference's f32 arithmetic is summation order plus a
+// ~2^-16 relative term per product.
 //
-// Shape of the launch (decode-oriented, weight-streaming):
-//   workgroup = 4 waves, tile = 64 rows x (16*NT) columns, the four waves
-//   split K into contiguous quarters and reduce through LDS.  Every weight
-//   element is read from HBM once per 64-row block of x.  The epilogue fuses
-//   the bias add, the residual accumulate (transformer.rs:328-332, :345) or
-//   SwiGLU (tensor.rs:175-189) on gate/up rows interleaved in groups of 8.
+// The epilogue fuses the bias add, the residual accumulate
+// (transformer.rs:328-332, :345) or SwiGLU (tensor.rs:175-189) on gate/up rows
+// interleaved in groups of 8.
 #include "common.hpp"
 #include "kernels.hpp"
+
+#include <algorithm>
 
 namespace orion {
 
 __device__ inline bf16x8 as_bf16x8(uint4 v) { return __builtin_bit_cast(bf16x8, v); }
 
+// x -> (hi, lo) bf16 fragments by truncation (x = hi + lo to ~2^-16 relative).
 __device__ inline void split8(const float (&a)[8], bf16x8& hi, bf16x8& lo) {
-  uint16_t h[8], l[8];
-#pragma unroll
-  for (int i = 0; i < 8; ++i) split_bf16(a[i], h[i], l[i]);
   uint4 hv, lv;
-  hv.x = h[0] | ((uint32_t)h[1] << 16);
-  hv.y = h[2] | ((uint32_t)h[3] << 16);
-  hv.z = h[4] | ((uint32_t)h[5] << 16);
-  hv.w = h[6] | ((uint32_t)h[7] << 16);
-  lv.x = l[0] | ((uint32_t)l[1] << 16);
-  lv.y = l[2] | ((uint32_t)l[3] << 16);
-  lv.z = l[4] | ((uint32_t)l[5] << 16);
-  lv.w = l[6] | ((uint32_t)l[7] << 16);
+  split2_trunc(a[0], a[1], hv.x, lv.x);
+  split2_trunc(a[2], a[3], hv.y, lv.y);
+  split2_trunc(a[4], a[5], hv.z, lv.z);
+  split2_trunc(a[6], a[7], hv.w, lv.w);
   hi = as_bf16x8(hv);
   lo = as_bf16x8(lv);
 }
 
-template <int NT>
-__global__ void __launch_bounds__(256)
+// Decode-shaped (small M) weight-streaming GEMM.  Workgroup = KW waves on one
+// 16*NT-column tile of up to 16*MT rows; the waves split K into KW contiguous
+// ranges and each walks its range UNR k-steps (32 k each) at a time, so UNR
+// weight loads per column tile are in flight before the MFMAs consume them.
+// Each x fragment (loaded from L2) feeds NT column tiles.  The KW partial
+// tiles are summed through LDS in wave order (deterministic) and the epilogue
+// is applied once.  Weights are read from HBM exactly once per 16*MT rows.
+template <int MT, int NT, int KW, int UNR>
+__global__ void __launch_bounds__(64 * KW)
     gemm_skinny_kernel(const float* __restrict__ x, const uint16_t* __restrict__ w,
                        const float* __restrict__ bias, int M, int N, int K, int ep,
                        float* __restrict__ out) {
   constexpr int BN = 16 * NT;
-  __shared__ float red[4][64][BN + 1];
+  constexpr int BM = 16 * MT;
+  __shared__ float red[KW][BM][BN + 1];
 
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
-  const int m0 = blockIdx.y * 64;
+  const int m0 = blockIdx.y * BM;
   const int n0 = blockIdx.x * BN;
-  const int mt_count = min(4, (M - m0 + 15) >> 4);
+  const int mt_count = min(MT, (M - m0 + 15) >> 4);
   const int ksteps = K >> 5;
-  const int ks0 = wave * ksteps / 4;
-  const int ks1 = (wave + 1) * ksteps / 4;
+  const int ks0 = wave * ksteps / KW;
+  const int ks1 = (wave + 1) * ksteps / KW;
   const int lr = lane & 15;
   const int lk = (lane >> 4) * 8;
 
@@ -67,45 +69,61 @@ __global__ void __launch_bounds__(256)
     const int n = min(n0 + nt * 16 + lr, N - 1);
     wrow[nt] = w + (int64_t)n * K + lk;
   }
-  const float* xrow[4];
-  bool xvalid[4];
+  const float* xrow[MT];
+  bool xvalid[MT];
 #pragma unroll
-  for (int mt = 0; mt < 4; ++mt) {
+  for (int mt = 0; mt < MT; ++mt) {
     const int m = m0 + mt * 16 + lr;
     xvalid[mt] = m < M;
     xrow[mt] = x + (int64_t)min(m, M - 1) * K + lk;
   }
 
-  f32x4 acc[4][NT];
+  f32x4 acc[MT][NT];
 #pragma unroll
-  for (int mt = 0; mt < 4; ++mt)
+  for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
     for (int nt = 0; nt < NT; ++nt) acc[mt][nt] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-  for (int ks = ks0; ks < ks1; ++ks) {
-    const int k = ks << 5;
-    bf16x8 b[NT];
+  for (int ks = ks0; ks < ks1; ks += UNR) {
+    // Fragments for UNR k-steps (indices clamped into the range; the
+    // products of a clamped step are skipped below).
+    bf16x8 b[UNR][NT];
+    float4 a0[UNR][MT], a1[UNR][MT];
 #pragma unroll
-    for (int nt = 0; nt < NT; ++nt) b[nt] = as_bf16x8(*reinterpret_cast<const uint4*>(wrow[nt] + k));
+    for (int u = 0; u < UNR; ++u) {
+      const int k = min(ks + u, ks1 - 1) << 5;
 #pragma unroll
-    for (int mt = 0; mt < 4; ++mt) {
-      if (mt < mt_count) {
-        float a[8];
-        if (xvalid[mt]) {
-          const float4 a0 = *reinterpret_cast<const float4*>(xrow[mt] + k);
-          const float4 a1 = *reinterpret_cast<const float4*>(xrow[mt] + k + 4);
-          a[0] = a0.x; a[1] = a0.y; a[2] = a0.z; a[3] = a0.w;
-          a[4] = a1.x; a[5] = a1.y; a[6] = a1.z; a[7] = a1.w;
+      for (int nt = 0; nt < NT; ++nt)
+        b[u][nt] = as_bf16x8(*reinterpret_cast<const uint4*>(wrow[nt] + k));
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) {
+        if (mt < mt_count && xvalid[mt]) {
+          a0[u][mt] = *reinterpret_cast<const float4*>(xrow[mt] + k);
+          a1[u][mt] = *reinterpret_cast<const float4*>(xrow[mt] + k + 4);
         } else {
-#pragma unroll
-          for (int i = 0; i < 8; ++i) a[i] = 0.f;
+          a0[u][mt] = make_float4(0.f, 0.f, 0.f, 0.f);
+          a1[u][mt] = a0[u][mt];
         }
-        bf16x8 ahi, alo;
-        split8(a, ahi, alo);
+      }
+    }
 #pragma unroll
-        for (int nt = 0; nt < NT; ++nt) {
-          acc[mt][nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ahi, b[nt], acc[mt][nt], 0, 0, 0);
-          acc[mt][nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(alo, b[nt], acc[mt][nt], 0, 0, 0);
+    for (int u = 0; u < UNR; ++u) {
+      if (ks + u < ks1) {
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) {
+          if (mt < mt_count) {
+            const float a[8] = {a0[u][mt].x, a0[u][mt].y, a0[u][mt].z, a0[u][mt].w,
+                                a1[u][mt].x, a1[u][mt].y, a1[u][mt].z, a1[u][mt].w};
+            bf16x8 ahi, alo;
+            split8(a, ahi, alo);
+#pragma unroll
+            for (int nt = 0; nt < NT; ++nt) {
+              acc[mt][nt] =
+                  __builtin_amdgcn_mfma_f32_16x16x32_bf16(ahi, b[u][nt], acc[mt][nt], 0, 0, 0);
+              acc[mt][nt] =
+                  __builtin_amdgcn_mfma_f32_16x16x32_bf16(alo, b[u][nt], acc[mt][nt], 0, 0, 0);
+            }
+          }
         }
       }
     }
@@ -113,21 +131,22 @@ __global__ void __launch_bounds__(256)
 
   // C fragment layout: lane holds rows 4*(lane/16) + i, column lane % 16.
 #pragma unroll
-  for (int mt = 0; mt < 4; ++mt) {
+  for (int mt = 0; mt < MT; ++mt) {
     if (mt < mt_count) {
 #pragma unroll
       for (int nt = 0; nt < NT; ++nt)
 #pragma unroll
-        for (int i = 0; i < 4; ++i) red[wave][mt * 16 + (lane >> 4) * 4 + i][nt * 16 + lr] = acc[mt][nt][i];
+        for (int i = 0; i < 4; ++i)
+          red[wave][mt * 16 + (lane >> 4) * 4 + i][nt * 16 + lr] = acc[mt][nt][i];
     }
   }
   __syncthreads();
 
-  const int rows = min(64, M - m0);
+  const int rows = min(BM, M - m0);
   if (ep == (int)Epilogue::kSwiGLU) {
     // Tile columns nt*16 + [0,8) are gate rows, nt*16 + [8,16) the matching up rows.
     const int half_n = N >> 1;
-    for (int idx = threadIdx.x; idx < rows * NT * 8; idx += 256) {
+    for (int idx = threadIdx.x; idx < rows * NT * 8; idx += 64 * KW) {
       const int r = idx / (NT * 8);
       const int cc = idx - r * (NT * 8);
       const int nt = cc >> 3, j = cc & 7;
@@ -135,7 +154,7 @@ __global__ void __launch_bounds__(256)
       if (gcol >= N) continue;
       float g = 0.f, u = 0.f;
 #pragma unroll
-      for (int wv = 0; wv < 4; ++wv) {
+      for (int wv = 0; wv < KW; ++wv) {
         g += red[wv][r][nt * 16 + j];
         u += red[wv][r][nt * 16 + 8 + j];
       }
@@ -143,12 +162,14 @@ __global__ void __launch_bounds__(256)
       out[(int64_t)(m0 + r) * half_n + (n0 >> 1) + nt * 8 + j] = act;
     }
   } else {
-    for (int idx = threadIdx.x; idx < rows * BN; idx += 256) {
+    for (int idx = threadIdx.x; idx < rows * BN; idx += 64 * KW) {
       const int r = idx / BN;
       const int cc = idx - r * BN;
       const int col = n0 + cc;
       if (col >= N) continue;
-      float v = red[0][r][cc] + red[1][r][cc] + red[2][r][cc] + red[3][r][cc];
+      float v = 0.f;
+#pragma unroll
+      for (int wv = 0; wv < KW; ++wv) v += red[wv][r][cc];
       float* op = out + (int64_t)(m0 + r) * N + col;
       if (ep == (int)Epilogue::kAccumulate)
         *op += v;
@@ -158,29 +179,61 @@ __global__ void __launch_bounds__(256)
   }
 }
 
+template <int MT, int NT, int UNR>
+static void launch_skinny(int KW, dim3 grid, hipStream_t st, const float* x, const uint16_t* w,
+                          const float* bias, int M, int N, int K, int ep, float* out) {
+  switch (KW) {
+    case 16:
+      hipLaunchKernelGGL((gemm_skinny_kernel<MT, NT, 16, UNR>), grid, dim3(1024), 0, st, x, w,
+                         bias, M, N, K, ep, out);
+      break;
+    case 8:
+      hipLaunchKernelGGL((gemm_skinny_kernel<MT, NT, 8, UNR>), grid, dim3(512), 0, st, x, w,
+                         bias, M, N, K, ep, out);
+      break;
+    case 4:
+      hipLaunchKernelGGL((gemm_skinny_kernel<MT, NT, 4, UNR>), grid, dim3(256), 0, st, x, w,
+                         bias, M, N, K, ep, out);
+      break;
+    default:
+      hipLaunchKernelGGL((gemm_skinny_kernel<MT, NT, 1, UNR>), grid, dim3(64), 0, st, x, w,
+                         bias, M, N, K, ep, out);
+      break;
+  }
+}
+
 hipError_t launch_gemm(hipStream_t st, const float* x, const uint16_t* w, const float* bias,
                        int64_t M, int64_t N, int64_t K, Epilogue ep, float* out) {
   if (M == 0 || N == 0) return hipSuccess;
   if (K % 32 != 0 || K == 0) return hipErrorInvalidValue;
   if (ep == Epilogue::kSwiGLU && N % 16 != 0) return hipErrorInvalidValue;
-  int NT = 1;
-  if (N / 64 >= 512) NT = 4;
-  else if (N / 32 >= 512) NT = 2;
-  const int BN = 16 * NT;
-  dim3 grid((unsigned)((N + BN - 1) / BN), (unsigned)((M + 63) / 64));
-  switch (NT) {
-    case 1:
-      hipLaunchKernelGGL(gemm_skinny_kernel<1>, grid, dim3(256), 0, st, x, w, bias, (int)M, (int)N,
-                         (int)K, (int)ep, out);
-      break;
-    case 2:
-      hipLaunchKernelGGL(gemm_skinny_kernel<2>, grid, dim3(256), 0, st, x, w, bias, (int)M, (int)N,
-                         (int)K, (int)ep, out);
-      break;
-    default:
-      hipLaunchKernelGGL(gemm_skinny_kernel<4>, grid, dim3(256), 0, st, x, w, bias, (int)M, (int)N,
-                         (int)K, (int)ep, out);
-      break;
+  // Rows per tile (MT x 16) and columns per tile (NT x 16): wide column tiles
+  // only when there are many of them.  Waves per tile (KW, splitting K): as
+  // many as it takes for each wave's whole k-range (<= UNR steps of 32) to be
+  // in flight in one round, up to 16; the LDS reduction buffer
+  // KW x 16MT x (16NT+1) floats stays <= 64 KiB.
+  const int MT = M <= 16 ? 1 : M <= 32 ? 2 : 4;
+  const int NT = (MT <= 2 && N >= 8192) ? 4 : (N > 4096 ? 2 : 1);
+  constexpr int UNR = 4;
+  const int64_t ksteps = K / 32;
+  const int kw_cap = (MT * NT <= 4) ? 16 : 8;
+  int KW = 1;
+  while (KW < kw_cap && (ksteps + KW - 1) / KW > UNR) KW <<= 1;
+  if (KW == 2) KW = 4;
+  const int BN = 16 * NT, BM = 16 * MT;
+  dim3 grid((unsigned)((N + BN - 1) / BN), (unsigned)((M + BM - 1) / BM));
+  const int m = (int)M, n = (int)N, k = (int)K, e = (int)ep;
+  if (MT == 1) {
+    if (NT == 4) launch_skinny<1, 4, UNR>(KW, grid, st, x, w, bias, m, n, k, e, out);
+    else if (NT == 2) launch_skinny<1, 2, UNR>(KW, grid, st, x, w, bias, m, n, k, e, out);
+    else launch_skinny<1, 1, UNR>(KW, grid, st, x, w, bias, m, n, k, e, out);
+  } else if (MT == 2) {
+    if (NT == 4) launch_skinny<2, 4, UNR>(KW, grid, st, x, w, bias, m, n, k, e, out);
+    else if (NT == 2) launch_skinny<2, 2, UNR>(KW, grid, st, x, w, bias, m, n, k, e, out);
+    else launch_skinny<2, 1, UNR>(KW, grid, st, x, w, bias, m, n, k, e, out);
+  } else {
+    if (NT == 2) launch_skinny<4, 2, UNR>(KW, grid, st, x, w, bias, m, n, k, e, out);
+    else launch_skinny<4, 1, UNR>(KW, grid, st, x, w, bias, m, n, k, e, out);
   }
   return hipGetLastError();
 }
