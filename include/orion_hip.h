@@ -254,18 +254,23 @@ int orion_hip_paged_attention_decode(orion_hip_device* dev, const orion_hip_kv_l
                                      const int64_t* d_bt_offsets, const uint32_t* d_bt_ids,
                                      const orion_hip_decode_plan* plan, float* d_out);
 
-/* Causal attention for prefill chunks on MFMA: sequence s contributes query
- * rows d_q[d_row_start[s] .. d_row_start[s] + d_row_count[s]) whose positions
- * are consecutive from d_first_pos[s]; each attends 0..=its position.  Same
- * result as paged_attention per row.  `max_rows` bounds d_row_count,
- * `max_position` bounds every position. */
+/* paged_attention (attention.rs:219-295) for prefill chunks, as a dense
+ * causal MFMA contraction: sequence s contributes query rows
+ * d_q[d_row_start[s] .. d_row_start[s] + d_row_count[s]) whose positions are
+ * consecutive from d_first_pos[s]; row i attends 0..=d_first_pos[s] + i.  Same
+ * result per row as orion_hip_paged_attention_decode.  `max_rows` bounds every
+ * d_row_count (it sizes the grid), `max_position` every position.  bf16 KV
+ * only (an f32 arena returns a Backend error).  hilo = 0 rounds Q and the
+ * softmax weights to bf16 (the MFMA-rate path for bf16 inputs); hilo = 1
+ * carries each as a hi + lo bf16 pair (~16-bit products, twice the MFMA work).
+ * Table lengths and block ids are the caller's guarantee, as for decode. */
 int orion_hip_paged_attention_prefill(orion_hip_device* dev, const orion_hip_kv_layout* kv,
                                       const void* d_arena, int64_t layer, const float* d_q,
                                       int64_t num_q_heads, int64_t num_seqs,
                                       const int32_t* d_row_start, const int32_t* d_row_count,
                                       const uint32_t* d_first_pos, const int64_t* d_bt_offsets,
                                       const uint32_t* d_bt_ids, int64_t max_rows,
-                                      int64_t max_position, float* d_out);
+                                      int64_t max_position, int32_t hilo, float* d_out);
 
 /* Slot mapping + KV write (transformer.rs:371-387 and :283-297) fused with
  * RoPE (tensor.rs:283-298): for each row, rotates its Q heads from d_q_in

@@ -1,14 +1,370 @@
-// Chunked-prefill causal attention over the paged cache (placeholder until
-// the MFMA kernel lands).
+// Chunked-prefill causal attention over the paged KV cache, on bf16 MFMA.
+//
+// Same result per query row as the reference's paged_attention
+// (crates/orion-models/src/attention.rs:219-295): query head h reads kv head
+// h / (Hq/Hkv), attends positions 0..=its own position (context_len is not
+// consulted), scores are (q.k) / sqrt(d), softmax, weighted sum of V.  The
+// rows of one prefill chunk hold consecutive positions, so a chunk is one
+// dense causal contraction against its sequence's cached prefix plus itself.
+//
+// Work unit (one 256-thread workgroup): one (sequence, kv head) and a tile of
+// 128 "packed rows", packed row p = (chunk row p / G, query head p % G) with
+// G = Hq/Hkv.  Packing the G query heads that share a kv head into the M
+// dimension means every K/V tile staged in LDS is used by all of them: K and
+// V are read from HBM once per 128 packed rows instead of once per head.
+// Each of the 4 waves owns 32 packed rows (two 16-row MFMA tiles).
+//
+// Per 64-key tile:
+//   S^T = K . Q^T   (v_mfma_f32_16x16x32_bf16; A = K rows from LDS, B = the
+//                    wave's queries held in registers as bf16 fragments)
+//   online softmax per query (a query is one lane column of S^T, so its
+//   running max / sum are per-lane scalars; the max is only exchanged across
+//   the four lane groups when a score exceeds it by more than 8)
+//   O^T += V^T . P^T (A = V^T via ds_read_tr16_b64 from the row-major LDS V
+//                    tile, B = P^T, which is the S^T accumulator layout
+//                    converted in place)
+// K/V tiles are double-buffered in LDS; the global loads of tile t+1 and the
+// block-table lookups of tile t+2 are in flight while tile t computes.
+//
+// Operand precision: with HILO = false Q and P are rounded to bf16 (RNE,
+// the MFMA-rate path for bf16 inputs); with HILO = true each is carried as a
+// hi + lo bf16 pair (two MFMAs), so products keep ~16 mantissa bits, matching
+// the decode kernels' precision.
 #include "common.hpp"
 #include "kernels.hpp"
 
 namespace orion {
 
-hipError_t launch_paged_prefill(hipStream_t, const KvGeom&, const void*, int64_t, const float*,
-                                int64_t, int64_t, const int32_t*, const int32_t*, const uint32_t*,
-                                const int64_t*, const uint32_t*, int64_t, int64_t, float*) {
-  return hipErrorNotSupported;
+namespace {
+
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) u32x4 lds_u32x4;
+typedef short v4s __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) v4s lds_v4s;
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+
+constexpr int kWaves = 4;
+constexpr int kNR = 2;                      // 16-row MFMA tiles per wave
+constexpr int kBM = kWaves * 16 * kNR;      // packed rows per workgroup
+constexpr int kBN = 64;                     // keys per tile
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kLazy = 8.0f;               // log2 units: weights stay <= 2^8
+
+// RNE pack of two f32 into bf16x2 bits (v_cvt_pk_bf16_f32).
+__device__ inline uint32_t pack_bf16_rne(float a, float b) {
+  const f32x2 v = {a, b};
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2));
+}
+
+__device__ inline bf16x8 u4_bf16x8(uint4 v) { return __builtin_bit_cast(bf16x8, v); }
+
+}  // namespace
+
+template <int D, bool HILO>
+__global__ void __launch_bounds__(256)
+    paged_prefill_kernel(const uint16_t* __restrict__ kv_layer, uint32_t blk_stride,
+                         uint32_t v_off, uint32_t slot_stride, int bs_log2, int num_kv_heads,
+                         int num_q_heads, const float* __restrict__ q,
+                         const int32_t* __restrict__ row_start,
+                         const int32_t* __restrict__ row_count,
+                         const uint32_t* __restrict__ first_pos,
+                         const int64_t* __restrict__ bt_offsets,
+                         const uint32_t* __restrict__ bt_ids, int max_tiles, float scale_log2,
+                         float* __restrict__ out) {
+  constexpr int KCH = D / 32;           // S^T k-steps
+  constexpr int DT = D / 16;            // O^T dim tiles
+  constexpr int ROW = D + 8;            // padded LDS row (bf16 elements)
+  constexpr int CPR = D / 8;            // 16-byte chunks per key row
+  constexpr int KPP = 256 / CPR;        // key rows per load pass
+  constexpr int PASSES = kBN / KPP;     // load passes per tile (K and V each)
+  constexpr int TILE = kBN * ROW;       // one K or V tile, elements
+  static_assert(PASSES >= 1 && KPP * PASSES == kBN, "tile shape");
+
+  __shared__ __attribute__((aligned(16))) uint16_t lds[2][2][TILE];  // [buf][k|v]
+
+  const int seq = blockIdx.x / num_kv_heads;
+  const int kvh = blockIdx.x - seq * num_kv_heads;
+  const int tile = max_tiles - 1 - (int)blockIdx.y;  // longest tiles first
+  const int G = num_q_heads / num_kv_heads;
+  const int cnt = row_count[seq];
+  const int P = cnt * G;
+  if (tile * kBM >= P) return;
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int l16 = lane & 15;
+  const int grp = lane >> 4;
+  const int bs_mask = (1 << bs_log2) - 1;
+
+  const int pos0 = (int)first_pos[seq];
+  const int64_t rs = row_start[seq];
+  const uint32_t* tbl = bt_ids + bt_offsets[seq];
+  const int p_lo = tile * kBM;
+  const int p_hi = min(P, p_lo + kBM) - 1;
+  const int kv_len = pos0 + p_hi / G + 1;          // keys this workgroup reads
+  const int min_pos = pos0 + p_lo / G;             // no masking below this key
+  const int ntiles = (kv_len + kBN - 1) / kBN;
+
+  // ---- this lane's queries (packed rows of its two row tiles) ----
+  int qpos[kNR];
+  bf16x8 qhi[kNR][KCH], qlo[kNR][KCH];
+#pragma unroll
+  for (int rt = 0; rt < kNR; ++rt) {
+    const int p = min(p_lo + wave * 16 * kNR + rt * 16 + l16, P - 1);
+    const int r = p / G;
+    qpos[rt] = pos0 + r;
+    const float* qp = q + ((rs + r) * num_q_heads + (int64_t)kvh * G + (p - r * G)) * D + grp * 8;
+#pragma unroll
+    for (int c = 0; c < KCH; ++c) {
+      const float4 x0 = *reinterpret_cast<const float4*>(qp + 32 * c);
+      const float4 x1 = *reinterpret_cast<const float4*>(qp + 32 * c + 4);
+      uint4 h, l;
+      if constexpr (HILO) {
+        split2_trunc(x0.x, x0.y, h.x, l.x);
+        split2_trunc(x0.z, x0.w, h.y, l.y);
+        split2_trunc(x1.x, x1.y, h.z, l.z);
+        split2_trunc(x1.z, x1.w, h.w, l.w);
+        qlo[rt][c] = u4_bf16x8(l);
+      } else {
+        h.x = pack_bf16_rne(x0.x, x0.y);
+        h.y = pack_bf16_rne(x0.z, x0.w);
+        h.z = pack_bf16_rne(x1.x, x1.y);
+        h.w = pack_bf16_rne(x1.z, x1.w);
+        (void)l;
+      }
+      qhi[rt][c] = u4_bf16x8(h);
+    }
+  }
+
+  // ---- K/V tile loader: thread -> (key row kr + KPP*pass, 16-byte chunk) ----
+  const int kr = tid / CPR;
+  const int kc = tid - kr * CPR;
+  const uint16_t* head_base = kv_layer + (uint32_t)kvh * D + kc * 8;
+  uint32_t ids_next[PASSES];   // block ids of the tile after the one in flight
+  uint4 kst[PASSES], vst[PASSES];
+  auto key_of = [&](int t, int pass) { return min(t * kBN + pass * KPP + kr, kv_len - 1); };
+  auto load_ids = [&](int t, uint32_t (&ids)[PASSES]) {
+    const int tt = min(t, ntiles - 1);
+#pragma unroll
+    for (int ps = 0; ps < PASSES; ++ps) ids[ps] = tbl[key_of(tt, ps) >> bs_log2];
+  };
+  auto load_tile = [&](int t, const uint32_t (&ids)[PASSES]) {
+#pragma unroll
+    for (int ps = 0; ps < PASSES; ++ps) {
+      const uint16_t* src =
+          head_base + ids[ps] * blk_stride + (uint32_t)(key_of(t, ps) & bs_mask) * slot_stride;
+      kst[ps] = *reinterpret_cast<const uint4*>(src);
+      vst[ps] = *reinterpret_cast<const uint4*>(src + v_off);
+    }
+  };
+  const uint32_t lds_base = (uint32_t)(uintptr_t)&lds[0][0][0];
+  auto store_tile = [&](int buf) {
+    const uint32_t kb = lds_base + (uint32_t)(buf * 2 * TILE + kr * ROW + kc * 8) * 2;
+#pragma unroll
+    for (int ps = 0; ps < PASSES; ++ps) {
+      *(lds_u32x4*)(uintptr_t)(kb + ps * KPP * ROW * 2) = __builtin_bit_cast(u32x4, kst[ps]);
+      *(lds_u32x4*)(uintptr_t)(kb + (TILE + ps * KPP * ROW) * 2) =
+          __builtin_bit_cast(u32x4, vst[ps]);
+    }
+  };
+
+  // ---- prologue: tile 0 into LDS buffer 0, ids of tile 1 ready ----
+  {
+    uint32_t ids0[PASSES];
+    load_ids(0, ids0);
+    load_tile(0, ids0);
+    load_ids(1, ids_next);
+    store_tile(0);
+  }
+  __syncthreads();
+
+  float m[kNR], lsum[kNR];
+  f32x4 o[kNR][DT];
+#pragma unroll
+  for (int rt = 0; rt < kNR; ++rt) {
+    m[rt] = -INFINITY;
+    lsum[rt] = 0.f;
+#pragma unroll
+    for (int t = 0; t < DT; ++t) o[rt][t] = f32x4{0.f, 0.f, 0.f, 0.f};
+  }
+
+  // LDS read offsets (bytes): K A-fragment (key l16, dims grp*8) and the
+  // transposed V read (lane 4r + c of a group addresses key 4*grp + r,
+  // dims 4c .. 4c+3 of a 16-dim tile).
+  const uint32_t k_rd = (uint32_t)(l16 * ROW + grp * 8) * 2;
+  const uint32_t v_rd = (uint32_t)(TILE + (4 * grp + (l16 >> 2)) * ROW + 4 * (l16 & 3)) * 2;
+
+  for (int t = 0; t < ntiles; ++t) {
+    const int buf = t & 1;
+    const bool more = t + 1 < ntiles;
+    if (more) {
+      load_tile(t + 1, ids_next);
+      load_ids(t + 2, ids_next);
+    }
+    const uint32_t kbuf = lds_base + (uint32_t)(buf * 2 * TILE) * 2;
+
+    // S^T[rt][kt]: keys t*64 + kt*16 + 4*grp + i, query l16 of row tile rt.
+    f32x4 s[kNR][4];
+#pragma unroll
+    for (int rt = 0; rt < kNR; ++rt)
+#pragma unroll
+      for (int kt = 0; kt < 4; ++kt) s[rt][kt] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int c = 0; c < KCH; ++c) {
+#pragma unroll
+      for (int kt = 0; kt < 4; ++kt) {
+        const u32x4 kraw = *(const lds_u32x4*)(uintptr_t)(kbuf + k_rd + (kt * 16 * ROW + c * 32) * 2);
+        const bf16x8 ka = __builtin_bit_cast(bf16x8, kraw);
+#pragma unroll
+        for (int rt = 0; rt < kNR; ++rt) {
+          s[rt][kt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ka, qhi[rt][c], s[rt][kt], 0, 0, 0);
+          if constexpr (HILO)
+            s[rt][kt] =
+                __builtin_amdgcn_mfma_f32_16x16x32_bf16(ka, qlo[rt][c], s[rt][kt], 0, 0, 0);
+        }
+      }
+    }
+
+    // Online softmax in log2 units; P^T fragments for the P.V MFMA.
+    const bool masked = t * kBN + kBN - 1 > min_pos;
+    bf16x8 phi[kNR][2], plo[kNR][2];
+#pragma unroll
+    for (int rt = 0; rt < kNR; ++rt) {
+      float mx = -INFINITY;
+#pragma unroll
+      for (int kt = 0; kt < 4; ++kt)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          float v = s[rt][kt][i] * scale_log2;
+          if (masked && t * kBN + kt * 16 + 4 * grp + i > qpos[rt]) v = -INFINITY;
+          s[rt][kt][i] = v;
+          mx = fmaxf(mx, v);
+        }
+      if (__builtin_amdgcn_ballot_w64(mx > m[rt] + kLazy) != 0) {
+        mx = fmaxf(mx, __shfl_xor(mx, 16));
+        mx = fmaxf(mx, __shfl_xor(mx, 32));
+        const float m_new = fmaxf(m[rt], mx);
+        const float alpha = __builtin_amdgcn_exp2f(m[rt] - m_new);
+        m[rt] = m_new;
+        lsum[rt] *= alpha;
+#pragma unroll
+        for (int d = 0; d < DT; ++d) o[rt][d] *= alpha;
+      }
+      float ps = 0.f;
+#pragma unroll
+      for (int kp = 0; kp < 2; ++kp) {
+        float pv[8];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          pv[i] = __builtin_amdgcn_exp2f(s[rt][2 * kp][i] - m[rt]);
+          pv[4 + i] = __builtin_amdgcn_exp2f(s[rt][2 * kp + 1][i] - m[rt]);
+        }
+        ps += ((pv[0] + pv[1]) + (pv[2] + pv[3])) + ((pv[4] + pv[5]) + (pv[6] + pv[7]));
+        uint4 h, l;
+        if constexpr (HILO) {
+          split2_trunc(pv[0], pv[1], h.x, l.x);
+          split2_trunc(pv[2], pv[3], h.y, l.y);
+          split2_trunc(pv[4], pv[5], h.z, l.z);
+          split2_trunc(pv[6], pv[7], h.w, l.w);
+          plo[rt][kp] = u4_bf16x8(l);
+        } else {
+          h.x = pack_bf16_rne(pv[0], pv[1]);
+          h.y = pack_bf16_rne(pv[2], pv[3]);
+          h.z = pack_bf16_rne(pv[4], pv[5]);
+          h.w = pack_bf16_rne(pv[6], pv[7]);
+          (void)l;
+        }
+        phi[rt][kp] = u4_bf16x8(h);
+      }
+      lsum[rt] += ps;
+    }
+
+    // O^T[rt][d] += V^T . P^T; k-slots 0..3 = keys kp*32 + 4*grp + r,
+    // slots 4..7 = the same + 16 (the layout of S^T tiles 2kp and 2kp + 1).
+#pragma unroll
+    for (int d = 0; d < DT; ++d) {
+#pragma unroll
+      for (int kp = 0; kp < 2; ++kp) {
+        const uint32_t a0 = kbuf + v_rd + (kp * 32 * ROW + d * 16) * 2;
+        const v4s v0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4s*)(uintptr_t)a0);
+        const v4s v1 =
+            __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4s*)(uintptr_t)(a0 + 16 * ROW * 2));
+        typedef short v8s __attribute__((ext_vector_type(8)));
+        const v8s vv = __builtin_shufflevector(v0, v1, 0, 1, 2, 3, 4, 5, 6, 7);
+        const bf16x8 va = __builtin_bit_cast(bf16x8, vv);
+#pragma unroll
+        for (int rt = 0; rt < kNR; ++rt) {
+          o[rt][d] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(va, phi[rt][kp], o[rt][d], 0, 0, 0);
+          if constexpr (HILO)
+            o[rt][d] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(va, plo[rt][kp], o[rt][d], 0, 0, 0);
+        }
+      }
+    }
+
+    if (more) store_tile(buf ^ 1);
+    __syncthreads();
+  }
+
+  // ---- normalise and store: lane holds dims 16d + 4*grp .. +3 of query l16 ----
+#pragma unroll
+  for (int rt = 0; rt < kNR; ++rt) {
+    float l = lsum[rt];
+    l += __shfl_xor(l, 16);
+    l += __shfl_xor(l, 32);
+    const int p = p_lo + wave * 16 * kNR + rt * 16 + l16;
+    if (p < P) {
+      const int r = p / G;
+      const float inv = 1.0f / l;
+      float* op = out + ((rs + r) * num_q_heads + (int64_t)kvh * G + (p - r * G)) * D + 4 * grp;
+#pragma unroll
+      for (int d = 0; d < DT; ++d)
+        *reinterpret_cast<float4*>(op + 16 * d) =
+            make_float4(o[rt][d][0] * inv, o[rt][d][1] * inv, o[rt][d][2] * inv,
+                        o[rt][d][3] * inv);
+    }
+  }
+}
+
+int prefill_tile_rows() { return kBM; }
+
+hipError_t launch_paged_prefill(hipStream_t st, const KvGeom& kv, const void* arena,
+                                int64_t layer, const float* q, int64_t hq, int64_t num_seqs,
+                                const int32_t* row_start, const int32_t* row_count,
+                                const uint32_t* first_pos, const int64_t* bt_offsets,
+                                const uint32_t* bt_ids, int64_t max_rows, int64_t max_position,
+                                bool hilo, float* out) {
+  (void)max_position;
+  if (num_seqs == 0 || max_rows == 0) return hipSuccess;
+  if (!kv.dtype_bf16) return hipErrorNotSupported;
+  const int64_t hkv = kv.num_kv_heads, D = kv.head_dim;
+  if (hkv <= 0 || hq % hkv != 0 || (D != 64 && D != 128)) return hipErrorInvalidValue;
+  const int64_t G = hq / hkv;
+  int bs_log2 = 0;
+  while ((1 << bs_log2) < kv.block_size) ++bs_log2;
+  const int64_t slot_stride = hkv * D;
+  const int64_t v_off = kv.block_size * slot_stride;
+  const int64_t blk_stride = 2 * v_off;
+  const int64_t layer_elems = kv.num_blocks * blk_stride;
+  if (layer_elems > (int64_t)UINT32_MAX) return hipErrorInvalidValue;
+  const uint16_t* base = static_cast<const uint16_t*>(arena) + layer * layer_elems;
+  const int64_t tiles = (max_rows * G + kBM - 1) / kBM;
+  if (tiles > 65535 || num_seqs * hkv > INT32_MAX) return hipErrorInvalidValue;
+  const float scale_log2 = kLog2e / sqrtf((float)D);
+  const dim3 grid((unsigned)(num_seqs * hkv), (unsigned)tiles);
+#define ORION_PREFILL(DD, HH)                                                                   \
+  hipLaunchKernelGGL((paged_prefill_kernel<DD, HH>), grid, dim3(256), 0, st, base,              \
+                     (uint32_t)blk_stride, (uint32_t)v_off, (uint32_t)slot_stride, bs_log2,     \
+                     (int)hkv, (int)hq, q, row_start, row_count, first_pos, bt_offsets, bt_ids, \
+                     (int)tiles, scale_log2, out)
+  if (D == 128) {
+    if (hilo) ORION_PREFILL(128, true); else ORION_PREFILL(128, false);
+  } else {
+    if (hilo) ORION_PREFILL(64, true); else ORION_PREFILL(64, false);
+  }
+#undef ORION_PREFILL
+  return hipGetLastError();
 }
 
 }  // namespace orion

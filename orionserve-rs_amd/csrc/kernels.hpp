@@ -53,7 +53,9 @@ hipError_t launch_paged_prefill(hipStream_t st, const KvGeom& kv, const void* ar
                                 const int32_t* row_start, const int32_t* row_count,
                                 const uint32_t* first_pos, const int64_t* bt_off,
                                 const uint32_t* bt_ids, int64_t max_rows, int64_t max_position,
-                                float* out);
+                                bool hilo, float* out);
+// Packed (row, query head) rows per prefill workgroup tile.
+int prefill_tile_rows();
 
 // ---- GEMM -------------------------------------------------------------------
 enum class Epilogue : int {

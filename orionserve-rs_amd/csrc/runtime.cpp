@@ -1013,7 +1013,8 @@ ORION_EXPORT int orion_hip_paged_attention_prefill(
     orion_hip_device* dev, const orion_hip_kv_layout* kv, const void* d_arena, int64_t layer,
     const float* d_q, int64_t num_q_heads, int64_t num_seqs, const int32_t* d_row_start,
     const int32_t* d_row_count, const uint32_t* d_first_pos, const int64_t* d_bt_offsets,
-    const uint32_t* d_bt_ids, int64_t max_rows, int64_t max_position, float* d_out) {
+    const uint32_t* d_bt_ids, int64_t max_rows, int64_t max_position, int32_t hilo,
+    float* d_out) {
   const char* st = "paged_attention_prefill";
   KvGeom g;
   if (int rc = kv_geom_from(kv, &g, st)) return rc;
@@ -1022,7 +1023,7 @@ ORION_EXPORT int orion_hip_paged_attention_prefill(
   HIP_TRY(st, hipSetDevice(dev->ordinal));
   HIP_TRY(st, launch_paged_prefill(dev->stream, g, d_arena, layer, d_q, num_q_heads, num_seqs,
                                    d_row_start, d_row_count, d_first_pos, d_bt_offsets, d_bt_ids,
-                                   max_rows, max_position, d_out));
+                                   max_rows, max_position, hilo != 0, d_out));
   return ORION_HIP_OK;
 }
 

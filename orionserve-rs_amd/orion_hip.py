@@ -146,7 +146,8 @@ def load_library(path: str = LIB_PATH) -> C.CDLL:
         "orion_hip_paged_attention_decode": (
             [vp, P(KvLayout), vp, i64, vp, i64, i64, vp, vp, vp, vp, vp, vp], C.c_int),
         "orion_hip_paged_attention_prefill": (
-            [vp, P(KvLayout), vp, i64, vp, i64, i64, vp, vp, vp, vp, vp, i64, i64, vp], C.c_int),
+            [vp, P(KvLayout), vp, i64, vp, i64, i64, vp, vp, vp, vp, vp, i64, i64, C.c_int32, vp],
+            C.c_int),
         "orion_hip_rope_and_cache": (
             [vp, P(KvLayout), vp, i64, i64, i64, vp, i64, vp, vp, i64, vp, i64, vp, vp, vp, vp,
              vp, vp], C.c_int),
@@ -532,10 +533,11 @@ def paged_attention_prefill(be: HipBackend, kv: KvLayout, arena_ptr: int, layer:
                             num_q_heads: int, num_seqs: int, row_start_ptr: int,
                             row_count_ptr: int, first_pos_ptr: int, bt_off_ptr: int,
                             bt_ids_ptr: int, max_rows: int, max_position: int,
-                            out_ptr: int) -> None:
+                            out_ptr: int, hilo: bool = False) -> None:
     _check(be.lib.orion_hip_paged_attention_prefill(
         be.handle, C.byref(kv), arena_ptr, layer, q_ptr, num_q_heads, num_seqs, row_start_ptr,
-        row_count_ptr, first_pos_ptr, bt_off_ptr, bt_ids_ptr, max_rows, max_position, out_ptr))
+        row_count_ptr, first_pos_ptr, bt_off_ptr, bt_ids_ptr, max_rows, max_position,
+        1 if hilo else 0, out_ptr))
 
 
 def rope_and_cache(be: HipBackend, kv: KvLayout, arena_ptr: int, layer: int, num_rows: int,

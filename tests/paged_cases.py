@@ -75,3 +75,51 @@ def cfg2(seed=20261202, num_seqs=64):
     rng = np.random.default_rng(seed)
     ctxs = rng.integers(128, 4097, size=num_seqs)
     return PagedCase(seed + 1, ctxs, 32, 8, 128, 16, dtype="bf16", pool_factor=1.25)
+
+
+class PrefillCase(PagedCase):
+    """Chunked prefill: sequence s has `prefixes[s]` cached tokens plus a new
+    chunk of `chunks[s]` rows at consecutive positions prefix .. prefix +
+    chunk - 1 (all of whose K/V are already in the arena, as after the KV
+    write).  Rows are laid out sequence after sequence.  With bf16 KV the
+    queries are bf16-representable too ("bf16 inputs")."""
+
+    def __init__(self, seed, prefixes, chunks, hq, hkv, d, block_size, dtype="bf16",
+                 **kw):
+        prefixes = np.asarray(prefixes, np.int64)
+        chunks = np.asarray(chunks, np.int64)
+        super().__init__(seed, prefixes + chunks, hq, hkv, d, block_size, dtype=dtype, **kw)
+        rng = np.random.default_rng(seed + 7)
+        self.prefixes, self.chunks = prefixes, chunks
+        self.row_start = np.zeros(self.S, np.int32)
+        self.row_start[1:] = np.cumsum(chunks)[:-1]
+        self.row_count = chunks.astype(np.int32)
+        self.first_pos = prefixes.astype(np.uint32)
+        n = int(chunks.sum())
+        self.positions = np.concatenate(
+            [np.arange(p, p + c, dtype=np.uint32) for p, c in zip(prefixes, chunks)]) \
+            if n else np.zeros(0, np.uint32)
+        self.row_seq = np.repeat(np.arange(self.S, dtype=np.int32), chunks)
+        q = rng.standard_normal((n, hq * d), dtype=np.float32)
+        if dtype == "bf16":
+            from model_fixtures import bf16_round
+            q = bf16_round(q)
+        self.q = q
+
+    def flops(self):
+        """Algorithmic flops: 4 * Hq * d per (query row, attended key)."""
+        per_seq = self.chunks * self.prefixes + self.chunks * (self.chunks + 1) // 2
+        return 4 * self.hq * self.d * int(per_seq.sum())
+
+    def oracle_rows(self, rows):
+        """Oracle output for the listed rows only ([len(rows), Hq*d])."""
+        rows = np.asarray(rows, np.int64)
+        return self.oracle(self.positions[rows], self.row_seq[rows], self.q[rows])
+
+
+def cfg3(seed=20261203):
+    """8 seqs x 512-token chunk on a prefix U[0,7680], bs 16,
+    32q/8kv, d 128, bf16 inputs, scattered tables."""
+    rng = np.random.default_rng(seed)
+    prefixes = rng.integers(0, 7681, size=8)
+    return PrefillCase(seed + 1, prefixes, [512] * 8, 32, 8, 128, 16, dtype="bf16")

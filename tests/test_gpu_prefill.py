@@ -1,0 +1,120 @@
+"""Chunked-prefill attention (MFMA) on the MI355X against the CPU oracle's
+paged_attention (crates/orion-models/src/attention.rs:219-295), and against
+the decode kernel on the same rows."""
+import numpy as np
+import pytest
+
+import oracle as orc
+import orion_hip as oh
+from paged_cases import PrefillCase, cfg3
+from test_gpu_attention import run_decode
+
+pytestmark = pytest.mark.gpu
+
+
+def run_prefill(be, case, hilo):
+    n = len(case.positions)
+    kv = oh.kv_layout(1, case.num_blocks, case.bs, case.hkv, case.d,
+                      oh.BF16 if case.dtype == "bf16" else oh.F32)
+    bufs = [be.to_device(case.arena_device_bytes()), be.to_device(case.q),
+            be.to_device(case.row_start), be.to_device(case.row_count),
+            be.to_device(case.first_pos), be.to_device(case.bt_offsets),
+            be.to_device(case.bt_ids), be.alloc(max(n, 1) * case.hq * case.d * 4)]
+    arena, dq, drs, drc, dfp, dbo, dbi, dout = bufs
+    max_rows = int(case.row_count.max()) if case.S else 0
+    max_pos = int(case.positions.max()) if n else 0
+    print(f"[prefill] seqs={case.S} rows={n} hq={case.hq} hkv={case.hkv} d={case.d} "
+          f"bs={case.bs} hilo={hilo} max_rows={max_rows} max_pos={max_pos}", flush=True)
+    try:
+        oh.paged_attention_prefill(be, kv, arena.ptr, 0, dq.ptr, case.hq, case.S, drs.ptr,
+                                   drc.ptr, dfp.ptr, dbo.ptr, dbi.ptr, max_rows, max_pos,
+                                   dout.ptr, hilo=hilo)
+        return dout.download(np.float32, (n, case.hq * case.d))
+    finally:
+        for b in bufs:
+            b.free()
+
+
+def sample_rows(case, per_seq, seed=0):
+    """First, last and `per_seq` random rows of every sequence's chunk."""
+    rng = np.random.default_rng(seed)
+    rows = []
+    for s in range(case.S):
+        a, c = int(case.row_start[s]), int(case.row_count[s])
+        if c == 0:
+            continue
+        pick = {a, a + c - 1} | set((a + rng.integers(0, c, size=min(per_seq, c))).tolist())
+        rows += sorted(pick)
+    return np.array(rows, np.int64)
+
+
+@pytest.mark.parametrize("hilo", [False, True])
+def test_cfg3_full_size_sampled_rows(backend, hilo):
+    case = cfg3()
+    got = run_prefill(backend, case, hilo)
+    rows = sample_rows(case, 24)
+    want = case.oracle_rows(rows)
+    err = float(np.abs(got[rows] - want).max())
+    print(f"cfg3 hilo={hilo} sampled rows={len(rows)} max_abs_err={err:.3g}", flush=True)
+    assert err <= 1e-2, err                    # north-star tolerance on attention outputs
+    if hilo:
+        assert err <= 1e-4, err                # hi/lo operands: f32-class products
+    assert np.isfinite(got).all()
+
+
+@pytest.mark.parametrize("hq,hkv,d,bs", [
+    (32, 8, 128, 16), (28, 4, 128, 16), (32, 4, 64, 16), (8, 2, 64, 16), (8, 8, 64, 8),
+    (12, 4, 128, 32), (6, 1, 64, 1), (16, 16, 128, 64),
+])
+@pytest.mark.parametrize("hilo", [False, True])
+def test_shapes_against_oracle(backend, hq, hkv, d, bs, hilo):
+    # Prefixes 0 / inside a block / block- and tile-aligned; chunks of 1, 2,
+    # a ragged tile and several tiles.
+    prefixes = [0, 0, 5, 16, 63, 64, 200, 1000]
+    chunks = [1, 2, 33, 64, 129, 17, 300, 70]
+    case = PrefillCase(hq * 100 + d + bs, prefixes, chunks, hq, hkv, d, bs)
+    got = run_prefill(backend, case, hilo)
+    want = case.oracle()
+    tol = orc.Tolerance(1e-4, 1e-4) if hilo else orc.Tolerance(1e-2, 1e-2)
+    mm, ma, mr, wi = orc.validate(want, got, tol)
+    assert mm == 0, (ma, mr, wi)
+    assert float(np.abs(got - want).max()) <= (1e-4 if hilo else 1e-2)
+
+
+def test_matches_decode_kernel_on_same_rows(backend):
+    # The two kernels restate the same per-row computation; with hi/lo
+    # operands they agree to f32-class rounding.
+    case = PrefillCase(77, [0, 900, 3000], [150, 64, 257], 32, 8, 128, 16)
+    got = run_prefill(backend, case, True)
+    dec = run_decode(backend, case)
+    assert float(np.abs(got - dec).max()) <= 5e-5
+
+
+def test_single_row_and_uniform_keys(backend):
+    # Closed forms: a row at position 0 returns V[0] exactly (one weight of 1);
+    # identical keys give the mean of the attended V rows.
+    case = PrefillCase(5, [0], [40], 8, 2, 64, 16)
+    kvd = case.hkv * case.d
+    a = case.arena_f32.reshape(case.num_blocks, 2, case.bs, kvd)
+    tbl = case.tables[0]
+    a[tbl, 0] = a[tbl[0], 0, 0]                      # every key identical
+    got = run_prefill(backend, case, False)
+    v = a[:, 1][tbl].reshape(-1, case.hkv, case.d)   # V rows in position order
+    for r in range(40):
+        for h in range(case.hq):
+            want = v[:r + 1, h // (case.hq // case.hkv)].mean(axis=0)
+            np.testing.assert_allclose(got[r, h * case.d:(h + 1) * case.d], want,
+                                       rtol=0, atol=2e-6 * (r + 1))
+
+
+def test_empty_and_zero_row_sequences(backend):
+    case = PrefillCase(9, [10, 0, 50], [0, 3, 0], 8, 2, 64, 16)
+    got = run_prefill(backend, case, False)
+    want = case.oracle()
+    assert float(np.abs(got - want).max()) <= 1e-2
+
+
+def test_f32_arena_is_a_backend_error(backend):
+    case = PrefillCase(3, [4], [8], 8, 2, 64, 16, dtype="f32")
+    with pytest.raises(oh.BackendError):
+        run_prefill(backend, case, False)
