@@ -59,10 +59,39 @@ __device__ inline uint32_t pack_bf16_rne(float a, float b) {
 
 __device__ inline bf16x8 u4_bf16x8(uint4 v) { return __builtin_bit_cast(bf16x8, v); }
 
+// global_load_lds_dwordx4: the wave's 64 lanes each fetch 16 bytes from their
+// own global address and the hardware stores them to LDS at lds_wave_base +
+// 16 * lane (lds_wave_base must be wave-uniform).  Written as inline asm so
+// the compiler's wait-count tracking does not treat every later LDS read as
+// a possible reader of the in-flight copy; the kernel orders these copies
+// itself (vmcnt(0) then a workgroup barrier before the tile is read).
+// Nothing else in these kernels uses M0.
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+__device__ inline void lds_load16(const void* src, uint32_t lds_wave_base) {
+  asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, off"
+               :
+               : "s"(lds_wave_base), "v"(src)
+               : "memory", "m0");
+}
+#pragma clang diagnostic pop
+
 }  // namespace
 
+// LDS K/V tiles are unpadded rows of D bf16 (kBN rows), written by
+// global_load_lds (each wave instruction fills 1 KiB: 64 lanes x 16 bytes in
+// lane order).  The 16-byte chunks of row r are stored XOR-permuted,
+// chunk' = chunk ^ swz(r), so that both read patterns are free of bank
+// conflicts: the K fragment read (16 consecutive rows, one chunk) and the
+// transposed V read (8 consecutive rows x 2 adjacent chunks per half-wave).
+template <int D>
+__device__ inline int swz(int r) {
+  if constexpr (D == 128) return ((r & 7) << 1) | ((r >> 3) & 1);
+  else return (((r >> 1) & 3) << 1) | ((r >> 3) & 1);
+}
+
 template <int D, bool HILO>
-__global__ void __launch_bounds__(256)
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2)))
     paged_prefill_kernel(const uint16_t* __restrict__ kv_layer, uint32_t blk_stride,
                          uint32_t v_off, uint32_t slot_stride, int bs_log2, int num_kv_heads,
                          int num_q_heads, const float* __restrict__ q,
@@ -74,14 +103,13 @@ __global__ void __launch_bounds__(256)
                          float* __restrict__ out) {
   constexpr int KCH = D / 32;           // S^T k-steps
   constexpr int DT = D / 16;            // O^T dim tiles
-  constexpr int ROW = D + 8;            // padded LDS row (bf16 elements)
   constexpr int CPR = D / 8;            // 16-byte chunks per key row
-  constexpr int KPP = 256 / CPR;        // key rows per load pass
-  constexpr int PASSES = kBN / KPP;     // load passes per tile (K and V each)
-  constexpr int TILE = kBN * ROW;       // one K or V tile, elements
-  static_assert(PASSES >= 1 && KPP * PASSES == kBN, "tile shape");
+  constexpr int RPI = 64 / CPR;         // key rows per wave load instruction
+  constexpr int LPW = kBN / kWaves / RPI;  // load instructions per wave (K and V each)
+  constexpr int TILE = kBN * D;         // one K or V tile, elements
+  static_assert(LPW >= 1 && RPI * LPW * kWaves == kBN, "tile shape");
 
-  __shared__ __attribute__((aligned(16))) uint16_t lds[2][2][TILE];  // [buf][k|v]
+  __shared__ __attribute__((aligned(1024))) uint16_t lds[2][2][TILE];  // [buf][k|v]
 
   const int seq = blockIdx.x / num_kv_heads;
   const int kvh = blockIdx.x - seq * num_kv_heads;
@@ -138,85 +166,101 @@ __global__ void __launch_bounds__(256)
     }
   }
 
-  // ---- K/V tile loader: thread -> (key row kr + KPP*pass, 16-byte chunk) ----
-  const int kr = tid / CPR;
-  const int kc = tid - kr * CPR;
-  const uint16_t* head_base = kv_layer + (uint32_t)kvh * D + kc * 8;
-  uint32_t ids_next[PASSES];   // block ids of the tile after the one in flight
-  uint4 kst[PASSES], vst[PASSES];
-  auto key_of = [&](int t, int pass) { return min(t * kBN + pass * KPP + kr, kv_len - 1); };
-  auto load_ids = [&](int t, uint32_t (&ids)[PASSES]) {
+  // ---- K/V tile loader: wave instruction j fills rows wave*RPI*LPW + j*RPI
+  // + lane / CPR; the lane stores LDS chunk lane % CPR of its row, which
+  // holds global chunk (lane % CPR) ^ swz(row). ----
+  const int ld_row0 = wave * RPI * LPW + lane / CPR;
+  const uint16_t* head_base = kv_layer + (uint32_t)kvh * D;
+  uint32_t ld_chunk_off[LPW];   // element offset of the fetched chunk within a key row
+#pragma unroll
+  for (int j = 0; j < LPW; ++j)
+    ld_chunk_off[j] = (uint32_t)(((lane % CPR) ^ swz<D>(ld_row0 + j * RPI)) * 8);
+  uint32_t ids_next[LPW];       // block ids of the tile after the one in flight
+  auto key_of = [&](int t, int j) { return min(t * kBN + ld_row0 + j * RPI, kv_len - 1); };
+  auto load_ids = [&](int t, uint32_t (&ids)[LPW]) {
     const int tt = min(t, ntiles - 1);
 #pragma unroll
-    for (int ps = 0; ps < PASSES; ++ps) ids[ps] = tbl[key_of(tt, ps) >> bs_log2];
-  };
-  auto load_tile = [&](int t, const uint32_t (&ids)[PASSES]) {
-#pragma unroll
-    for (int ps = 0; ps < PASSES; ++ps) {
-      const uint16_t* src =
-          head_base + ids[ps] * blk_stride + (uint32_t)(key_of(t, ps) & bs_mask) * slot_stride;
-      kst[ps] = *reinterpret_cast<const uint4*>(src);
-      vst[ps] = *reinterpret_cast<const uint4*>(src + v_off);
-    }
+    for (int j = 0; j < LPW; ++j) ids[j] = tbl[key_of(tt, j) >> bs_log2];
   };
   const uint32_t lds_base = (uint32_t)(uintptr_t)&lds[0][0][0];
-  auto store_tile = [&](int buf) {
-    const uint32_t kb = lds_base + (uint32_t)(buf * 2 * TILE + kr * ROW + kc * 8) * 2;
+  auto load_tile = [&](int t, int buf, const uint32_t (&ids)[LPW]) {
 #pragma unroll
-    for (int ps = 0; ps < PASSES; ++ps) {
-      *(lds_u32x4*)(uintptr_t)(kb + ps * KPP * ROW * 2) = __builtin_bit_cast(u32x4, kst[ps]);
-      *(lds_u32x4*)(uintptr_t)(kb + (TILE + ps * KPP * ROW) * 2) =
-          __builtin_bit_cast(u32x4, vst[ps]);
+    for (int j = 0; j < LPW; ++j) {
+      const uint32_t off = __umul24(ids[j], blk_stride) +
+                           __umul24((uint32_t)(key_of(t, j) & bs_mask), slot_stride) +
+                           ld_chunk_off[j];
+      const uint16_t* src = head_base + off;
+      const uint32_t dk = lds_base + (uint32_t)((buf * 2 * TILE + (wave * LPW + j) * RPI * D) * 2);
+      lds_load16(src, __builtin_amdgcn_readfirstlane(dk));
+      lds_load16(src + v_off, __builtin_amdgcn_readfirstlane(dk + TILE * 2));
     }
   };
 
   // ---- prologue: tile 0 into LDS buffer 0, ids of tile 1 ready ----
   {
-    uint32_t ids0[PASSES];
+    uint32_t ids0[LPW];
     load_ids(0, ids0);
-    load_tile(0, ids0);
+    load_tile(0, 0, ids0);
     load_ids(1, ids_next);
-    store_tile(0);
   }
+  __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): this wave's LDS loads have landed
   __syncthreads();
 
-  float m[kNR], lsum[kNR];
-  f32x4 o[kNR][DT];
+  float m[kNR];                 // running max of raw scores (q.k), per query
+  f32x4 o[kNR][DT];             // O^T: dims 16d + 4*grp + i, query l16
+  f32x4 lsum[kNR];              // row sums of the weights, from a ones-row MFMA
 #pragma unroll
   for (int rt = 0; rt < kNR; ++rt) {
     m[rt] = -INFINITY;
-    lsum[rt] = 0.f;
+    lsum[rt] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int t = 0; t < DT; ++t) o[rt][t] = f32x4{0.f, 0.f, 0.f, 0.f};
   }
+  const bf16x8 ones = __builtin_bit_cast(bf16x8, uint4{0x3F803F80u, 0x3F803F80u, 0x3F803F80u,
+                                                       0x3F803F80u});
 
-  // LDS read offsets (bytes): K A-fragment (key l16, dims grp*8) and the
-  // transposed V read (lane 4r + c of a group addresses key 4*grp + r,
-  // dims 4c .. 4c+3 of a 16-dim tile).
-  const uint32_t k_rd = (uint32_t)(l16 * ROW + grp * 8) * 2;
-  const uint32_t v_rd = (uint32_t)(TILE + (4 * grp + (l16 >> 2)) * ROW + 4 * (l16 & 3)) * 2;
+  // LDS read offsets (elements, within a tile): the K fragment of row
+  // kt*16 + l16 / chunk 4c + grp; the transposed V read of lane 4rr + cc of
+  // a group: row 4*grp + rr (+16), dims 16d + 4cc .. +3.
+  const int vr = 4 * grp + (l16 >> 2);
+  const int vcc = l16 & 3;
+  const float lazy_raw = kLazy / scale_log2;
 
   for (int t = 0; t < ntiles; ++t) {
     const int buf = t & 1;
     const bool more = t + 1 < ntiles;
     if (more) {
-      load_tile(t + 1, ids_next);
+      __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): the block ids are in
+      load_tile(t + 1, buf ^ 1, ids_next);
       load_ids(t + 2, ids_next);
     }
-    const uint32_t kbuf = lds_base + (uint32_t)(buf * 2 * TILE) * 2;
+    const uint16_t* kt_lds = &lds[buf][0][0];
+    const uint16_t* vt_lds = &lds[buf][1][0];
 
-    // S^T[rt][kt]: keys t*64 + kt*16 + 4*grp + i, query l16 of row tile rt.
+    // S^T[rt][kt]: raw scores of keys t*64 + kt*16 + 4*grp + i, query l16.
     f32x4 s[kNR][4];
 #pragma unroll
     for (int rt = 0; rt < kNR; ++rt)
 #pragma unroll
       for (int kt = 0; kt < 4; ++kt) s[rt][kt] = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int c = 0; c < KCH; ++c) {
+    // K fragments one k-step ahead of the MFMAs that consume them.
+    u32x4 kf[2][4];
+    auto read_k = [&](int c, u32x4 (&dst)[4]) {
 #pragma unroll
       for (int kt = 0; kt < 4; ++kt) {
-        const u32x4 kraw = *(const lds_u32x4*)(uintptr_t)(kbuf + k_rd + (kt * 16 * ROW + c * 32) * 2);
-        const bf16x8 ka = __builtin_bit_cast(bf16x8, kraw);
+        const int row = kt * 16 + l16;
+        const uint16_t* a = kt_lds + row * D + (((4 * c + grp) ^ swz<D>(row)) * 8);
+        dst[kt] = *(const lds_u32x4*)(uintptr_t)(uint32_t)(uintptr_t)a;
+      }
+    };
+    read_k(0, kf[0]);
+#pragma unroll
+    for (int c = 0; c < KCH; ++c) {
+      if (c + 1 < KCH) read_k(c + 1, kf[(c + 1) & 1]);
+      __builtin_amdgcn_sched_barrier(0);  // keep the prefetch ahead of the MFMAs
+#pragma unroll
+      for (int kt = 0; kt < 4; ++kt) {
+        const bf16x8 ka = __builtin_bit_cast(bf16x8, kf[c & 1][kt]);
 #pragma unroll
         for (int rt = 0; rt < kNR; ++rt) {
           s[rt][kt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ka, qhi[rt][c], s[rt][kt], 0, 0, 0);
@@ -227,41 +271,45 @@ __global__ void __launch_bounds__(256)
       }
     }
 
-    // Online softmax in log2 units; P^T fragments for the P.V MFMA.
+    // Online softmax: weights exp2((s - m) * scale_log2); m only rises (with
+    // an exact cross-group max and a rescale) when a score exceeds it by
+    // more than kLazy in log2 units.
     const bool masked = t * kBN + kBN - 1 > min_pos;
     bf16x8 phi[kNR][2], plo[kNR][2];
 #pragma unroll
     for (int rt = 0; rt < kNR; ++rt) {
+      if (masked) {
+#pragma unroll
+        for (int kt = 0; kt < 4; ++kt)
+#pragma unroll
+          for (int i = 0; i < 4; ++i)
+            if (t * kBN + kt * 16 + 4 * grp + i > qpos[rt]) s[rt][kt][i] = -INFINITY;
+      }
       float mx = -INFINITY;
 #pragma unroll
       for (int kt = 0; kt < 4; ++kt)
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          float v = s[rt][kt][i] * scale_log2;
-          if (masked && t * kBN + kt * 16 + 4 * grp + i > qpos[rt]) v = -INFINITY;
-          s[rt][kt][i] = v;
-          mx = fmaxf(mx, v);
-        }
-      if (__builtin_amdgcn_ballot_w64(mx > m[rt] + kLazy) != 0) {
+        mx = fmaxf(fmaxf(mx, fmaxf(s[rt][kt][0], s[rt][kt][1])),
+                   fmaxf(s[rt][kt][2], s[rt][kt][3]));
+      if (__builtin_amdgcn_ballot_w64(mx > m[rt] + lazy_raw) != 0) {
         mx = fmaxf(mx, __shfl_xor(mx, 16));
         mx = fmaxf(mx, __shfl_xor(mx, 32));
         const float m_new = fmaxf(m[rt], mx);
-        const float alpha = __builtin_amdgcn_exp2f(m[rt] - m_new);
+        const float alpha = __builtin_amdgcn_exp2f((m[rt] - m_new) * scale_log2);
         m[rt] = m_new;
         lsum[rt] *= alpha;
 #pragma unroll
         for (int d = 0; d < DT; ++d) o[rt][d] *= alpha;
       }
-      float ps = 0.f;
+      const float nm = -m[rt] * scale_log2;
 #pragma unroll
       for (int kp = 0; kp < 2; ++kp) {
         float pv[8];
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          pv[i] = __builtin_amdgcn_exp2f(s[rt][2 * kp][i] - m[rt]);
-          pv[4 + i] = __builtin_amdgcn_exp2f(s[rt][2 * kp + 1][i] - m[rt]);
+          pv[i] = __builtin_amdgcn_exp2f(__builtin_fmaf(s[rt][2 * kp][i], scale_log2, nm));
+          pv[4 + i] =
+              __builtin_amdgcn_exp2f(__builtin_fmaf(s[rt][2 * kp + 1][i], scale_log2, nm));
         }
-        ps += ((pv[0] + pv[1]) + (pv[2] + pv[3])) + ((pv[4] + pv[5]) + (pv[6] + pv[7]));
         uint4 h, l;
         if constexpr (HILO) {
           split2_trunc(pv[0], pv[1], h.x, l.x);
@@ -278,22 +326,46 @@ __global__ void __launch_bounds__(256)
         }
         phi[rt][kp] = u4_bf16x8(h);
       }
-      lsum[rt] += ps;
     }
 
-    // O^T[rt][d] += V^T . P^T; k-slots 0..3 = keys kp*32 + 4*grp + r,
+    // O^T[rt][d] += V^T . P^T; k-slots 0..3 = keys kp*32 + 4*grp + rr,
     // slots 4..7 = the same + 16 (the layout of S^T tiles 2kp and 2kp + 1).
+    // The row sums come from the same P^T against a row of ones.
 #pragma unroll
-    for (int d = 0; d < DT; ++d) {
+    for (int kp = 0; kp < 2; ++kp) {
+#pragma unroll
+      for (int rt = 0; rt < kNR; ++rt) {
+        lsum[rt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ones, phi[rt][kp], lsum[rt], 0, 0, 0);
+        if constexpr (HILO)
+          lsum[rt] =
+              __builtin_amdgcn_mfma_f32_16x16x32_bf16(ones, plo[rt][kp], lsum[rt], 0, 0, 0);
+      }
+    }
+    // V^T fragments (two transposed reads per 32 keys) one dim tile ahead.
+    typedef short v8s __attribute__((ext_vector_type(8)));
+    v8s vf[2][2];
+    auto read_v = [&](int d, v8s (&dst)[2]) {
 #pragma unroll
       for (int kp = 0; kp < 2; ++kp) {
-        const uint32_t a0 = kbuf + v_rd + (kp * 32 * ROW + d * 16) * 2;
-        const v4s v0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4s*)(uintptr_t)a0);
-        const v4s v1 =
-            __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4s*)(uintptr_t)(a0 + 16 * ROW * 2));
-        typedef short v8s __attribute__((ext_vector_type(8)));
-        const v8s vv = __builtin_shufflevector(v0, v1, 0, 1, 2, 3, 4, 5, 6, 7);
-        const bf16x8 va = __builtin_bit_cast(bf16x8, vv);
+        const int r0 = kp * 32 + vr, r1 = r0 + 16;
+        const int ch = 2 * d + (vcc >> 1);
+        const uint16_t* a0 = vt_lds + r0 * D + ((ch ^ swz<D>(r0)) * 8) + (vcc & 1) * 4;
+        const uint16_t* a1 = vt_lds + r1 * D + ((ch ^ swz<D>(r1)) * 8) + (vcc & 1) * 4;
+        const v4s v0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+            (lds_v4s*)(uintptr_t)(uint32_t)(uintptr_t)a0);
+        const v4s v1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+            (lds_v4s*)(uintptr_t)(uint32_t)(uintptr_t)a1);
+        dst[kp] = __builtin_shufflevector(v0, v1, 0, 1, 2, 3, 4, 5, 6, 7);
+      }
+    };
+    read_v(0, vf[0]);
+#pragma unroll
+    for (int d = 0; d < DT; ++d) {
+      if (d + 1 < DT) read_v(d + 1, vf[(d + 1) & 1]);
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int kp = 0; kp < 2; ++kp) {
+        const bf16x8 va = __builtin_bit_cast(bf16x8, vf[d & 1][kp]);
 #pragma unroll
         for (int rt = 0; rt < kNR; ++rt) {
           o[rt][d] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(va, phi[rt][kp], o[rt][d], 0, 0, 0);
@@ -303,20 +375,17 @@ __global__ void __launch_bounds__(256)
       }
     }
 
-    if (more) store_tile(buf ^ 1);
+    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): next tile's LDS loads have landed
     __syncthreads();
   }
 
   // ---- normalise and store: lane holds dims 16d + 4*grp .. +3 of query l16 ----
 #pragma unroll
   for (int rt = 0; rt < kNR; ++rt) {
-    float l = lsum[rt];
-    l += __shfl_xor(l, 16);
-    l += __shfl_xor(l, 32);
     const int p = p_lo + wave * 16 * kNR + rt * 16 + l16;
     if (p < P) {
       const int r = p / G;
-      const float inv = 1.0f / l;
+      const float inv = 1.0f / lsum[rt][0];
       float* op = out + ((rs + r) * num_q_heads + (int64_t)kvh * G + (p - r * G)) * D + 4 * grp;
 #pragma unroll
       for (int d = 0; d < DT; ++d)
