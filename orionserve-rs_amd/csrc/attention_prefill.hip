@@ -33,6 +33,8 @@
 #include "common.hpp"
 #include "kernels.hpp"
 
+#include <type_traits>
+
 namespace orion {
 
 namespace {
@@ -90,7 +92,7 @@ __device__ inline int swz(int r) {
   else return (((r >> 1) & 3) << 1) | ((r >> 3) & 1);
 }
 
-template <int D, bool HILO>
+template <int D, bool HILO, bool BIG>
 __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2)))
     paged_prefill_kernel(const uint16_t* __restrict__ kv_layer, uint32_t blk_stride,
                          uint32_t v_off, uint32_t slot_stride, int bs_log2, int num_kv_heads,
@@ -168,29 +170,37 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2)))
 
   // ---- K/V tile loader: wave instruction j fills rows wave*RPI*LPW + j*RPI
   // + lane / CPR; the lane stores LDS chunk lane % CPR of its row, which
-  // holds global chunk (lane % CPR) ^ swz(row). ----
+  // holds global chunk (lane % CPR) ^ swz(row).  With blocks of >= 16 slots
+  // a wave's 16 rows of a tile lie in one block: one (uniform) table read. ----
+  constexpr int NID = BIG ? 1 : LPW;
+  const int wave_u = __builtin_amdgcn_readfirstlane(wave);
   const int ld_row0 = wave * RPI * LPW + lane / CPR;
   const uint16_t* head_base = kv_layer + (uint32_t)kvh * D;
   uint32_t ld_chunk_off[LPW];   // element offset of the fetched chunk within a key row
 #pragma unroll
   for (int j = 0; j < LPW; ++j)
     ld_chunk_off[j] = (uint32_t)(((lane % CPR) ^ swz<D>(ld_row0 + j * RPI)) * 8);
-  uint32_t ids_next[LPW];       // block ids of the tile after the one in flight
+  uint32_t ids_next[NID];       // block ids of the tile after the one in flight
   auto key_of = [&](int t, int j) { return min(t * kBN + ld_row0 + j * RPI, kv_len - 1); };
-  auto load_ids = [&](int t, uint32_t (&ids)[LPW]) {
+  auto load_ids = [&](int t, uint32_t (&ids)[NID]) {
     const int tt = min(t, ntiles - 1);
+    if constexpr (BIG) {
+      ids[0] = tbl[min(tt * kBN + wave_u * RPI * LPW, kv_len - 1) >> bs_log2];
+    } else {
 #pragma unroll
-    for (int j = 0; j < LPW; ++j) ids[j] = tbl[key_of(tt, j) >> bs_log2];
+      for (int j = 0; j < LPW; ++j) ids[j] = tbl[key_of(tt, j) >> bs_log2];
+    }
   };
   const uint32_t lds_base = (uint32_t)(uintptr_t)&lds[0][0][0];
-  auto load_tile = [&](int t, int buf, const uint32_t (&ids)[LPW]) {
+  auto load_tile = [&](int t, int buf, const uint32_t (&ids)[NID]) {
 #pragma unroll
     for (int j = 0; j < LPW; ++j) {
-      const uint32_t off = __umul24(ids[j], blk_stride) +
+      const uint32_t off = __umul24(ids[BIG ? 0 : j], blk_stride) +
                            __umul24((uint32_t)(key_of(t, j) & bs_mask), slot_stride) +
                            ld_chunk_off[j];
       const uint16_t* src = head_base + off;
-      const uint32_t dk = lds_base + (uint32_t)((buf * 2 * TILE + (wave * LPW + j) * RPI * D) * 2);
+      const uint32_t dk =
+          lds_base + (uint32_t)((buf * 2 * TILE + (wave_u * LPW + j) * RPI * D) * 2);
       lds_load16(src, __builtin_amdgcn_readfirstlane(dk));
       lds_load16(src + v_off, __builtin_amdgcn_readfirstlane(dk + TILE * 2));
     }
@@ -198,7 +208,7 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2)))
 
   // ---- prologue: tile 0 into LDS buffer 0, ids of tile 1 ready ----
   {
-    uint32_t ids0[LPW];
+    uint32_t ids0[NID];
     load_ids(0, ids0);
     load_tile(0, 0, ids0);
     load_ids(1, ids_next);
@@ -219,23 +229,33 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2)))
   const bf16x8 ones = __builtin_bit_cast(bf16x8, uint4{0x3F803F80u, 0x3F803F80u, 0x3F803F80u,
                                                        0x3F803F80u});
 
-  // LDS read offsets (elements, within a tile): the K fragment of row
-  // kt*16 + l16 / chunk 4c + grp; the transposed V read of lane 4rr + cc of
-  // a group: row 4*grp + rr (+16), dims 16d + 4cc .. +3.
+  // Loop-invariant LDS byte addresses (buffer 0).  K fragment: row
+  // kt*16 + l16, chunk 4c + grp (kt only adds a constant: swz depends on the
+  // low 4 row bits).  Transposed V read, lane 4rr + cc of a group: row
+  // 4*grp + rr (+16, +32: constants), dims 16d + 4cc .. +3.
   const int vr = 4 * grp + (l16 >> 2);
   const int vcc = l16 & 3;
+  uint32_t k_addr[KCH], v_addr[DT];
+#pragma unroll
+  for (int c = 0; c < KCH; ++c)
+    k_addr[c] = lds_base + (uint32_t)(l16 * D + (((4 * c + grp) ^ swz<D>(l16)) * 8)) * 2;
+#pragma unroll
+  for (int d = 0; d < DT; ++d)
+    v_addr[d] = lds_base + (uint32_t)(TILE + vr * D +
+                                      ((2 * d + (vcc >> 1)) ^ swz<D>(vr)) * 8 + (vcc & 1) * 4) * 2;
   const float lazy_raw = kLazy / scale_log2;
 
-  for (int t = 0; t < ntiles; ++t) {
-    const int buf = t & 1;
+  // One key tile; BUF (the LDS buffer holding it) is a compile-time constant
+  // so every LDS read is a loop-invariant address plus an immediate offset.
+  auto step = [&](int t, auto buf_tag) {
+    constexpr int BUF = decltype(buf_tag)::value;
+    constexpr uint32_t kBufOff = BUF * 2 * TILE * 2;
     const bool more = t + 1 < ntiles;
     if (more) {
       __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): the block ids are in
-      load_tile(t + 1, buf ^ 1, ids_next);
+      load_tile(t + 1, BUF ^ 1, ids_next);
       load_ids(t + 2, ids_next);
     }
-    const uint16_t* kt_lds = &lds[buf][0][0];
-    const uint16_t* vt_lds = &lds[buf][1][0];
 
     // S^T[rt][kt]: raw scores of keys t*64 + kt*16 + 4*grp + i, query l16.
     f32x4 s[kNR][4];
@@ -247,11 +267,8 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2)))
     u32x4 kf[2][4];
     auto read_k = [&](int c, u32x4 (&dst)[4]) {
 #pragma unroll
-      for (int kt = 0; kt < 4; ++kt) {
-        const int row = kt * 16 + l16;
-        const uint16_t* a = kt_lds + row * D + (((4 * c + grp) ^ swz<D>(row)) * 8);
-        dst[kt] = *(const lds_u32x4*)(uintptr_t)(uint32_t)(uintptr_t)a;
-      }
+      for (int kt = 0; kt < 4; ++kt)
+        dst[kt] = *(const lds_u32x4*)(uintptr_t)(k_addr[c] + kBufOff + kt * 16 * D * 2);
     };
     read_k(0, kf[0]);
 #pragma unroll
@@ -347,14 +364,10 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2)))
     auto read_v = [&](int d, v8s (&dst)[2]) {
 #pragma unroll
       for (int kp = 0; kp < 2; ++kp) {
-        const int r0 = kp * 32 + vr, r1 = r0 + 16;
-        const int ch = 2 * d + (vcc >> 1);
-        const uint16_t* a0 = vt_lds + r0 * D + ((ch ^ swz<D>(r0)) * 8) + (vcc & 1) * 4;
-        const uint16_t* a1 = vt_lds + r1 * D + ((ch ^ swz<D>(r1)) * 8) + (vcc & 1) * 4;
-        const v4s v0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-            (lds_v4s*)(uintptr_t)(uint32_t)(uintptr_t)a0);
-        const v4s v1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-            (lds_v4s*)(uintptr_t)(uint32_t)(uintptr_t)a1);
+        const uint32_t a0 = v_addr[d] + kBufOff + kp * 32 * D * 2;
+        const v4s v0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4s*)(uintptr_t)a0);
+        const v4s v1 =
+            __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4s*)(uintptr_t)(a0 + 16 * D * 2));
         dst[kp] = __builtin_shufflevector(v0, v1, 0, 1, 2, 3, 4, 5, 6, 7);
       }
     };
@@ -377,6 +390,11 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2)))
 
     __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): next tile's LDS loads have landed
     __syncthreads();
+  };
+
+  for (int t = 0; t < ntiles; t += 2) {
+    step(t, std::integral_constant<int, 0>{});
+    if (t + 1 < ntiles) step(t + 1, std::integral_constant<int, 1>{});
   }
 
   // ---- normalise and store: lane holds dims 16d + 4*grp .. +3 of query l16 ----
@@ -422,17 +440,26 @@ hipError_t launch_paged_prefill(hipStream_t st, const KvGeom& kv, const void* ar
   if (tiles > 65535 || num_seqs * hkv > INT32_MAX) return hipErrorInvalidValue;
   const float scale_log2 = kLog2e / sqrtf((float)D);
   const dim3 grid((unsigned)(num_seqs * hkv), (unsigned)tiles);
-#define ORION_PREFILL(DD, HH)                                                                   \
-  hipLaunchKernelGGL((paged_prefill_kernel<DD, HH>), grid, dim3(256), 0, st, base,              \
+#define ORION_PREFILL_B(DD, HH, BB)                                                             \
+  hipLaunchKernelGGL((paged_prefill_kernel<DD, HH, BB>), grid, dim3(256), 0, st, base,              \
                      (uint32_t)blk_stride, (uint32_t)v_off, (uint32_t)slot_stride, bs_log2,     \
                      (int)hkv, (int)hq, q, row_start, row_count, first_pos, bt_offsets, bt_ids, \
                      (int)tiles, scale_log2, out)
+#define ORION_PREFILL(DD, HH)        \
+  do {                               \
+    if (big)                         \
+      ORION_PREFILL_B(DD, HH, true); \
+    else                             \
+      ORION_PREFILL_B(DD, HH, false);\
+  } while (0)
+  const bool big = kv.block_size >= 16;
   if (D == 128) {
     if (hilo) ORION_PREFILL(128, true); else ORION_PREFILL(128, false);
   } else {
     if (hilo) ORION_PREFILL(64, true); else ORION_PREFILL(64, false);
   }
 #undef ORION_PREFILL
+#undef ORION_PREFILL_B
   return hipGetLastError();
 }
 
