@@ -83,13 +83,18 @@ __device__ inline void lds_load16(const void* src, uint32_t lds_wave_base) {
 // LDS K/V tiles are unpadded rows of D bf16 (kBN rows), written by
 // global_load_lds (each wave instruction fills 1 KiB: 64 lanes x 16 bytes in
 // lane order).  The 16-byte chunks of row r are stored XOR-permuted,
-// chunk' = chunk ^ swz(r), so that both read patterns are free of bank
-// conflicts: the K fragment read (16 consecutive rows, one chunk) and the
-// transposed V read (8 consecutive rows x 2 adjacent chunks per half-wave).
+// chunk' = chunk ^ swz(r), chosen per tile by measurement on gfx950 so that
+// the K fragment read (ds_read_b128: 16 consecutive rows x 2 chunk groups
+// per 32-lane pass) and the transposed V read (ds_read_b64_tr_b16: 16 rows x
+// 2 adjacent chunks) run at the bank-conflict-free rate.
 template <int D>
-__device__ inline int swz(int r) {
+__device__ inline int swz_k(int r) {
+  return D == 128 ? (r & 15) : (r & 7);
+}
+template <int D>
+__device__ inline int swz_v(int r) {
   if constexpr (D == 128) return ((r & 7) << 1) | ((r >> 3) & 1);
-  else return (((r >> 1) & 3) << 1) | ((r >> 3) & 1);
+  else return r & 7;
 }
 
 template <int D, bool HILO, bool BIG>
@@ -176,10 +181,12 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2)))
   const int wave_u = __builtin_amdgcn_readfirstlane(wave);
   const int ld_row0 = wave * RPI * LPW + lane / CPR;
   const uint16_t* head_base = kv_layer + (uint32_t)kvh * D;
-  uint32_t ld_chunk_off[LPW];   // element offset of the fetched chunk within a key row
+  uint32_t ld_off_k[LPW], ld_off_v[LPW];  // element offsets of the fetched chunks
 #pragma unroll
-  for (int j = 0; j < LPW; ++j)
-    ld_chunk_off[j] = (uint32_t)(((lane % CPR) ^ swz<D>(ld_row0 + j * RPI)) * 8);
+  for (int j = 0; j < LPW; ++j) {
+    ld_off_k[j] = (uint32_t)(((lane % CPR) ^ swz_k<D>(ld_row0 + j * RPI)) * 8);
+    ld_off_v[j] = (uint32_t)(((lane % CPR) ^ swz_v<D>(ld_row0 + j * RPI)) * 8) + v_off;
+  }
   uint32_t ids_next[NID];       // block ids of the tile after the one in flight
   auto key_of = [&](int t, int j) { return min(t * kBN + ld_row0 + j * RPI, kv_len - 1); };
   auto load_ids = [&](int t, uint32_t (&ids)[NID]) {
@@ -196,13 +203,11 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2)))
 #pragma unroll
     for (int j = 0; j < LPW; ++j) {
       const uint32_t off = __umul24(ids[BIG ? 0 : j], blk_stride) +
-                           __umul24((uint32_t)(key_of(t, j) & bs_mask), slot_stride) +
-                           ld_chunk_off[j];
-      const uint16_t* src = head_base + off;
+                           __umul24((uint32_t)(key_of(t, j) & bs_mask), slot_stride);
       const uint32_t dk =
           lds_base + (uint32_t)((buf * 2 * TILE + (wave_u * LPW + j) * RPI * D) * 2);
-      lds_load16(src, __builtin_amdgcn_readfirstlane(dk));
-      lds_load16(src + v_off, __builtin_amdgcn_readfirstlane(dk + TILE * 2));
+      lds_load16(head_base + off + ld_off_k[j], __builtin_amdgcn_readfirstlane(dk));
+      lds_load16(head_base + off + ld_off_v[j], __builtin_amdgcn_readfirstlane(dk + TILE * 2));
     }
   };
 
@@ -230,19 +235,19 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2)))
                                                        0x3F803F80u});
 
   // Loop-invariant LDS byte addresses (buffer 0).  K fragment: row
-  // kt*16 + l16, chunk 4c + grp (kt only adds a constant: swz depends on the
-  // low 4 row bits).  Transposed V read, lane 4rr + cc of a group: row
+  // kt*16 + l16, chunk 4c + grp (kt only adds a constant: the swizzles depend
+  // on the low 4 row bits only).  Transposed V read, lane 4rr + cc of a group: row
   // 4*grp + rr (+16, +32: constants), dims 16d + 4cc .. +3.
   const int vr = 4 * grp + (l16 >> 2);
   const int vcc = l16 & 3;
   uint32_t k_addr[KCH], v_addr[DT];
 #pragma unroll
   for (int c = 0; c < KCH; ++c)
-    k_addr[c] = lds_base + (uint32_t)(l16 * D + (((4 * c + grp) ^ swz<D>(l16)) * 8)) * 2;
+    k_addr[c] = lds_base + (uint32_t)(l16 * D + (((4 * c + grp) ^ swz_k<D>(l16)) * 8)) * 2;
 #pragma unroll
   for (int d = 0; d < DT; ++d)
     v_addr[d] = lds_base + (uint32_t)(TILE + vr * D +
-                                      ((2 * d + (vcc >> 1)) ^ swz<D>(vr)) * 8 + (vcc & 1) * 4) * 2;
+                                      ((2 * d + (vcc >> 1)) ^ swz_v<D>(vr)) * 8 + (vcc & 1) * 4) * 2;
   const float lazy_raw = kLazy / scale_log2;
 
   // One key tile; BUF (the LDS buffer holding it) is a compile-time constant
