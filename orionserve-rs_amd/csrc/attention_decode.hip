@@ -794,14 +794,18 @@ __global__ void __launch_bounds__(256)
 template <int D>
 __global__ void __launch_bounds__(256)
     paged_decode_combine_kernel(int num_rows, int num_q_heads, const uint32_t* __restrict__ positions,
+                                const int32_t* __restrict__ row_list,
                                 int partition, int max_splits, const float* __restrict__ ws_o,
                                 const float* __restrict__ ws_ml, float* __restrict__ out) {
   constexpr int PER = D / 64;
   constexpr int MAXS = 8;
   const int lane = threadIdx.x & 63;
-  const int64_t item = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
-  if (item >= (int64_t)num_rows * num_q_heads) return;
-  const int row = (int)(item / num_q_heads);
+  const int64_t slot = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (slot >= (int64_t)num_rows * num_q_heads) return;
+  // num_rows counts row_list entries when a list is given.
+  const int li = (int)(slot / num_q_heads);
+  const int row = row_list ? row_list[li] : li;
+  const int64_t item = (int64_t)row * num_q_heads + (slot - (int64_t)li * num_q_heads);
   const int len = (int)positions[row] + 1;
   const int nsplit = (len + partition - 1) / partition;
   if (nsplit <= 1) return;
@@ -898,14 +902,20 @@ static int64_t simulate_makespan(const std::vector<int>& lens, int64_t hkv, int 
 
 void build_decode_plan(const uint32_t* positions, const int32_t* row_seq,
                        const int64_t* bt_offsets, const uint32_t* bt_ids, int64_t rows,
-                       int64_t hkv, int64_t block_size, int64_t wave_slots, DecodePlanHost* plan) {
+                       int64_t hkv, int64_t block_size, int64_t wave_slots,
+                       const uint8_t* skip_rows, DecodePlanHost* plan) {
   int bs_log2 = 0;
   while ((1 << bs_log2) < block_size) ++bs_log2;
+  // Rows flagged in skip_rows get no work (another kernel covers them);
+  // their length counts as 0 for the chunk choice and the split bound.
   std::vector<int> lens(rows);
   int max_len = 0;
+  plan->rows.clear();
   for (int64_t r = 0; r < rows; ++r) {
-    lens[r] = (int)positions[r] + 1;
+    const bool skip = skip_rows && skip_rows[r];
+    lens[r] = skip ? 0 : (int)positions[r] + 1;
     max_len = std::max(max_len, lens[r]);
+    if (skip_rows && !skip) plan->rows.push_back((int32_t)r);
   }
   int best_c = 0;
   int64_t best_t = 0;
@@ -1042,6 +1052,22 @@ static hipError_t launch_mfma2(int G, dim3 grid, dim3 block, hipStream_t st, con
   return hipGetLastError();
 }
 
+// Merges the split-K partials of every row (or of plan.rows) into out.
+static hipError_t launch_combine(hipStream_t st, int64_t D, int64_t rows, int64_t hq,
+                                 const uint32_t* positions, const DecodePlanDev& plan, int C,
+                                 int ms, const float* ws_o, const float* ws_ml, float* out) {
+  const int64_t nr = plan.rows ? plan.num_rows : rows;
+  if (nr == 0) return hipSuccess;
+  dim3 cgrid((unsigned)((nr * hq + 3) / 4));
+  if (D == 128)
+    hipLaunchKernelGGL(paged_decode_combine_kernel<128>, cgrid, dim3(256), 0, st, (int)nr,
+                       (int)hq, positions, plan.rows, C, ms, ws_o, ws_ml, out);
+  else
+    hipLaunchKernelGGL(paged_decode_combine_kernel<64>, cgrid, dim3(256), 0, st, (int)nr,
+                       (int)hq, positions, plan.rows, C, ms, ws_o, ws_ml, out);
+  return hipGetLastError();
+}
+
 hipError_t launch_paged_decode(hipStream_t st, const KvGeom& kv, const void* arena, int64_t layer,
                                const float* q, int64_t rows, int64_t hq,
                                const uint32_t* positions, const int32_t* row_seq,
@@ -1106,14 +1132,7 @@ hipError_t launch_paged_decode(hipStream_t st, const KvGeom& kv, const void* are
 #undef ORION_MFMA2
 #undef ORION_MFMA2_NS
       if (e != hipSuccess || ms == 1) return e;
-      dim3 cgrid((unsigned)((rows * hq + 3) / 4));
-      if (D == 128)
-        hipLaunchKernelGGL(paged_decode_combine_kernel<128>, cgrid, dim3(256), 0, st, (int)rows,
-                           (int)hq, positions, C, ms, ws_o, ws_ml, out);
-      else
-        hipLaunchKernelGGL(paged_decode_combine_kernel<64>, cgrid, dim3(256), 0, st, (int)rows,
-                           (int)hq, positions, C, ms, ws_o, ws_ml, out);
-      return hipGetLastError();
+      return launch_combine(st, D, rows, hq, positions, plan, C, ms, ws_o, ws_ml, out);
     }
     if (loads_only && D == 128 && G == 4 && big) {
       hipLaunchKernelGGL((paged_decode_mfma_kernel<128, 4, 2, true, true>), grid, block, 0, st,
@@ -1144,14 +1163,7 @@ hipError_t launch_paged_decode(hipStream_t st, const KvGeom& kv, const void* are
       return hipErrorInvalidValue;
   }
   if (e != hipSuccess || ms == 1) return e;
-  dim3 cgrid((unsigned)((rows * hq + 3) / 4));
-  if (D == 128)
-    hipLaunchKernelGGL(paged_decode_combine_kernel<128>, cgrid, dim3(256), 0, st, (int)rows,
-                       (int)hq, positions, C, ms, ws_o, ws_ml, out);
-  else
-    hipLaunchKernelGGL(paged_decode_combine_kernel<64>, cgrid, dim3(256), 0, st, (int)rows,
-                       (int)hq, positions, C, ms, ws_o, ws_ml, out);
-  return hipGetLastError();
+  return launch_combine(st, D, rows, hq, positions, plan, C, ms, ws_o, ws_ml, out);
 }
 
 }  // namespace orion

@@ -29,6 +29,7 @@ struct DecodePlanHost {
   int chunk = 0;       // tokens per chunk (power of two)
   int max_splits = 0;  // chunks of the longest row
   std::vector<DecodeWork> work;
+  std::vector<int32_t> rows;  // rows covered when a skip mask was given (else all)
 };
 struct DecodePlanDev {
   const DecodeWork* work = nullptr;
@@ -37,10 +38,13 @@ struct DecodePlanDev {
   int max_splits = 0;
   float* ws = nullptr;  // split-K partials, decode_workspace_bytes()
   size_t ws_bytes = 0;
+  const int32_t* rows = nullptr;  // rows to merge (nullptr: every row)
+  int num_rows = 0;
 };
 void build_decode_plan(const uint32_t* positions, const int32_t* row_seq,
                        const int64_t* bt_offsets, const uint32_t* bt_ids, int64_t rows,
-                       int64_t hkv, int64_t block_size, int64_t wave_slots, DecodePlanHost* plan);
+                       int64_t hkv, int64_t block_size, int64_t wave_slots,
+                       const uint8_t* skip_rows, DecodePlanHost* plan);
 size_t decode_workspace_bytes(int64_t rows, int64_t hq, int64_t D, int64_t max_splits);
 hipError_t launch_paged_decode(hipStream_t st, const KvGeom& kv, const void* arena, int64_t layer,
                                const float* q, int64_t rows, int64_t hq,

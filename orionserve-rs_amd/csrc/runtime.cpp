@@ -818,10 +818,44 @@ ORION_EXPORT int orion_hip_model_forward(orion_hip_model* m, const orion_hip_bat
   HIP_TRY(st, m->act.reserve(n * F * 4));
   HIP_TRY(st, m->logits.reserve(S * V * 4));
   HIP_TRY(st, m->argmax.reserve(S * 8));
-  // Decode plan (longest-first chunk list), shared by every layer.
+  // Attention routing, shared by every layer.  A sequence whose rows are a
+  // chunk of consecutive positions with at least half a prefill tile of
+  // (row, query head) pairs goes to the MFMA prefill kernel (bf16 arena);
+  // every other row goes to the split-K decode kernel.
+  const int64_t G = Hq / d.num_kv_heads;
+  std::vector<uint8_t> skip(n, 0);
+  std::vector<int32_t> pf_start, pf_count;
+  std::vector<uint32_t> pf_pos;
+  std::vector<int64_t> pf_btoff;
+  int64_t pf_max_rows = 0;
+  // ORION_PREFILL_ROUTE=0 sends every row to the decode kernel (read per
+  // call; lets tests compare the two routes on one batch).
+  const char* route = getenv("ORION_PREFILL_ROUTE");
+  const bool route_pf = !(route && route[0] == '0');
+  if (route_pf && m->kv.dtype_bf16 && (d.head_dim == 64 || d.head_dim == 128)) {
+    int64_t r0 = 0;
+    for (int64_t s = 0; s < S; ++s) {
+      const int64_t c = b->slot_token_counts[s];
+      bool chunk = c * G >= prefill_tile_rows() / 2;
+      for (int64_t i = 1; chunk && i < c; ++i)
+        chunk = b->positions[r0 + i] == b->positions[r0] + (uint32_t)i;
+      if (chunk) {
+        pf_start.push_back((int32_t)r0);
+        pf_count.push_back((int32_t)c);
+        pf_pos.push_back(b->positions[r0]);
+        pf_btoff.push_back(b->block_table_offsets[s]);
+        pf_max_rows = std::max(pf_max_rows, c);
+        std::fill(skip.begin() + r0, skip.begin() + r0 + c, (uint8_t)1);
+      }
+      r0 += c;
+    }
+  }
+  const int64_t npf = (int64_t)pf_start.size();
+  // Decode plan (longest-first chunk list) over the remaining rows.
   DecodePlanHost plan;
   build_decode_plan(b->positions, hb.row_seq.data(), b->block_table_offsets, b->block_table_ids, n,
-                    d.num_kv_heads, d.block_size, m->dev->wave_slots, &plan);
+                    d.num_kv_heads, d.block_size, m->dev->wave_slots,
+                    npf ? skip.data() : nullptr, &plan);
   HIP_TRY(st, m->ws.reserve(decode_workspace_bytes(n, Hq, d.head_dim, plan.max_splits)));
 
   // ---- upload the batch: one pinned staging area, one copy ----
@@ -832,7 +866,12 @@ ORION_EXPORT int orion_hip_model_forward(orion_hip_model* m, const orion_hip_bat
   const size_t o_btoff = (o_last + S * 4 + 7) & ~(size_t)7;
   const size_t o_btids = o_btoff + (S + 1) * 8;
   const size_t o_work = (o_btids + nbt * 4 + 31) & ~(size_t)31;
-  const size_t total = o_work + plan.work.size() * sizeof(DecodeWork);
+  const size_t o_pfoff = (o_work + plan.work.size() * sizeof(DecodeWork) + 7) & ~(size_t)7;
+  const size_t o_pfstart = o_pfoff + npf * 8;
+  const size_t o_pfcount = o_pfstart + npf * 4;
+  const size_t o_pfpos = o_pfcount + npf * 4;
+  const size_t o_drows = o_pfpos + npf * 4;
+  const size_t total = o_drows + plan.rows.size() * 4;
   if (total > m->pinned_bytes) {
     if (m->pinned) {
       HIP_TRY(st, hipStreamSynchronize(stream));
@@ -853,6 +892,11 @@ ORION_EXPORT int orion_hip_model_forward(orion_hip_model* m, const orion_hip_bat
   std::memcpy(hp + o_btoff, b->block_table_offsets, (S + 1) * 8);
   std::memcpy(hp + o_btids, b->block_table_ids, nbt * 4);
   std::memcpy(hp + o_work, plan.work.data(), plan.work.size() * sizeof(DecodeWork));
+  std::memcpy(hp + o_pfoff, pf_btoff.data(), npf * 8);
+  std::memcpy(hp + o_pfstart, pf_start.data(), npf * 4);
+  std::memcpy(hp + o_pfcount, pf_count.data(), npf * 4);
+  std::memcpy(hp + o_pfpos, pf_pos.data(), npf * 4);
+  std::memcpy(hp + o_drows, plan.rows.data(), plan.rows.size() * 4);
   char* dp = m->b_tokens.as<char>();
   HIP_TRY(st, hipMemcpyAsync(dp, hp, total, hipMemcpyHostToDevice, stream));
   const uint32_t* d_tok = reinterpret_cast<const uint32_t*>(dp + o_tok);
@@ -868,6 +912,14 @@ ORION_EXPORT int orion_hip_model_forward(orion_hip_model* m, const orion_hip_bat
   dplan.max_splits = plan.max_splits;
   dplan.ws = m->ws.as<float>();
   dplan.ws_bytes = m->ws.bytes;
+  if (npf) {
+    dplan.rows = reinterpret_cast<const int32_t*>(dp + o_drows);
+    dplan.num_rows = (int)plan.rows.size();
+  }
+  const int64_t* d_pfoff = reinterpret_cast<const int64_t*>(dp + o_pfoff);
+  const int32_t* d_pfstart = reinterpret_cast<const int32_t*>(dp + o_pfstart);
+  const int32_t* d_pfcount = reinterpret_cast<const int32_t*>(dp + o_pfcount);
+  const uint32_t* d_pfpos = reinterpret_cast<const uint32_t*>(dp + o_pfpos);
 
   float* hidden = m->hidden.as<float>();
   float* xn = m->xn.as<float>();
@@ -886,6 +938,10 @@ ORION_EXPORT int orion_hip_model_forward(orion_hip_model* m, const orion_hip_bat
                                       d_rs, d_btoff, d_btids, m->rope_cos, m->rope_sin));
     HIP_TRY(st, launch_paged_decode(stream, m->kv, m->arena, l, qrot, n, Hq, d_pos, d_rs, d_btoff,
                                     d_btids, dplan, attn));
+    if (npf)
+      HIP_TRY(st, launch_paged_prefill(stream, m->kv, m->arena, l, qrot, Hq, npf, d_pfstart,
+                                       d_pfcount, d_pfpos, d_pfoff, d_btids, pf_max_rows,
+                                       hb.max_position, /*hilo=*/true, attn));
     HIP_TRY(st, launch_gemm(stream, attn, L.w_o, nullptr, n, H, m->qd, Epilogue::kAccumulate,
                             hidden));
     HIP_TRY(st, launch_rmsnorm(stream, hidden, nullptr, L.post_norm, n, H, d.rms_norm_eps, xn));
@@ -954,7 +1010,7 @@ ORION_EXPORT int orion_hip_decode_plan_create(orion_hip_device* dev, const uint3
                       positions[i]);
   }
   build_decode_plan(positions, row_seq, block_table_offsets, block_table_ids, num_rows,
-                    num_kv_heads, block_size, dev->wave_slots, &p->host);
+                    num_kv_heads, block_size, dev->wave_slots, nullptr, &p->host);
   const size_t wbytes = p->host.work.size() * sizeof(DecodeWork);
   HIP_TRY(st, p->work.reserve(wbytes));
   if (wbytes)
