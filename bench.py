@@ -26,7 +26,69 @@ for _p in (ROOT, os.path.join(ROOT, "orionserve-rs_amd"), os.path.join(ROOT, "te
 
 import numpy as np  # noqa: E402
 
-HBM_PEAK_GBS = 8000.0  # MI355X HBM3E, published
+HBM_PEAK_GBS = 8000.0      # MI355X HBM3E, published
+BF16_PEAK_TFLOPS = 2500.0  # MI355X dense bf16 MFMA, published
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "paged_decode_cfg2_pmc.txt")
+
+
+def measured_traffic():
+    """HBM bytes per launch of the decode split-K kernel, from the committed
+    rocprofv3 FETCH_SIZE / WRITE_SIZE summary (None when absent)."""
+    import re
+    try:
+        text = open(TRAFFIC_FILE).read()
+    except OSError:
+        return None
+    m = re.search(r"traffic_bytes_per_launch\s*=\s*(\d+)", text)
+    return int(m.group(1)) if m else None
+
+
+def prefill_cfg3(be, steps=20, warmup=3):
+    """chunked-prefill causal attention over the paged
+    cache as an MFMA contraction (8 seqs x 512-token chunks on prefixes
+    U[0,7680], 32q/8kv, d 128, bf16).  Timed per kernel with HIP events."""
+    import orion_hip as oh
+    from paged_cases import cfg3
+
+    case = cfg3()
+    n = len(case.positions)
+    kv = oh.kv_layout(1, case.num_blocks, case.bs, case.hkv, case.d, oh.BF16)
+    bufs = [be.to_device(case.arena_device_bytes()), be.to_device(case.q),
+            be.to_device(case.row_start), be.to_device(case.row_count),
+            be.to_device(case.first_pos), be.to_device(case.bt_offsets),
+            be.to_device(case.bt_ids), be.alloc(n * case.hq * case.d * 4)]
+    arena, dq, drs, drc, dfp, dbo, dbi, dout = bufs
+    flops = case.flops()
+    res = {"workload": "chunked-prefill attention, config 3: 8 seqs x 512-token chunks, prefix "
+                       "U[0,7680], 32q/8kv, head_dim 128, bf16, block 16",
+           "flops_per_call": flops}
+    for hilo in (False, True):
+        def call():
+            oh.paged_attention_prefill(be, kv, arena.ptr, 0, dq.ptr, case.hq, case.S, drs.ptr,
+                                       drc.ptr, dfp.ptr, dbo.ptr, dbi.ptr, 512,
+                                       int(case.positions.max()), dout.ptr, hilo=hilo)
+        for _ in range(warmup):
+            call()
+        be.kernel_timing(True)
+        for _ in range(steps):
+            call()
+        tot, cnt = be.kernel_timing_read(be.K_PREFILL)
+        be.kernel_timing(False)
+        ms = tot / cnt
+        tf = flops / (ms * 1e-3) / 1e12
+        key = "hilo" if hilo else "bf16"
+        res[key] = {"ms": round(ms, 4), "tflops": round(tf, 1),
+                    "frac_of_bf16_peak": round(tf / BF16_PEAK_TFLOPS, 4)}
+        if not hilo:
+            got = dout.download(np.float32, (n, case.hq * case.d))
+            rows = np.array([0, 511, 512 * 3 + 100, n - 1])
+            res[key]["max_abs_err_vs_oracle"] = float(
+                np.abs(got[rows] - case.oracle_rows(rows)).max())
+    res["operands"] = ("bf16: Q and softmax weights rounded to bf16 (MFMA rate); hilo: each as "
+                       "a hi+lo bf16 pair (2x MFMA work)")
+    for b in bufs:
+        b.free()
+    return res
 
 
 def algorithmic_bytes(case):
@@ -183,6 +245,9 @@ def main():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU oracle baseline")
     ap.add_argument("--no-e2e", action="store_true", help="skip the config-4 decode step")
+    ap.add_argument("--no-prefill", action="store_true", help="skip the config-3 prefill kernel")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="also run 3 plain 1 GiB device copies (PMC byte-counter scale)")
     a = ap.parse_args()
     if a.gpus != 1:
         print(f"bench.py measures one GPU only (this build is single-GPU); --gpus {a.gpus} "
@@ -220,6 +285,16 @@ def main():
     ms = be.timer_stop()
     be.synchronize()
     ms_per_step = ms / a.steps
+    # The dominant kernel alone (split-K pass; the merge kernel is separate),
+    # HIP events on the library's stream around each launch.
+    be.kernel_timing(True)
+    for _ in range(a.steps):
+        step()
+    split_ms, split_n = be.kernel_timing_read(be.K_DECODE_SPLIT)
+    merge_ms, merge_n = be.kernel_timing_read(be.K_DECODE_MERGE)
+    be.kernel_timing(False)
+    split_avg = split_ms / max(split_n, 1)
+    merge_avg = merge_ms / max(merge_n, 1)
 
     # correctness spot-check of the measured output (cheap: 4 rows)
     got = dout.download(np.float32, (case.S, case.hq * case.d))
@@ -229,6 +304,7 @@ def main():
 
     nbytes = algorithmic_bytes(case)
     gbs = nbytes / (ms_per_step * 1e-3) / 1e9
+    kern_gbs = nbytes / (split_avg * 1e-3) / 1e9
     result = {
         "metric": "paged-attn decode HBM GB/s (% peak) at Llama-3-8B shape; decode tokens/sec",
         "value": round(gbs, 1),
@@ -255,16 +331,32 @@ def main():
         },
         "roofline": {
             "bound": "hbm",
-            "achieved": round(gbs, 1),
+            "kernel": "paged_decode_mfma2_kernel (split-K pass)",
+            "achieved": round(kern_gbs, 1),
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
-            "frac": round(gbs / HBM_PEAK_GBS, 4),
-            "traffic": None,
+            "frac": round(kern_gbs / HBM_PEAK_GBS, 4),
+            "traffic": measured_traffic(),
+            "kernel_ms": round(split_avg, 5),
+            "merge_kernel_ms": round(merge_avg, 5),
         },
         "max_abs_err_vs_oracle": max_err,
     }
     if not a.no_cpu:
         result["cpu_baseline"] = cpu_baseline(case)
+    for b in (arena, dq, dpos, drs, dbo, dbi, dout):
+        b.free()
+    plan.close()
+    if not a.no_prefill:
+        result["prefill_cfg3"] = prefill_cfg3(be)
+    if a.copy_calibration:
+        # A plain device-to-device copy of known size, for scaling the PMC
+        # byte counters (rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE).
+        src, dst = be.alloc(1 << 30), be.alloc(1 << 30)
+        for _ in range(3):
+            be.memcpy_d2d(dst.ptr, src.ptr, 1 << 30)
+        be.synchronize()
+        result["copy_calibration_bytes"] = 1 << 30
     be.close()
     if not a.no_e2e:
         result["decode_e2e"] = decode_e2e(cpu=not a.no_cpu)

@@ -1072,7 +1072,8 @@ hipError_t launch_paged_decode(hipStream_t st, const KvGeom& kv, const void* are
                                const float* q, int64_t rows, int64_t hq,
                                const uint32_t* positions, const int32_t* row_seq,
                                const int64_t* bt_off, const uint32_t* bt_ids,
-                               const DecodePlanDev& plan, float* out) {
+                               const DecodePlanDev& plan, float* out,
+                               DecodePhase phase) {
   if (rows == 0 || plan.num_work == 0) return hipSuccess;
   const int64_t hkv = kv.num_kv_heads, D = kv.head_dim;
   const int G = (int)(hq / hkv);
@@ -1081,6 +1082,10 @@ hipError_t launch_paged_decode(hipStream_t st, const KvGeom& kv, const void* are
     return hipErrorInvalidValue;
   float* ws_o = plan.ws;
   float* ws_ml = ws_o ? ws_o + rows * hq * ms * D : nullptr;
+  if (phase == DecodePhase::kMerge) {
+    if (ms <= 1) return hipSuccess;
+    return launch_combine(st, D, rows, hq, positions, plan, C, ms, ws_o, ws_ml, out);
+  }
   int bs_log2 = 0;
   while ((1 << bs_log2) < kv.block_size) ++bs_log2;
   const int64_t slot_stride = hkv * D;
@@ -1131,7 +1136,7 @@ hipError_t launch_paged_decode(hipStream_t st, const KvGeom& kv, const void* are
         return hipErrorInvalidValue;
 #undef ORION_MFMA2
 #undef ORION_MFMA2_NS
-      if (e != hipSuccess || ms == 1) return e;
+      if (e != hipSuccess || ms == 1 || phase == DecodePhase::kSplit) return e;
       return launch_combine(st, D, rows, hq, positions, plan, C, ms, ws_o, ws_ml, out);
     }
     if (loads_only && D == 128 && G == 4 && big) {
@@ -1162,7 +1167,7 @@ hipError_t launch_paged_decode(hipStream_t st, const KvGeom& kv, const void* are
     else
       return hipErrorInvalidValue;
   }
-  if (e != hipSuccess || ms == 1) return e;
+  if (e != hipSuccess || ms == 1 || phase == DecodePhase::kSplit) return e;
   return launch_combine(st, D, rows, hq, positions, plan, C, ms, ws_o, ws_ml, out);
 }
 

@@ -46,11 +46,15 @@ void build_decode_plan(const uint32_t* positions, const int32_t* row_seq,
                        int64_t hkv, int64_t block_size, int64_t wave_slots,
                        const uint8_t* skip_rows, DecodePlanHost* plan);
 size_t decode_workspace_bytes(int64_t rows, int64_t hq, int64_t D, int64_t max_splits);
+// Which launches of a decode pass to issue (the merge only runs when the
+// plan splits some row).
+enum class DecodePhase { kBoth, kSplit, kMerge };
 hipError_t launch_paged_decode(hipStream_t st, const KvGeom& kv, const void* arena, int64_t layer,
                                const float* q, int64_t rows, int64_t hq,
                                const uint32_t* positions, const int32_t* row_seq,
                                const int64_t* bt_off, const uint32_t* bt_ids,
-                               const DecodePlanDev& plan, float* out);
+                               const DecodePlanDev& plan, float* out,
+                               DecodePhase phase = DecodePhase::kBoth);
 
 hipError_t launch_paged_prefill(hipStream_t st, const KvGeom& kv, const void* arena,
                                 int64_t layer, const float* q, int64_t hq, int64_t num_seqs,

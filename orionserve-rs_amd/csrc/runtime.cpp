@@ -141,6 +141,30 @@ struct orion_hip_device {
   hipEvent_t ev_start = nullptr, ev_stop = nullptr;
   std::string name;
   int64_t wave_slots = 2048;  // resident decode waves: CUs x 4 SIMDs x 2
+  // Per-kernel timing (orion_hip_kernel_timing): event pairs per kernel
+  // index, resolved when read.
+  bool ktiming = false;
+  std::vector<std::pair<hipEvent_t, hipEvent_t>> kevents[3];
+  std::vector<hipEvent_t> event_pool;
+  hipEvent_t take_event() {
+    if (!event_pool.empty()) {
+      hipEvent_t e = event_pool.back();
+      event_pool.pop_back();
+      return e;
+    }
+    hipEvent_t e = nullptr;
+    if (hipEventCreate(&e) != hipSuccess) return nullptr;
+    return e;
+  }
+  void recycle_events() {
+    for (auto& v : kevents) {
+      for (auto& p : v) {
+        event_pool.push_back(p.first);
+        event_pool.push_back(p.second);
+      }
+      v.clear();
+    }
+  }
 };
 
 struct orion_hip_decode_plan {
@@ -268,6 +292,8 @@ ORION_EXPORT void orion_hip_device_close(orion_hip_device* dev) {
   (void)hipStreamSynchronize(dev->stream);
   (void)hipEventDestroy(dev->ev_start);
   (void)hipEventDestroy(dev->ev_stop);
+  dev->recycle_events();
+  for (hipEvent_t e : dev->event_pool) (void)hipEventDestroy(e);
   (void)hipStreamDestroy(dev->stream);
   delete dev;
 }
@@ -344,6 +370,49 @@ ORION_EXPORT int orion_hip_timer_stop(orion_hip_device* dev, float* ms) {
   HIP_TRY("timer", hipEventSynchronize(dev->ev_stop));
   HIP_TRY("timer", hipEventElapsedTime(ms, dev->ev_start, dev->ev_stop));
   return ORION_HIP_OK;
+}
+
+ORION_EXPORT int orion_hip_kernel_timing(orion_hip_device* dev, int enable) {
+  HIP_TRY("kernel_timing", hipSetDevice(dev->ordinal));
+  HIP_TRY("kernel_timing", hipStreamSynchronize(dev->stream));
+  dev->recycle_events();
+  dev->ktiming = enable != 0;
+  return ORION_HIP_OK;
+}
+
+ORION_EXPORT int orion_hip_kernel_timing_read(orion_hip_device* dev, int kernel, double* total_ms,
+                                              int64_t* calls) {
+  const char* st = "kernel_timing";
+  if (kernel < 0 || kernel > 2) return internal(st, "kernel index %d is not 0, 1 or 2", kernel);
+  double sum = 0.0;
+  for (auto& p : dev->kevents[kernel]) {
+    HIP_TRY(st, hipEventSynchronize(p.second));
+    float ms = 0.f;
+    HIP_TRY(st, hipEventElapsedTime(&ms, p.first, p.second));
+    sum += ms;
+  }
+  *total_ms = sum;
+  *calls = (int64_t)dev->kevents[kernel].size();
+  return ORION_HIP_OK;
+}
+
+// Records a (start, stop) event pair for kernel index k around `launch` when
+// per-kernel timing is on.
+template <typename F>
+static hipError_t timed_launch(orion_hip_device* dev, int k, F&& launch) {
+  if (!dev->ktiming) return launch();
+  hipEvent_t a = dev->take_event(), b = dev->take_event();
+  if (!a || !b) return hipErrorOutOfMemory;
+  hipError_t e = hipEventRecord(a, dev->stream);
+  if (e == hipSuccess) e = launch();
+  if (e == hipSuccess) e = hipEventRecord(b, dev->stream);
+  if (e != hipSuccess) {
+    dev->event_pool.push_back(a);
+    dev->event_pool.push_back(b);
+    return e;
+  }
+  dev->kevents[k].push_back({a, b});
+  return hipSuccess;
 }
 
 // ---------------------------------------------------------------------------
@@ -1059,9 +1128,24 @@ ORION_EXPORT int orion_hip_paged_attention_decode(
       plan->block_size != g.block_size)
     return internal(st, "decode plan does not match this call's geometry");
   HIP_TRY(st, hipSetDevice(dev->ordinal));
-  HIP_TRY(st, launch_paged_decode(dev->stream, g, d_arena, layer, d_q, num_rows, num_q_heads,
-                                  d_positions, d_row_seq, d_bt_offsets, d_bt_ids, plan->view(),
-                                  d_out));
+  if (!dev->ktiming) {
+    HIP_TRY(st, launch_paged_decode(dev->stream, g, d_arena, layer, d_q, num_rows, num_q_heads,
+                                    d_positions, d_row_seq, d_bt_offsets, d_bt_ids, plan->view(),
+                                    d_out));
+    return ORION_HIP_OK;
+  }
+  // Timed: the split-K kernel and the merge kernel as separate launches.
+  DecodePlanDev pv = plan->view();
+  HIP_TRY(st, timed_launch(dev, 0, [&] {
+            return launch_paged_decode(dev->stream, g, d_arena, layer, d_q, num_rows, num_q_heads,
+                                       d_positions, d_row_seq, d_bt_offsets, d_bt_ids, pv, d_out,
+                                       DecodePhase::kSplit);
+          }));
+  HIP_TRY(st, timed_launch(dev, 1, [&] {
+            return launch_paged_decode(dev->stream, g, d_arena, layer, d_q, num_rows, num_q_heads,
+                                       d_positions, d_row_seq, d_bt_offsets, d_bt_ids, pv, d_out,
+                                       DecodePhase::kMerge);
+          }));
   return ORION_HIP_OK;
 }
 
@@ -1077,9 +1161,12 @@ ORION_EXPORT int orion_hip_paged_attention_prefill(
   if (g.num_kv_heads <= 0 || num_q_heads % g.num_kv_heads)
     return internal(st, "query heads cannot be grouped over kv heads");
   HIP_TRY(st, hipSetDevice(dev->ordinal));
-  HIP_TRY(st, launch_paged_prefill(dev->stream, g, d_arena, layer, d_q, num_q_heads, num_seqs,
-                                   d_row_start, d_row_count, d_first_pos, d_bt_offsets, d_bt_ids,
-                                   max_rows, max_position, hilo != 0, d_out));
+  HIP_TRY(st, timed_launch(dev, 2, [&] {
+            return launch_paged_prefill(dev->stream, g, d_arena, layer, d_q, num_q_heads,
+                                        num_seqs, d_row_start, d_row_count, d_first_pos,
+                                        d_bt_offsets, d_bt_ids, max_rows, max_position,
+                                        hilo != 0, d_out);
+          }));
   return ORION_HIP_OK;
 }
 

@@ -39,6 +39,7 @@ EXPORTED = [
     "orion_hip_mem_info", "orion_hip_synchronize", "orion_hip_supports_dtype",
     "orion_hip_alloc", "orion_hip_free", "orion_hip_memcpy_h2d", "orion_hip_memcpy_d2h",
     "orion_hip_memcpy_d2d", "orion_hip_memset", "orion_hip_timer_start", "orion_hip_timer_stop",
+    "orion_hip_kernel_timing", "orion_hip_kernel_timing_read",
     "orion_hip_model_create", "orion_hip_model_destroy", "orion_hip_model_upload_weight",
     "orion_hip_model_init_synthetic", "orion_hip_synthetic_value",
     "orion_hip_model_download_weight", "orion_hip_model_forward", "orion_hip_model_kv_read",
@@ -129,6 +130,8 @@ def load_library(path: str = LIB_PATH) -> C.CDLL:
         "orion_hip_memset": ([vp, vp, C.c_int, sz], C.c_int),
         "orion_hip_timer_start": ([vp], C.c_int),
         "orion_hip_timer_stop": ([vp, P(f32)], C.c_int),
+        "orion_hip_kernel_timing": ([vp, C.c_int], C.c_int),
+        "orion_hip_kernel_timing_read": ([vp, C.c_int, P(C.c_double), P(i64)], C.c_int),
         "orion_hip_model_create": ([vp, P(ModelDesc), P(vp)], C.c_int),
         "orion_hip_model_destroy": ([vp], None),
         "orion_hip_model_upload_weight": ([vp, C.c_int, C.c_int, vp, C.c_int, sz], C.c_int),
@@ -268,6 +271,9 @@ class HipBackend:
         arr = np.ascontiguousarray(arr)
         return self.alloc(arr.nbytes).upload(arr)
 
+    def memcpy_d2d(self, dst: int, src: int, nbytes: int) -> None:
+        _check(self.lib.orion_hip_memcpy_d2d(self.handle, dst, src, nbytes))
+
     def timer_start(self) -> None:
         _check(self.lib.orion_hip_timer_start(self.handle))
 
@@ -275,6 +281,20 @@ class HipBackend:
         ms = C.c_float()
         _check(self.lib.orion_hip_timer_stop(self.handle, C.byref(ms)))
         return ms.value
+
+    # Kernel indices for kernel_timing_read.
+    K_DECODE_SPLIT, K_DECODE_MERGE, K_PREFILL = 0, 1, 2
+
+    def kernel_timing(self, enable: bool) -> None:
+        """Start (and reset) or stop per-kernel event timing of the attention ops."""
+        _check(self.lib.orion_hip_kernel_timing(self.handle, 1 if enable else 0))
+
+    def kernel_timing_read(self, kernel: int):
+        """(total milliseconds, launches) recorded for `kernel` since enabling."""
+        ms, n = C.c_double(), C.c_int64()
+        _check(self.lib.orion_hip_kernel_timing_read(self.handle, kernel, C.byref(ms),
+                                                     C.byref(n)))
+        return ms.value, n.value
 
     def close(self) -> None:
         if self.handle:
