@@ -43,16 +43,16 @@ def measured_traffic():
     return int(m.group(1)) if m else None
 
 
-def prefill_cfg3(be, steps=20, warmup=3):
+def prefill_cfg3(be, steps=20, warmup=3, head_major=False):
     """chunked-prefill causal attention over the paged
     cache as an MFMA contraction (8 seqs x 512-token chunks on prefixes
     U[0,7680], 32q/8kv, d 128, bf16).  Timed per kernel with HIP events."""
     import orion_hip as oh
     from paged_cases import cfg3
 
-    case = cfg3()
+    case = cfg3(head_major=head_major)
     n = len(case.positions)
-    kv = oh.kv_layout(1, case.num_blocks, case.bs, case.hkv, case.d, oh.BF16)
+    kv = case.kv_layout()
     bufs = [be.to_device(case.arena_device_bytes()), be.to_device(case.q),
             be.to_device(case.row_start), be.to_device(case.row_count),
             be.to_device(case.first_pos), be.to_device(case.bt_offsets),
@@ -246,6 +246,8 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU oracle baseline")
     ap.add_argument("--no-e2e", action="store_true", help="skip the config-4 decode step")
     ap.add_argument("--no-prefill", action="store_true", help="skip the config-3 prefill kernel")
+    ap.add_argument("--kv-layout", choices=["head-major", "reference"], default="reference",
+                    help="block-internal order of the KV arena (reference = attention.rs order)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="also run 3 plain 1 GiB device copies (PMC byte-counter scale)")
     a = ap.parse_args()
@@ -257,9 +259,10 @@ def main():
     import orion_hip as oh
     from paged_cases import cfg2
 
-    case = cfg2()
+    head_major = a.kv_layout == "head-major"
+    case = cfg2(head_major=head_major)
     be = oh.HipBackend(0)
-    kv = oh.kv_layout(1, case.num_blocks, case.bs, case.hkv, case.d, oh.BF16)
+    kv = case.kv_layout()
     arena = be.to_device(case.arena_device_bytes())
     dq = be.to_device(case.q)
     dpos = be.to_device(case.positions)
@@ -326,6 +329,7 @@ def main():
             "sum_context": int(case.ctxs.sum()),
             "algorithmic_bytes_per_step": nbytes,
             "kv_dtype": "bf16",
+            "kv_layout": a.kv_layout,
             "accumulate": "f32",
             "decode_plan": plan.info(),
         },
@@ -348,7 +352,7 @@ def main():
         b.free()
     plan.close()
     if not a.no_prefill:
-        result["prefill_cfg3"] = prefill_cfg3(be)
+        result["prefill_cfg3"] = prefill_cfg3(be, head_major=head_major)
     if a.copy_calibration:
         # A plain device-to-device copy of known size, for scaling the PMC
         # byte counters (rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE).

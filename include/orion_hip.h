@@ -213,8 +213,8 @@ int orion_hip_model_kv_read(orion_hip_model* model, int64_t layer, uint32_t bloc
 int orion_hip_model_kv_write(orion_hip_model* model, int64_t layer, uint32_t block, int64_t slot,
                              int64_t head, int is_value, const float* vec, int64_t len);
 
-/* Device address and byte size of the model's KV arena, layout
- * [layer][block][k|v][slot][kv_head][head_dim] (attention.rs:11-22). */
+/* Device address and byte size of the model's KV arena; its geometry and
+ * block-internal layout come from orion_hip_model_kv_layout. */
 int orion_hip_model_kv_arena(orion_hip_model* model, void** d_arena, size_t* bytes);
 
 /* ---------------------------------------------------------------------------
@@ -222,7 +222,11 @@ int orion_hip_model_kv_arena(orion_hip_model* model, void** d_arena, size_t* byt
  * These are the per-kernel validation gate of docs/cuda.md:80-116.
  * ------------------------------------------------------------------------- */
 
-/* Geometry of a paged KV arena (KvStore, attention.rs:34-62). */
+/* Geometry of a paged KV arena (KvStore, attention.rs:34-62).  head_major = 0
+ * is the reference layout [layer][block][k|v][slot][kv_head][dim]
+ * (attention.rs:11-22); head_major = 1 stores each block as
+ * [kv_head][k|v][slot][dim], so one head's K (or V) of a block is one
+ * contiguous block_size x dim run.  Block ids index either the same way. */
 typedef struct orion_hip_kv_layout {
   int64_t num_layers;
   int64_t num_blocks;
@@ -230,7 +234,12 @@ typedef struct orion_hip_kv_layout {
   int64_t num_kv_heads;
   int64_t head_dim;
   int32_t dtype; /* ORION_DTYPE_F32 or ORION_DTYPE_BF16 */
+  int32_t head_major;
 } orion_hip_kv_layout;
+
+/* Geometry and layout of a model's KV arena (KvStore::new, attention.rs:45-62),
+ * for use with the op-level entry points on orion_hip_model_kv_arena. */
+int orion_hip_model_kv_layout(orion_hip_model* model, orion_hip_kv_layout* out);
 
 /* Work plan for paged decode attention over one batch of query rows.  Built
  * on the host from host copies of the rows' positions, their sequence index

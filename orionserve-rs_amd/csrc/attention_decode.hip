@@ -68,7 +68,8 @@ struct KvVec<uint16_t> {
 template <typename T, int D, int G>
 __device__ __forceinline__ void decode_wave_valu(
     const T* __restrict__ kv_layer, int64_t blk_stride, int64_t v_off, int64_t slot_stride,
-    int bs_log2, int num_q_heads, const float* __restrict__ q, const uint32_t* __restrict__ tbl,
+    int64_t head_stride, int bs_log2, int num_q_heads, const float* __restrict__ q,
+    const uint32_t* __restrict__ tbl,
     int max_splits, float scale, float* __restrict__ out, float* __restrict__ ws_o,
     float* __restrict__ ws_ml, int row, int kvh, int start, int end, int split, int nsplit) {
   constexpr int EPL = KvVec<T>::EPL;
@@ -106,7 +107,7 @@ __device__ __forceinline__ void decode_wave_valu(
   const int nblk = ((end - 1) >> bs_log2) - first_blk + 1;
   const int my_blk = lane < nblk ? (int)tbl[lane] : 0;
 
-  const T* kbase = kv_layer + (int64_t)kvh * D + c * EPL;
+  const T* kbase = kv_layer + (int64_t)kvh * head_stride + c * EPL;
 
   float m[G], l[G], o[G][EPL];
 #pragma unroll
@@ -225,7 +226,8 @@ __device__ __forceinline__ void decode_wave_valu(
 template <typename T, int D, int G>
 __global__ void __launch_bounds__(256)
     paged_decode_kernel(const T* __restrict__ kv_layer, int64_t blk_stride, int64_t v_off,
-                        int64_t slot_stride, int bs_log2, int num_kv_heads, int num_q_heads,
+                        int64_t slot_stride, int64_t head_stride, int bs_log2, int num_kv_heads,
+                        int num_q_heads,
                         const DecodeWork* __restrict__ work, int num_work, const float* __restrict__ q,
                         const uint32_t* __restrict__ positions, const int32_t* __restrict__ row_seq,
                         const int64_t* __restrict__ bt_off, const uint32_t* __restrict__ bt_ids,
@@ -235,277 +237,10 @@ __global__ void __launch_bounds__(256)
   if (w >= num_work) return;
   const DecodeWork wk = work[w];
   const int row = wk.item / num_kv_heads, kvh = wk.item - row * num_kv_heads;
-  decode_wave_valu<T, D, G>(kv_layer, blk_stride, v_off, slot_stride, bs_log2, num_q_heads, q,
+  decode_wave_valu<T, D, G>(kv_layer, blk_stride, v_off, slot_stride, head_stride, bs_log2,
+                            num_q_heads, q,
                             bt_ids + wk.tbl_off, max_splits, scale, out, ws_o, ws_ml, row, kvh,
                             wk.start, wk.end, wk.start / chunk, wk.nsplit);
-}
-
-// bf16-KV decode kernel with Q.K^T on MFMA.
-//
-// Each iteration covers NT tiles of 16 tokens.  Per tile a wave computes
-// S^T[head, token] = Q[G, D] . K^T[D, 16] with v_mfma_f32_16x16x32_bf16: the A
-// operand is the query group (rows = heads, zero rows past G) split into hi +
-// lo bf16 terms, so the product keeps ~16 bits of each f32 query element; the
-// B operand is the K tile itself, lane l holding token l%16, dims
-// (l/16)*8 + 32j .. +8, i.e. one 16-byte load straight from the cache.  The NT
-// tiles use independent accumulators.  Scores land as lane l: token l%16,
-// heads 4*(l/16)+i; the running max is wave-uniform per head (reduced over the
-// 16 token lanes once per iteration), and the softmax weights reach the P.V
-// lanes through a (16*NT) x G LDS tile.  P.V runs on VALU with lane (t, c) =
-// (token group, 8-dim chunk), the layout in which a V load is one coalesced
-// 16-byte access.
-//
-// Software pipeline: the next iteration's K loads are issued as soon as this
-// iteration's MFMAs have consumed K, and the next V loads as soon as P.V has
-// consumed V, so K(i+1) streams in under the softmax and P.V of step i and
-// V(i+1) under the next Q.K^T.
-template <int D, int G, int NS, bool BIG_BLOCKS, bool LOADS_ONLY = false>
-__device__ __forceinline__ void decode_wave_mfma(
-    const uint16_t* __restrict__ kv_layer, uint32_t blk_stride, uint32_t v_off,
-    uint32_t slot_stride, int bs_log2, int num_q_heads, const float* __restrict__ q,
-    const uint32_t* __restrict__ tbl, int max_splits, float scale, float* __restrict__ out,
-    float* __restrict__ ws_o, float* __restrict__ ws_ml, float* P, float* A, float* Lr, int row,
-    int kvh, int start, int end, int split, int nsplit) {
-  constexpr int KCH = D / 32;       // MFMA k-steps over the head dim
-  constexpr int CH = D / 8;         // P.V lanes per token (8 bf16 each)
-  constexpr int TPW = 64 / CH;      // tokens per V wave load
-  constexpr int RV = 16 / TPW;      // V loads per lane per 16-token step
-  constexpr int GP = (G + 3) & ~3;  // heads padded to the MFMA row quad
-  static_assert(G <= 16 && TPW <= 16 && (16 % TPW) == 0, "unsupported shape");
-
-  const int lane = threadIdx.x & 63;
-  const int bs_mask = (1 << bs_log2) - 1;
-
-  // ---- block-table slice of this chunk, one entry per lane ----
-  const int first_blk = start >> bs_log2;
-  const int nblk = ((end - 1) >> bs_log2) - first_blk + 1;
-  const int my_blk = lane < nblk ? (int)tbl[lane] : 0;
-
-  const uint16_t* base_k = kv_layer + (uint32_t)kvh * D;
-  const int kt = lane & 15;        // K token within the step (MFMA column)
-  const int kd = (lane >> 4) * 8;  // K dims chunk
-  const int vt = lane / CH;        // V token group
-  const int vc = lane % CH;        // V dims chunk
-
-  // Ring of NS register stages, each one 16-token step of K and V.
-  uint4 kr[NS][KCH], vr[NS][RV];
-  // Tokens past `end` are clamped to the last valid one; their weight is 0.
-  auto issue = [&](uint4 (&ks)[KCH], uint4 (&vs)[RV], int b) {
-    const int jk = min(b + kt, end - 1);
-    if constexpr (BIG_BLOCKS) {
-      // b is 16-aligned and blocks hold >= 16 tokens: one block per step.
-      const int blk = __builtin_amdgcn_readlane(my_blk, (b >> bs_log2) - first_blk);
-      const uint16_t* bb = base_k + (uint32_t)blk * blk_stride;
-      const uint16_t* kp = bb + (uint32_t)(jk & bs_mask) * slot_stride + kd;
-#pragma unroll
-      for (int c = 0; c < KCH; ++c) ks[c] = *reinterpret_cast<const uint4*>(kp + 32 * c);
-#pragma unroll
-      for (int r = 0; r < RV; ++r) {
-        const int jv = min(b + r * TPW + vt, end - 1);
-        vs[r] = *reinterpret_cast<const uint4*>(bb + (uint32_t)(jv & bs_mask) * slot_stride +
-                                                v_off + vc * 8);
-      }
-    } else {
-      const int bk = __shfl(my_blk, (jk >> bs_log2) - first_blk);
-      const uint16_t* kp =
-          base_k + (uint32_t)bk * blk_stride + (uint32_t)(jk & bs_mask) * slot_stride + kd;
-#pragma unroll
-      for (int c = 0; c < KCH; ++c) ks[c] = *reinterpret_cast<const uint4*>(kp + 32 * c);
-#pragma unroll
-      for (int r = 0; r < RV; ++r) {
-        const int jv = min(b + r * TPW + vt, end - 1);
-        const int bv = __shfl(my_blk, (jv >> bs_log2) - first_blk);
-        vs[r] = *reinterpret_cast<const uint4*>(base_k + (uint32_t)bv * blk_stride +
-                                                (uint32_t)(jv & bs_mask) * slot_stride + v_off +
-                                                vc * 8);
-      }
-    }
-  };
-
-  // ---- query group as the MFMA A operand (hi/lo bf16) ----
-  bf16x8 qa_hi[KCH], qa_lo[KCH];
-  {
-    const int h = lane & 15;
-    const float* qp = q + ((int64_t)row * num_q_heads + (int64_t)kvh * G + h) * D + kd;
-#pragma unroll
-    for (int j = 0; j < KCH; ++j) {
-      float a[8];
-      if (h < G) {
-        const float4 x0 = *reinterpret_cast<const float4*>(qp + 32 * j);
-        const float4 x1 = *reinterpret_cast<const float4*>(qp + 32 * j + 4);
-        a[0] = x0.x; a[1] = x0.y; a[2] = x0.z; a[3] = x0.w;
-        a[4] = x1.x; a[5] = x1.y; a[6] = x1.z; a[7] = x1.w;
-      } else {
-#pragma unroll
-        for (int e = 0; e < 8; ++e) a[e] = 0.f;
-      }
-      uint16_t hb[8], lb[8];
-#pragma unroll
-      for (int e = 0; e < 8; ++e) split_bf16(a[e], hb[e], lb[e]);
-      uint4 hv, lv;
-      hv.x = hb[0] | ((uint32_t)hb[1] << 16); hv.y = hb[2] | ((uint32_t)hb[3] << 16);
-      hv.z = hb[4] | ((uint32_t)hb[5] << 16); hv.w = hb[6] | ((uint32_t)hb[7] << 16);
-      lv.x = lb[0] | ((uint32_t)lb[1] << 16); lv.y = lb[2] | ((uint32_t)lb[3] << 16);
-      lv.z = lb[4] | ((uint32_t)lb[5] << 16); lv.w = lb[6] | ((uint32_t)lb[7] << 16);
-      qa_hi[j] = __builtin_bit_cast(bf16x8, hv);
-      qa_lo[j] = __builtin_bit_cast(bf16x8, lv);
-    }
-  }
-
-  float m[4], lsum[4];
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    m[i] = -INFINITY;
-    lsum[i] = 0.f;
-  }
-  float o[G][8];
-#pragma unroll
-  for (int g = 0; g < G; ++g)
-#pragma unroll
-    for (int e = 0; e < 8; ++e) o[g][e] = 0.f;
-
-  const int hrow = (lane >> 4) * 4;  // first head of this lane's score quad
-
-  // One 16-token step on stage registers (ks, vs).
-  auto compute = [&](const uint4 (&ks)[KCH], const uint4 (&vs)[RV], int b) {
-    // S^T = Q . K^T; hi and lo terms in independent accumulators.
-    f32x4 ah = {0.f, 0.f, 0.f, 0.f}, al4 = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int c = 0; c < KCH; ++c) {
-      const bf16x8 kb = __builtin_bit_cast(bf16x8, ks[c]);
-      ah = __builtin_amdgcn_mfma_f32_16x16x32_bf16(qa_hi[c], kb, ah, 0, 0, 0);
-      al4 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(qa_lo[c], kb, al4, 0, 0, 0);
-    }
-    const bool kvalid = b + kt < end;
-    float p[4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const float s = kvalid ? (ah[i] + al4[i]) * scale : -INFINITY;
-      const float m_new = fmaxf(m[i], group_max<16>(s));
-      const float alpha = __expf(m[i] - m_new);
-      p[i] = __expf(s - m_new);
-      lsum[i] = lsum[i] * alpha + p[i];
-      m[i] = m_new;
-      if (kt == 0 && hrow < GP) A[hrow + i] = alpha;
-    }
-    if (hrow < GP) *reinterpret_cast<float4*>(P + kt * GP + hrow) = make_float4(p[0], p[1], p[2], p[3]);
-    wave_lds_sync();
-
-    // P.V on VALU.
-    float alv[GP];
-#pragma unroll
-    for (int g4 = 0; g4 < GP; g4 += 4) {
-      const float4 a4 = *reinterpret_cast<const float4*>(A + g4);
-      alv[g4] = a4.x; alv[g4 + 1] = a4.y; alv[g4 + 2] = a4.z; alv[g4 + 3] = a4.w;
-    }
-    bool rescale = false;
-#pragma unroll
-    for (int g = 0; g < G; ++g) rescale |= alv[g] != 1.0f;
-    if (rescale) {
-#pragma unroll
-      for (int g = 0; g < G; ++g)
-#pragma unroll
-        for (int e = 0; e < 8; ++e) o[g][e] *= alv[g];
-    }
-#pragma unroll
-    for (int r = 0; r < RV; ++r) {
-      float pw[GP];
-      const float* pr = P + (r * TPW + vt) * GP;
-#pragma unroll
-      for (int g4 = 0; g4 < GP; g4 += 4) {
-        const float4 p4 = *reinterpret_cast<const float4*>(pr + g4);
-        pw[g4] = p4.x; pw[g4 + 1] = p4.y; pw[g4 + 2] = p4.z; pw[g4 + 3] = p4.w;
-      }
-      const uint4 v = vs[r];
-      const float vf[8] = {bf16lo(v.x), bf16hi(v.x), bf16lo(v.y), bf16hi(v.y),
-                           bf16lo(v.z), bf16hi(v.z), bf16lo(v.w), bf16hi(v.w)};
-#pragma unroll
-      for (int g = 0; g < G; ++g)
-#pragma unroll
-        for (int e = 0; e < 8; ++e) o[g][e] += pw[g] * vf[e];
-    }
-    wave_lds_sync();
-  };
-
-  // Software pipeline: stage s is computed while stages s+1 .. s+NS-1 load.
-  // Loads are issued unconditionally, with token indices clamped into the
-  // chunk (steps past the end re-read the last rows, which hit in cache), so
-  // no load sits under a branch and the compiler's wait counts stay exact:
-  // computing a stage waits only for that stage's loads.
-  const int nsteps = (end - start + 15) >> 4;
-  auto step_base = [&](int i) { return min(start + 16 * i, end - 1) & ~15; };
-#pragma unroll
-  for (int s = 0; s < NS - 1; ++s) issue(kr[s], vr[s], step_base(s));
-  uint32_t fold = 0;  // LOADS_ONLY measurement variant: consume the data trivially
-  int i = 0;
-  for (; i + NS <= nsteps; i += NS) {
-#pragma unroll
-    for (int s = 0; s < NS; ++s) {
-      issue(kr[(s + NS - 1) % NS], vr[(s + NS - 1) % NS], step_base(i + s + NS - 1));
-      if constexpr (!LOADS_ONLY) compute(kr[s], vr[s], start + 16 * (i + s));
-    }
-  }
-  for (; i < nsteps; i += NS) {
-#pragma unroll
-    for (int s = 0; s < NS; ++s) {
-      issue(kr[(s + NS - 1) % NS], vr[(s + NS - 1) % NS], step_base(i + s + NS - 1));
-      if (i + s < nsteps) {
-        if constexpr (LOADS_ONLY) {
-#pragma unroll
-          for (int c = 0; c < KCH; ++c) fold ^= kr[s][c].x ^ kr[s][c].y ^ kr[s][c].z ^ kr[s][c].w;
-#pragma unroll
-          for (int r = 0; r < RV; ++r) fold ^= vr[s][r].x ^ vr[s][r].y ^ vr[s][r].z ^ vr[s][r].w;
-        } else {
-          compute(kr[s], vr[s], start + 16 * (i + s));
-        }
-      }
-    }
-  }
-  if constexpr (LOADS_ONLY) {
-    if (fold == 0x9e3779b9u) out[0] = 0.f;
-    return;
-  }
-
-  // Row sums over the 16 token lanes; publish (m, l) per head through LDS.
-#pragma unroll
-  for (int i = 0; i < 4; ++i) lsum[i] = group_sum<16>(lsum[i]);
-  if (hrow < GP && kt == 0) {
-    *reinterpret_cast<float4*>(Lr + hrow) = make_float4(lsum[0], lsum[1], lsum[2], lsum[3]);
-    *reinterpret_cast<float4*>(A + hrow) = make_float4(m[0], m[1], m[2], m[3]);
-  }
-  // Sum the token groups of P.V (lanes vc, vc + CH, ...).
-#pragma unroll
-  for (int g = 0; g < G; ++g)
-#pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      float v = o[g][e];
-#pragma unroll
-      for (int off = CH; off < 64; off <<= 1) v += __shfl_xor(v, off);
-      o[g][e] = v;
-    }
-  wave_lds_sync();
-  if (vt != 0) return;
-  const int64_t head0 = (int64_t)row * num_q_heads + (int64_t)kvh * G;
-  if (nsplit == 1) {
-#pragma unroll
-    for (int g = 0; g < G; ++g) {
-      const float inv = 1.f / Lr[g];
-      float* op = out + (head0 + g) * D + vc * 8;
-      *reinterpret_cast<float4*>(op) =
-          make_float4(o[g][0] * inv, o[g][1] * inv, o[g][2] * inv, o[g][3] * inv);
-      *reinterpret_cast<float4*>(op + 4) =
-          make_float4(o[g][4] * inv, o[g][5] * inv, o[g][6] * inv, o[g][7] * inv);
-    }
-  } else {
-#pragma unroll
-    for (int g = 0; g < G; ++g) {
-      const int64_t slot = (head0 + g) * max_splits + split;
-      float* op = ws_o + slot * D + vc * 8;
-      *reinterpret_cast<float4*>(op) = make_float4(o[g][0], o[g][1], o[g][2], o[g][3]);
-      *reinterpret_cast<float4*>(op + 4) = make_float4(o[g][4], o[g][5], o[g][6], o[g][7]);
-      if (vc == 0) *reinterpret_cast<float2*>(ws_ml + slot * 2) = make_float2(A[g], Lr[g]);
-    }
-  }
 }
 
 // Second-generation bf16 decode wave: both contractions on MFMA.
@@ -525,10 +260,10 @@ __device__ __forceinline__ void decode_wave_mfma(
 template <int D, int G, int NS, bool BIG_BLOCKS>
 __device__ __forceinline__ void decode_wave_mfma2(
     const uint16_t* __restrict__ kv_layer, uint32_t blk_stride, uint32_t v_off,
-    uint32_t slot_stride, int bs_log2, int num_q_heads, const float* __restrict__ q,
+    uint32_t slot_stride, uint32_t head_stride, int bs_log2, int num_q_heads, const float* __restrict__ q,
     const uint32_t* __restrict__ tbl, int blk0, int max_splits, float scale,
     float* __restrict__ out, float* __restrict__ ws_o, float* __restrict__ ws_ml, uint16_t* VL,
-    uint4* QL, int row, int kvh,
+    uint16_t* QL, int row, int kvh,
     int start, int end, int split, int nsplit) {
   constexpr int KCH = D / 32;     // K . Q^T MFMA k-steps
   constexpr int DT = D / 16;      // output dim tiles of the P.V MFMA
@@ -547,7 +282,7 @@ __device__ __forceinline__ void decode_wave_mfma2(
   const int nblk = ((end - 1) >> bs_log2) - first_blk + 1;
   const int my_blk = lane < nblk ? (int)tbl[lane] : 0;
 
-  const uint16_t* base_k = kv_layer + (uint32_t)kvh * D;
+  const uint16_t* base_k = kv_layer + (uint32_t)kvh * head_stride;
   const int kd = grp * 8;          // K dims chunk
   const int vt = lane / CH;        // V row within a wave load
   const int vc = lane % CH;        // V 16-byte chunk
@@ -588,10 +323,11 @@ __device__ __forceinline__ void decode_wave_mfma2(
   };
 
   // ---- query group as the B operand of S = K . Q^T (hi/lo bf16) ----
-  // Kept in a per-wave LDS tile (lane-major, conflict-free 16-byte reads)
-  // rather than in 32 VGPRs, which keeps the wave at 3 per SIMD.
-  typedef __attribute__((address_space(3))) uint4 lds_q4;
-  const uint32_t ql_base = (uint32_t)(uintptr_t)QL;
+  // Kept in a small per-wave LDS tile [hi|lo][G][D + 8] rather than in 32
+  // VGPRs.  B-operand column l16 >= G reads head l16 % G: those columns of S
+  // are never used, and duplicating a real head keeps them finite.
+  constexpr int QROW = D + 8;
+  const int qh = l16 % G;
   {
     const float* qp = q + ((int64_t)row * num_q_heads + (int64_t)kvh * G + l16) * D + kd;
 #pragma unroll
@@ -611,14 +347,16 @@ __device__ __forceinline__ void decode_wave_mfma2(
       split2_trunc(a[2], a[3], hv.y, lv.y);
       split2_trunc(a[4], a[5], hv.z, lv.z);
       split2_trunc(a[6], a[7], hv.w, lv.w);
-      QL[(2 * j) * 64 + lane] = hv;
-      QL[(2 * j + 1) * 64 + lane] = lv;
+      if (l16 < G) {
+        *reinterpret_cast<uint4*>(&QL[l16 * QROW + 32 * j + kd]) = hv;
+        *reinterpret_cast<uint4*>(&QL[(G + l16) * QROW + 32 * j + kd]) = lv;
+      }
     }
   }
   wave_lds_sync();
   auto qb = [&](int j, int lo) -> bf16x8 {
     uint4 v;
-    __builtin_memcpy(&v, (const void*)&QL[(2 * j + lo) * 64 + lane], 16);
+    __builtin_memcpy(&v, (const void*)&QL[(lo * G + qh) * QROW + 32 * j + kd], 16);
     return __builtin_bit_cast(bf16x8, v);
   };
 
@@ -740,7 +478,8 @@ __device__ __forceinline__ void decode_wave_mfma2(
 template <int D, int G, int NS, bool BIG_BLOCKS>
 __global__ void __launch_bounds__(256)
     paged_decode_mfma2_kernel(const uint16_t* __restrict__ kv_layer, uint32_t blk_stride,
-                              uint32_t v_off, uint32_t slot_stride, int bs_log2, int num_kv_heads,
+                              uint32_t v_off, uint32_t slot_stride,
+                              uint32_t head_stride, int bs_log2, int num_kv_heads,
                               int num_q_heads, const DecodeWork* __restrict__ work, int num_work,
                               const float* __restrict__ q, const uint32_t* __restrict__ positions,
                               const int32_t* __restrict__ row_seq,
@@ -749,42 +488,17 @@ __global__ void __launch_bounds__(256)
                               float scale, float* __restrict__ out, float* __restrict__ ws_o,
                               float* __restrict__ ws_ml) {
   __shared__ __attribute__((aligned(16))) uint16_t lds_v[4][16 * (D + 8)];
-  __shared__ uint4 lds_q[4][2 * (D / 32) * 64];
+  __shared__ __attribute__((aligned(16))) uint16_t lds_q[4][2 * G * (D + 8)];
   const int wv = threadIdx.x >> 6;
   const int w = blockIdx.x * 4 + wv;
   if (w >= num_work) return;
   const DecodeWork wk = work[w];
   const int row = wk.item / num_kv_heads, kvh = wk.item - row * num_kv_heads;
-  decode_wave_mfma2<D, G, NS, BIG_BLOCKS>(kv_layer, blk_stride, v_off, slot_stride, bs_log2,
+  decode_wave_mfma2<D, G, NS, BIG_BLOCKS>(kv_layer, blk_stride, v_off, slot_stride, head_stride,
+                                          bs_log2,
                                           num_q_heads, q, bt_ids + wk.tbl_off, wk.blk0, max_splits,
                                           scale, out, ws_o, ws_ml, lds_v[wv], lds_q[wv], row, kvh,
                                           wk.start, wk.end, wk.start / chunk, wk.nsplit);
-}
-
-template <int D, int G, int NS, bool BIG_BLOCKS, bool LOADS_ONLY = false>
-__global__ void __launch_bounds__(256)
-    paged_decode_mfma_kernel(const uint16_t* __restrict__ kv_layer, uint32_t blk_stride,
-                             uint32_t v_off, uint32_t slot_stride, int bs_log2, int num_kv_heads,
-                             int num_q_heads, const DecodeWork* __restrict__ work, int num_work,
-                             const float* __restrict__ q, const uint32_t* __restrict__ positions,
-                             const int32_t* __restrict__ row_seq,
-                             const int64_t* __restrict__ bt_off, const uint32_t* __restrict__ bt_ids,
-                             int chunk, int max_splits, float scale, float* __restrict__ out,
-                             float* __restrict__ ws_o, float* __restrict__ ws_ml) {
-  constexpr int GP = (G + 3) & ~3;
-  __shared__ float lds_p[4][16 * GP];
-  __shared__ float lds_a[4][GP];
-  __shared__ float lds_l[4][GP];
-  const int wv = threadIdx.x >> 6;
-  const int w = blockIdx.x * 4 + wv;
-  if (w >= num_work) return;
-  const DecodeWork wk = work[w];
-  const int row = wk.item / num_kv_heads, kvh = wk.item - row * num_kv_heads;
-  decode_wave_mfma<D, G, NS, BIG_BLOCKS, LOADS_ONLY>(kv_layer, blk_stride, v_off, slot_stride,
-                                                     bs_log2, num_q_heads, q, bt_ids + wk.tbl_off,
-                                                     max_splits, scale, out, ws_o, ws_ml, lds_p[wv],
-                                                     lds_a[wv], lds_l[wv], row, kvh, wk.start,
-                                                     wk.end, wk.start / chunk, wk.nsplit);
 }
 
 // Merges the per-split states of rows whose context spans several splits.
@@ -967,16 +681,16 @@ size_t decode_workspace_bytes(int64_t rows, int64_t hq, int64_t D, int64_t max_s
 }
 
 template <typename T, int D>
-static hipError_t launch_valu(int G, dim3 grid, dim3 block, hipStream_t st, const T* kv,
-                              int64_t bstr, int64_t voff, int64_t sstr, int bsl, int hkv, int hq,
-                              const DecodeWork* work, int nwork, const float* q, const uint32_t* pos,
-                              const int32_t* rs, const int64_t* bo, const uint32_t* bi, int C,
-                              int ms, float scale, float* out, float* wo, float* wml) {
+static hipError_t launch_valu(int G, dim3 grid, hipStream_t st, const T* kv, const ArenaStrides& a,
+                              int bsl, int hkv, int hq, const DecodeWork* work, int nwork,
+                              const float* q, const uint32_t* pos, const int32_t* rs,
+                              const int64_t* bo, const uint32_t* bi, int C, int ms, float scale,
+                              float* out, float* wo, float* wml) {
 #define ORION_VALU_CASE(GG)                                                                   \
   case GG:                                                                                    \
-    hipLaunchKernelGGL((paged_decode_kernel<T, D, GG>), grid, block, 0, st, kv, bstr, voff,   \
-                       sstr, bsl, hkv, hq, work, nwork, q, pos, rs, bo, bi, C, ms, scale, out,\
-                       wo, wml);                                                              \
+    hipLaunchKernelGGL((paged_decode_kernel<T, D, GG>), grid, dim3(256), 0, st, kv, a.blk,    \
+                       a.v_off, a.slot, a.head, bsl, hkv, hq, work, nwork, q, pos, rs, bo, bi, \
+                       C, ms, scale, out, wo, wml);                                           \
     break;
   switch (G) {
     ORION_VALU_CASE(1)
@@ -994,47 +708,20 @@ static hipError_t launch_valu(int G, dim3 grid, dim3 block, hipStream_t st, cons
   return hipGetLastError();
 }
 
-template <int D, bool BIG, int NS>
-static hipError_t launch_mfma(int G, dim3 grid, dim3 block, hipStream_t st, const uint16_t* kv,
-                              uint32_t bstr, uint32_t voff, uint32_t sstr, int bsl, int hkv,
-                              int hq, const DecodeWork* work, int nwork, const float* q,
-                              const uint32_t* pos,
-                              const int32_t* rs, const int64_t* bo, const uint32_t* bi, int C,
-                              int ms, float scale, float* out, float* wo, float* wml) {
-#define ORION_MFMA_CASE(GG)                                                                   \
-  case GG:                                                                                    \
-    hipLaunchKernelGGL((paged_decode_mfma_kernel<D, GG, NS, BIG>), grid, block, 0, st, kv,    \
-                       bstr, voff, sstr, bsl, hkv, hq, work, nwork, q, pos, rs, bo, bi, C, ms,  \
-                       scale, out, wo, wml);                                                  \
-    break;
-  switch (G) {
-    ORION_MFMA_CASE(1)
-    ORION_MFMA_CASE(2)
-    ORION_MFMA_CASE(3)
-    ORION_MFMA_CASE(4)
-    ORION_MFMA_CASE(5)
-    ORION_MFMA_CASE(6)
-    ORION_MFMA_CASE(7)
-    ORION_MFMA_CASE(8)
-    default:
-      return hipErrorInvalidValue;
-  }
-#undef ORION_MFMA_CASE
-  return hipGetLastError();
-}
-
-template <int D, bool BIG, int NS>
-static hipError_t launch_mfma2(int G, dim3 grid, dim3 block, hipStream_t st, const uint16_t* kv,
-                               uint32_t bstr, uint32_t voff, uint32_t sstr, int bsl, int hkv,
-                               int hq, const DecodeWork* work, int nwork, const float* q,
+template <int D, bool BIG>
+static hipError_t launch_mfma2(int G, dim3 grid, hipStream_t st, const uint16_t* kv,
+                               const ArenaStrides& a, int bsl, int hkv, int hq,
+                               const DecodeWork* work, int nwork, const float* q,
                                const uint32_t* pos, const int32_t* rs, const int64_t* bo,
                                const uint32_t* bi, int C, int ms, float scale, float* out,
                                float* wo, float* wml) {
+  constexpr int NS = 2;
 #define ORION_MFMA2_CASE(GG)                                                                   \
   case GG:                                                                                     \
-    hipLaunchKernelGGL((paged_decode_mfma2_kernel<D, GG, NS, BIG>), grid, block, 0, st, kv,    \
-                       bstr, voff, sstr, bsl, hkv, hq, work, nwork, q, pos, rs, bo, bi, C, ms,   \
-                       scale, out, wo, wml);                                                   \
+    hipLaunchKernelGGL((paged_decode_mfma2_kernel<D, GG, NS, BIG>), grid, dim3(256), 0, st, kv, \
+                       (uint32_t)a.blk, (uint32_t)a.v_off, (uint32_t)a.slot, (uint32_t)a.head, \
+                       bsl, hkv, hq, work, nwork, q, pos, rs, bo, bi, C, ms, scale, out, wo,   \
+                       wml);                                                                   \
     break;
   switch (G) {
     ORION_MFMA2_CASE(1)
@@ -1072,10 +759,10 @@ hipError_t launch_paged_decode(hipStream_t st, const KvGeom& kv, const void* are
                                const float* q, int64_t rows, int64_t hq,
                                const uint32_t* positions, const int32_t* row_seq,
                                const int64_t* bt_off, const uint32_t* bt_ids,
-                               const DecodePlanDev& plan, float* out,
-                               DecodePhase phase) {
+                               const DecodePlanDev& plan, float* out, DecodePhase phase) {
   if (rows == 0 || plan.num_work == 0) return hipSuccess;
   const int64_t hkv = kv.num_kv_heads, D = kv.head_dim;
+  if (hkv <= 0 || hq % hkv != 0) return hipErrorInvalidValue;
   const int G = (int)(hq / hkv);
   const int C = plan.chunk, ms = plan.max_splits;
   if (ms > 1 && plan.ws_bytes < decode_workspace_bytes(rows, hq, D, ms))
@@ -1088,82 +775,35 @@ hipError_t launch_paged_decode(hipStream_t st, const KvGeom& kv, const void* are
   }
   int bs_log2 = 0;
   while ((1 << bs_log2) < kv.block_size) ++bs_log2;
-  const int64_t slot_stride = hkv * D;
-  const int64_t v_off = kv.block_size * slot_stride;
-  const int64_t blk_stride = 2 * v_off;
-  const int64_t layer_elems = kv.num_blocks * blk_stride;
+  const ArenaStrides a = arena_strides(kv);
   const float scale = 1.0f / sqrtf((float)D);
   const dim3 grid((unsigned)((plan.num_work + 3) / 4));
-  const dim3 block(256);
   hipError_t e;
   if (kv.dtype_bf16) {
-    if (layer_elems > (int64_t)UINT32_MAX) return hipErrorInvalidValue;
-    const uint16_t* base = static_cast<const uint16_t*>(arena) + layer * layer_elems;
+    if (a.layer > (int64_t)UINT32_MAX) return hipErrorInvalidValue;
+    const uint16_t* base = static_cast<const uint16_t*>(arena) + layer * a.layer;
     const bool big = kv.block_size >= 16;
-  // ORION_DECODE_STAGES (2..4): register pipeline depth (measurement knob).
-  static const int stages = [] {
-    const char* e = getenv("ORION_DECODE_STAGES");
-    const int v = e ? atoi(e) : 3;
-    return (v >= 2 && v <= 4) ? v : 3;
-  }();
-#define ORION_MFMA_NS(DD, BB, NN)                                                             \
-  launch_mfma<DD, BB, NN>(G, grid, block, st, base, (uint32_t)blk_stride, (uint32_t)v_off,   \
-                          (uint32_t)slot_stride, bs_log2, (int)hkv, (int)hq, plan.work,      \
-                          plan.num_work, q, positions, row_seq, bt_off, bt_ids, C, ms, scale, \
-                          out, ws_o, ws_ml)
-#define ORION_MFMA(DD, BB)                                                                     \
-  (stages == 2 ? ORION_MFMA_NS(DD, BB, 2)                                                      \
-               : stages == 4 ? ORION_MFMA_NS(DD, BB, 4) : ORION_MFMA_NS(DD, BB, 3))
-    static const bool loads_only = getenv("ORION_DECODE_LOADS_ONLY") != nullptr;
-    static const bool gen1 = [] {
-      const char* e = getenv("ORION_DECODE_KERNEL");
-      return e && atoi(e) == 1;
-    }();
-    if (!gen1 && !loads_only) {
-#define ORION_MFMA2_NS(DD, BB, NN)                                                             \
-  launch_mfma2<DD, BB, NN>(G, grid, block, st, base, (uint32_t)blk_stride, (uint32_t)v_off,    \
-                           (uint32_t)slot_stride, bs_log2, (int)hkv, (int)hq, plan.work,      \
-                           plan.num_work, q, positions, row_seq, bt_off, bt_ids, C, ms, scale, \
-                           out, ws_o, ws_ml)
-#define ORION_MFMA2(DD, BB)                                                                     \
-  (stages == 2 ? ORION_MFMA2_NS(DD, BB, 2)                                                      \
-               : stages == 4 ? ORION_MFMA2_NS(DD, BB, 4) : ORION_MFMA2_NS(DD, BB, 3))
-      if (D == 128)
-        e = big ? ORION_MFMA2(128, true) : ORION_MFMA2(128, false);
-      else if (D == 64)
-        e = big ? ORION_MFMA2(64, true) : ORION_MFMA2(64, false);
-      else
-        return hipErrorInvalidValue;
-#undef ORION_MFMA2
-#undef ORION_MFMA2_NS
-      if (e != hipSuccess || ms == 1 || phase == DecodePhase::kSplit) return e;
-      return launch_combine(st, D, rows, hq, positions, plan, C, ms, ws_o, ws_ml, out);
-    }
-    if (loads_only && D == 128 && G == 4 && big) {
-      hipLaunchKernelGGL((paged_decode_mfma_kernel<128, 4, 2, true, true>), grid, block, 0, st,
-                         base, (uint32_t)blk_stride, (uint32_t)v_off, (uint32_t)slot_stride,
-                         bs_log2, (int)hkv, (int)hq, plan.work, plan.num_work, q, positions,
-                         row_seq, bt_off, bt_ids, C, ms, scale, out, ws_o, ws_ml);
-      return hipGetLastError();
-    }
+#define ORION_MFMA2(DD, BB)                                                                      \
+  launch_mfma2<DD, BB>(G, grid, st, base, a, bs_log2, (int)hkv, (int)hq, plan.work,              \
+                       plan.num_work, q, positions, row_seq, bt_off, bt_ids, C, ms, scale, out, \
+                       ws_o, ws_ml)
     if (D == 128)
-      e = big ? ORION_MFMA(128, true) : ORION_MFMA(128, false);
+      e = big ? ORION_MFMA2(128, true) : ORION_MFMA2(128, false);
     else if (D == 64)
-      e = big ? ORION_MFMA(64, true) : ORION_MFMA(64, false);
+      e = big ? ORION_MFMA2(64, true) : ORION_MFMA2(64, false);
     else
       return hipErrorInvalidValue;
-#undef ORION_MFMA_NS
-#undef ORION_MFMA
+#undef ORION_MFMA2
   } else {
-    const float* base = static_cast<const float*>(arena) + layer * layer_elems;
+    const float* base = static_cast<const float*>(arena) + layer * a.layer;
     if (D == 128)
-      e = launch_valu<float, 128>(G, grid, block, st, base, blk_stride, v_off, slot_stride,
-                                  bs_log2, (int)hkv, (int)hq, plan.work, plan.num_work, q, positions, row_seq,
-                                  bt_off, bt_ids, C, ms, scale, out, ws_o, ws_ml);
+      e = launch_valu<float, 128>(G, grid, st, base, a, bs_log2, (int)hkv, (int)hq, plan.work,
+                                  plan.num_work, q, positions, row_seq, bt_off, bt_ids, C, ms,
+                                  scale, out, ws_o, ws_ml);
     else if (D == 64)
-      e = launch_valu<float, 64>(G, grid, block, st, base, blk_stride, v_off, slot_stride,
-                                 bs_log2, (int)hkv, (int)hq, plan.work, plan.num_work, q, positions, row_seq,
-                                 bt_off, bt_ids, C, ms, scale, out, ws_o, ws_ml);
+      e = launch_valu<float, 64>(G, grid, st, base, a, bs_log2, (int)hkv, (int)hq, plan.work,
+                                 plan.num_work, q, positions, row_seq, bt_off, bt_ids, C, ms,
+                                 scale, out, ws_o, ws_ml);
     else
       return hipErrorInvalidValue;
   }

@@ -100,7 +100,8 @@ __device__ inline int swz_v(int r) {
 template <int D, bool HILO, bool BIG>
 __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2)))
     paged_prefill_kernel(const uint16_t* __restrict__ kv_layer, uint32_t blk_stride,
-                         uint32_t v_off, uint32_t slot_stride, int bs_log2, int num_kv_heads,
+                         uint32_t v_off, uint32_t slot_stride, uint32_t head_stride,
+                         int bs_log2, int num_kv_heads,
                          int num_q_heads, const float* __restrict__ q,
                          const int32_t* __restrict__ row_start,
                          const int32_t* __restrict__ row_count,
@@ -180,7 +181,7 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2)))
   constexpr int NID = BIG ? 1 : LPW;
   const int wave_u = __builtin_amdgcn_readfirstlane(wave);
   const int ld_row0 = wave * RPI * LPW + lane / CPR;
-  const uint16_t* head_base = kv_layer + (uint32_t)kvh * D;
+  const uint16_t* head_base = kv_layer + (uint32_t)kvh * head_stride;
   uint32_t ld_off_k[LPW], ld_off_v[LPW];  // element offsets of the fetched chunks
 #pragma unroll
   for (int j = 0; j < LPW; ++j) {
@@ -435,10 +436,8 @@ hipError_t launch_paged_prefill(hipStream_t st, const KvGeom& kv, const void* ar
   const int64_t G = hq / hkv;
   int bs_log2 = 0;
   while ((1 << bs_log2) < kv.block_size) ++bs_log2;
-  const int64_t slot_stride = hkv * D;
-  const int64_t v_off = kv.block_size * slot_stride;
-  const int64_t blk_stride = 2 * v_off;
-  const int64_t layer_elems = kv.num_blocks * blk_stride;
+  const ArenaStrides a = arena_strides(kv);
+  const int64_t layer_elems = a.layer;
   if (layer_elems > (int64_t)UINT32_MAX) return hipErrorInvalidValue;
   const uint16_t* base = static_cast<const uint16_t*>(arena) + layer * layer_elems;
   const int64_t tiles = (max_rows * G + kBM - 1) / kBM;
@@ -447,7 +446,8 @@ hipError_t launch_paged_prefill(hipStream_t st, const KvGeom& kv, const void* ar
   const dim3 grid((unsigned)(num_seqs * hkv), (unsigned)tiles);
 #define ORION_PREFILL_B(DD, HH, BB)                                                             \
   hipLaunchKernelGGL((paged_prefill_kernel<DD, HH, BB>), grid, dim3(256), 0, st, base,              \
-                     (uint32_t)blk_stride, (uint32_t)v_off, (uint32_t)slot_stride, bs_log2,     \
+                     (uint32_t)a.blk, (uint32_t)a.v_off, (uint32_t)a.slot, (uint32_t)a.head,   \
+                     bs_log2,                                                                  \
                      (int)hkv, (int)hq, q, row_start, row_count, first_pos, bt_offsets, bt_ids, \
                      (int)tiles, scale_log2, out)
 #define ORION_PREFILL(DD, HH)        \

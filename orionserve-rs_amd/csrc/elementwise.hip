@@ -73,7 +73,8 @@ __device__ inline void store_kv<uint16_t>(uint16_t* p, float v) { *p = f32_to_bf
 template <typename T>
 __global__ void __launch_bounds__(256)
     rope_cache_kernel(T* __restrict__ kv_layer, int64_t blk_stride, int64_t v_off,
-                      int64_t slot_stride, int bs_log2, int hq, int hkv, int D,
+                      int64_t slot_stride, int64_t head_stride, int bs_log2, int hq, int hkv,
+                      int D,
                       const float* __restrict__ q_in, int64_t q_stride, float* __restrict__ q_out,
                       const float* __restrict__ k, int64_t k_stride, const float* __restrict__ v,
                       int64_t v_stride, const uint32_t* __restrict__ positions,
@@ -107,12 +108,14 @@ __global__ void __launch_bounds__(256)
       const int h = kk / half, i = kk - h * half;
       const float* src = k + row * k_stride + h * D;
       const float x0 = src[i], x1 = src[i + half];
-      store_kv<T>(kdst + h * D + i, x0 * cs[i] - x1 * sn[i]);
-      store_kv<T>(kdst + h * D + i + half, x0 * sn[i] + x1 * cs[i]);
+      store_kv<T>(kdst + h * head_stride + i, x0 * cs[i] - x1 * sn[i]);
+      store_kv<T>(kdst + h * head_stride + i + half, x0 * sn[i] + x1 * cs[i]);
     }
   }
-  for (int idx = threadIdx.x; idx < hkv * D; idx += blockDim.x)
-    store_kv<T>(vdst + idx, v[row * v_stride + idx]);
+  for (int idx = threadIdx.x; idx < hkv * D; idx += blockDim.x) {
+    const int h = idx / D;
+    store_kv<T>(vdst + h * head_stride + (idx - h * D), v[row * v_stride + idx]);
+  }
 }
 
 hipError_t launch_rope_and_cache(hipStream_t st, const KvGeom& kv, void* arena, int64_t layer,
@@ -124,20 +127,17 @@ hipError_t launch_rope_and_cache(hipStream_t st, const KvGeom& kv, void* arena, 
   if (rows == 0) return hipSuccess;
   int bs_log2 = 0;
   while ((1 << bs_log2) < kv.block_size) ++bs_log2;
-  const int64_t slot_stride = kv.num_kv_heads * kv.head_dim;
-  const int64_t v_off = kv.block_size * slot_stride;
-  const int64_t blk_stride = 2 * v_off;
-  const int64_t layer_elems = kv.num_blocks * blk_stride;
+  const ArenaStrides a = arena_strides(kv);
   if (kv.dtype_bf16) {
-    uint16_t* base = static_cast<uint16_t*>(arena) + layer * layer_elems;
+    uint16_t* base = static_cast<uint16_t*>(arena) + layer * a.layer;
     hipLaunchKernelGGL(rope_cache_kernel<uint16_t>, dim3((unsigned)rows), dim3(256), 0, st, base,
-                       blk_stride, v_off, slot_stride, bs_log2, (int)hq, (int)kv.num_kv_heads,
+                       a.blk, a.v_off, a.slot, a.head, bs_log2, (int)hq, (int)kv.num_kv_heads,
                        (int)kv.head_dim, q_in, q_stride, q_out, k, k_stride, v, v_stride,
                        positions, row_seq, bt_off, bt_ids, cos_t, sin_t);
   } else {
-    float* base = static_cast<float*>(arena) + layer * layer_elems;
+    float* base = static_cast<float*>(arena) + layer * a.layer;
     hipLaunchKernelGGL(rope_cache_kernel<float>, dim3((unsigned)rows), dim3(256), 0, st, base,
-                       blk_stride, v_off, slot_stride, bs_log2, (int)hq, (int)kv.num_kv_heads,
+                       a.blk, a.v_off, a.slot, a.head, bs_log2, (int)hq, (int)kv.num_kv_heads,
                        (int)kv.head_dim, q_in, q_stride, q_out, k, k_stride, v, v_stride,
                        positions, row_seq, bt_off, bt_ids, cos_t, sin_t);
   }

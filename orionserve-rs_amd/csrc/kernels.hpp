@@ -13,7 +13,32 @@ namespace orion {
 struct KvGeom {
   int64_t num_layers, num_blocks, block_size, num_kv_heads, head_dim;
   bool dtype_bf16;
+  bool head_major = false;  // block-internal order [kv_head][k|v][slot] instead of [k|v][slot][kv_head]
 };
+
+// Element strides of the arena (one layer = num_blocks blocks).  Reference
+// layout (attention.rs:11-22): [block][k|v][slot][kv_head][dim].  Head-major
+// layout: [block][kv_head][k|v][slot][dim], so one head's K (or V) of a block
+// is one contiguous block_size x dim run.
+struct ArenaStrides {
+  int64_t blk, v_off, slot, head, layer;
+};
+inline ArenaStrides arena_strides(const KvGeom& kv) {
+  ArenaStrides a;
+  const int64_t bs = kv.block_size, hkv = kv.num_kv_heads, D = kv.head_dim;
+  a.blk = 2 * bs * hkv * D;
+  if (kv.head_major) {
+    a.head = 2 * bs * D;
+    a.v_off = bs * D;
+    a.slot = D;
+  } else {
+    a.head = D;
+    a.v_off = bs * hkv * D;
+    a.slot = hkv * D;
+  }
+  a.layer = kv.num_blocks * a.blk;
+  return a;
+}
 
 // ---- attention --------------------------------------------------------------
 // One decode work item: KV head `item % Hkv` of query row `item / Hkv` over

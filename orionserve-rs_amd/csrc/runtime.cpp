@@ -456,8 +456,13 @@ ORION_EXPORT int orion_hip_model_create(orion_hip_device* dev, const orion_hip_m
   m->qd = (int64_t)d.num_attention_heads * d.head_dim;
   m->kvd = (int64_t)d.num_kv_heads * d.head_dim;
   m->qkvd = m->qd + 2 * m->kvd;
+  // Block-internal KV layout of the arena: the reference order unless
+  // ORION_KV_LAYOUT=head-major (read at model creation; both measure the same
+  // on the decode and prefill kernels).
+  const char* lay = getenv("ORION_KV_LAYOUT");
+  const bool head_major = lay && std::strcmp(lay, "head-major") == 0;
   m->kv = KvGeom{d.num_layers, d.num_blocks, d.block_size, d.num_kv_heads, d.head_dim,
-                 d.kv_dtype == ORION_DTYPE_BF16};
+                 d.kv_dtype == ORION_DTYPE_BF16, head_major};
   const int64_t H = d.hidden_size, F = d.intermediate_size, V = d.vocab_size;
   const char* st = "model_create";
   HIP_TRY(st, m->alloc(&m->w_embed, (size_t)(V * H)));
@@ -736,12 +741,9 @@ static int kv_bounds(orion_hip_model* m, int64_t layer, uint32_t block, int64_t 
 
 static size_t kv_offset_elems(orion_hip_model* m, int64_t layer, uint32_t block, int is_value,
                               int64_t slot, int64_t head) {
-  const auto& d = m->desc;
-  const int64_t stride = (int64_t)d.block_size * d.num_kv_heads * d.head_dim;
-  const int64_t per_block = 2 * stride;
-  const int64_t per_layer = (int64_t)d.num_blocks * per_block;
-  return (size_t)(layer * per_layer + (int64_t)block * per_block + (is_value ? stride : 0) +
-                  (slot * d.num_kv_heads + head) * d.head_dim);
+  const ArenaStrides a = arena_strides(m->kv);
+  return (size_t)(layer * a.layer + (int64_t)block * a.blk + (is_value ? a.v_off : 0) +
+                  slot * a.slot + head * a.head);
 }
 
 ORION_EXPORT int orion_hip_model_kv_read(orion_hip_model* model, int64_t layer, uint32_t block,
@@ -789,6 +791,18 @@ ORION_EXPORT int orion_hip_model_kv_write(orion_hip_model* model, int64_t layer,
 ORION_EXPORT int orion_hip_model_kv_arena(orion_hip_model* model, void** d_arena, size_t* bytes) {
   *d_arena = model->arena;
   *bytes = model->arena_bytes;
+  return ORION_HIP_OK;
+}
+
+ORION_EXPORT int orion_hip_model_kv_layout(orion_hip_model* model, orion_hip_kv_layout* out) {
+  const KvGeom& g = model->kv;
+  out->num_layers = g.num_layers;
+  out->num_blocks = g.num_blocks;
+  out->block_size = g.block_size;
+  out->num_kv_heads = g.num_kv_heads;
+  out->head_dim = g.head_dim;
+  out->dtype = g.dtype_bf16 ? ORION_DTYPE_BF16 : ORION_DTYPE_F32;
+  out->head_major = g.head_major ? 1 : 0;
   return ORION_HIP_OK;
 }
 
@@ -1047,7 +1061,7 @@ static int kv_geom_from(const orion_hip_kv_layout* kv, KvGeom* g, const char* st
     return set_err(ORION_HIP_ERR_BACKEND, st, "head_dim %lld unsupported (64 or 128)",
                    (long long)kv->head_dim);
   *g = KvGeom{kv->num_layers, kv->num_blocks, kv->block_size, kv->num_kv_heads, kv->head_dim,
-              kv->dtype == ORION_DTYPE_BF16};
+              kv->dtype == ORION_DTYPE_BF16, kv->head_major != 0};
   return ORION_HIP_OK;
 }
 

@@ -43,7 +43,7 @@ EXPORTED = [
     "orion_hip_model_create", "orion_hip_model_destroy", "orion_hip_model_upload_weight",
     "orion_hip_model_init_synthetic", "orion_hip_synthetic_value",
     "orion_hip_model_download_weight", "orion_hip_model_forward", "orion_hip_model_kv_read",
-    "orion_hip_model_kv_write", "orion_hip_model_kv_arena", "orion_hip_decode_plan_create",
+    "orion_hip_model_kv_write", "orion_hip_model_kv_arena", "orion_hip_model_kv_layout", "orion_hip_decode_plan_create",
     "orion_hip_decode_plan_destroy", "orion_hip_decode_plan_info", "orion_hip_paged_attention_decode",
     "orion_hip_paged_attention_prefill", "orion_hip_rope_and_cache", "orion_hip_rmsnorm",
     "orion_hip_gemm", "orion_hip_silu_mul", "orion_hip_argmax",
@@ -93,6 +93,7 @@ class KvLayout(C.Structure):
     _fields_ = [
         ("num_layers", C.c_int64), ("num_blocks", C.c_int64), ("block_size", C.c_int64),
         ("num_kv_heads", C.c_int64), ("head_dim", C.c_int64), ("dtype", C.c_int32),
+        ("head_major", C.c_int32),
     ]
 
 
@@ -142,6 +143,7 @@ def load_library(path: str = LIB_PATH) -> C.CDLL:
         "orion_hip_model_kv_read": ([vp, i64, u32, i64, i64, C.c_int, vp], C.c_int),
         "orion_hip_model_kv_write": ([vp, i64, u32, i64, i64, C.c_int, vp, i64], C.c_int),
         "orion_hip_model_kv_arena": ([vp, P(vp), P(sz)], C.c_int),
+        "orion_hip_model_kv_layout": ([vp, P(KvLayout)], C.c_int),
         "orion_hip_decode_plan_create": ([vp, vp, vp, vp, vp, i64, i64, i64, i64, i64, P(vp)],
                                          C.c_int),
         "orion_hip_decode_plan_destroy": ([vp], None),
@@ -491,6 +493,11 @@ class HipTransformerModel:
         _check(self._backend.lib.orion_hip_model_kv_arena(self.handle, C.byref(p), C.byref(n)))
         return p.value, n.value
 
+    def kv_layout(self) -> "KvLayout":
+        lay = KvLayout()
+        _check(self._backend.lib.orion_hip_model_kv_layout(self.handle, C.byref(lay)))
+        return lay
+
     def close(self) -> None:
         if self.handle:
             self._backend.lib.orion_hip_model_destroy(self.handle)
@@ -506,8 +513,12 @@ def synthetic_value(seed: int, which: int, layer: int, index: int, std: float = 
 # ---------------------------------------------------------------------------
 
 
-def kv_layout(num_layers, num_blocks, block_size, num_kv_heads, head_dim, dtype) -> KvLayout:
-    return KvLayout(num_layers, num_blocks, block_size, num_kv_heads, head_dim, dtype)
+def kv_layout(num_layers, num_blocks, block_size, num_kv_heads, head_dim, dtype,
+              head_major=False) -> KvLayout:
+    """Arena geometry; head_major selects the [kv_head][k|v][slot][dim] block order
+    instead of the reference [k|v][slot][kv_head][dim]."""
+    return KvLayout(num_layers, num_blocks, block_size, num_kv_heads, head_dim, dtype,
+                    1 if head_major else 0)
 
 
 class DecodePlan:

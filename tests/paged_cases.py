@@ -10,12 +10,13 @@ class PagedCase:
     (also the never-referenced blocks), stored in `dtype` ('f32' | 'bf16')."""
 
     def __init__(self, seed, ctxs, hq, hkv, d, block_size, num_blocks=None, dtype="f32",
-                 pool_factor=1.25, disjoint=True):
+                 pool_factor=1.25, disjoint=True, head_major=False):
         rng = np.random.default_rng(seed)
         self.ctxs = np.asarray(ctxs, dtype=np.int64)
         self.S = len(ctxs)
         self.hq, self.hkv, self.d, self.bs = hq, hkv, d, block_size
         self.dtype = dtype
+        self.head_major = head_major  # device arena block order (the oracle's is reference)
         need = [-(-int(c) // block_size) for c in self.ctxs]
         total = sum(need)
         self.num_blocks = int(num_blocks or int(np.ceil(pool_factor * total)) or 1)
@@ -44,11 +45,24 @@ class PagedCase:
     def dims(self):
         return (1, self.num_blocks, self.bs, self.hkv, self.d)
 
+    def arena_device(self):
+        """The arena in the device layout (reference order unless head_major)."""
+        a = self.arena_f32
+        if self.head_major:
+            a = np.ascontiguousarray(
+                a.reshape(self.num_blocks, 2, self.bs, self.hkv, self.d).transpose(0, 3, 1, 2, 4))
+        return a.reshape(-1)
+
     def arena_device_bytes(self):
         if self.dtype == "bf16":
             import orion_hip
-            return orion_hip.f32_to_bf16_bits(self.arena_f32)
-        return self.arena_f32
+            return orion_hip.f32_to_bf16_bits(self.arena_device())
+        return self.arena_device()
+
+    def kv_layout(self):
+        import orion_hip as oh
+        return oh.kv_layout(1, self.num_blocks, self.bs, self.hkv, self.d,
+                            oh.BF16 if self.dtype == "bf16" else oh.F32, self.head_major)
 
     def kv_bytes_read(self):
         esz = 2 if self.dtype == "bf16" else 4
@@ -69,12 +83,13 @@ def cfg1(seed=20261201):
     return PagedCase(seed + 1, ctxs, 8, 2, 64, 16, num_blocks=256, dtype="f32")
 
 
-def cfg2(seed=20261202, num_seqs=64):
+def cfg2(seed=20261202, num_seqs=64, head_major=False):
     """64 seqs, ctx U[128,4096], bs 16, 32q/8kv, d 128, bf16 KV,
     pool 1.25x the blocks needed, scattered tables."""
     rng = np.random.default_rng(seed)
     ctxs = rng.integers(128, 4097, size=num_seqs)
-    return PagedCase(seed + 1, ctxs, 32, 8, 128, 16, dtype="bf16", pool_factor=1.25)
+    return PagedCase(seed + 1, ctxs, 32, 8, 128, 16, dtype="bf16", pool_factor=1.25,
+                     head_major=head_major)
 
 
 class PrefillCase(PagedCase):
@@ -117,9 +132,10 @@ class PrefillCase(PagedCase):
         return self.oracle(self.positions[rows], self.row_seq[rows], self.q[rows])
 
 
-def cfg3(seed=20261203):
+def cfg3(seed=20261203, head_major=False):
     """8 seqs x 512-token chunk on a prefix U[0,7680], bs 16,
     32q/8kv, d 128, bf16 inputs, scattered tables."""
     rng = np.random.default_rng(seed)
     prefixes = rng.integers(0, 7681, size=8)
-    return PrefillCase(seed + 1, prefixes, [512] * 8, 32, 8, 128, 16, dtype="bf16")
+    return PrefillCase(seed + 1, prefixes, [512] * 8, 32, 8, 128, 16, dtype="bf16",
+                       head_major=head_major)

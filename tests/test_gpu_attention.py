@@ -15,8 +15,7 @@ def run_decode(be, case, positions=None, row_seq=None, q=None):
     row_seq = case.row_seq if row_seq is None else np.asarray(row_seq, np.int32)
     q = case.q if q is None else q
     rows = len(positions)
-    kv = oh.kv_layout(1, case.num_blocks, case.bs, case.hkv, case.d,
-                      oh.BF16 if case.dtype == "bf16" else oh.F32)
+    kv = case.kv_layout()
     bufs = [be.to_device(case.arena_device_bytes()), be.to_device(q), be.to_device(positions),
             be.to_device(row_seq), be.to_device(case.bt_offsets), be.to_device(case.bt_ids),
             be.alloc(rows * case.hq * case.d * 4)]
@@ -42,8 +41,9 @@ def test_cfg1_matches_oracle_f32_tolerance(backend):
     assert mm == 0, (ma, mr, wi)
 
 
-def test_cfg2_full_size_bf16_kv(backend):
-    case = cfg2()
+@pytest.mark.parametrize("head_major", [False, True])
+def test_cfg2_full_size_bf16_kv(backend, head_major):
+    case = cfg2(head_major=head_major)
     got = run_decode(backend, case)
     want = case.oracle()
     err = np.abs(got - want).max()
@@ -56,9 +56,10 @@ def test_cfg2_full_size_bf16_kv(backend):
     (28, 4, 128, 16, "bf16"), (32, 4, 64, 16, "bf16"), (20, 4, 64, 32, "f32"),
     (10, 2, 128, 4, "f32"), (6, 1, 64, 256, "bf16"), (64, 8, 128, 64, "bf16"),
 ])
-def test_shapes_groups_and_block_sizes(backend, hq, hkv, d, bs, dtype):
+@pytest.mark.parametrize("head_major", [False, True])
+def test_shapes_groups_and_block_sizes(backend, hq, hkv, d, bs, dtype, head_major):
     ctxs = [1, 2, 15, 16, 17, 63, 64, 65, 255, 256, 257, 511, 512, 513, 1000, 2049]
-    case = PagedCase(hq * 1000 + d + bs, ctxs, hq, hkv, d, bs, dtype=dtype)
+    case = PagedCase(hq * 1000 + d + bs, ctxs, hq, hkv, d, bs, dtype=dtype, head_major=head_major)
     got = run_decode(backend, case)
     want = case.oracle()
     tol = orc.Tolerance.F32 if dtype == "f32" else orc.Tolerance(1e-4, 1e-4)

@@ -66,8 +66,8 @@ def test_rmsnorm_matches_oracle(backend, rows, cols):
     assert np.all(do.download(np.float32, (1, cols)) == 0)
 
 
-@pytest.mark.parametrize("dtype", ["f32", "bf16"])
-def test_rope_and_cache_is_bit_exact(backend, dtype):
+@pytest.mark.parametrize("dtype,head_major", [("f32", False), ("bf16", False), ("bf16", True)])
+def test_rope_and_cache_is_bit_exact(backend, dtype, head_major):
     # RoPE + slot mapping + KV write against the oracle's apply_rope and
     # KvStore.write: the rotated Q, and every arena element, bit for bit.
     rng = np.random.default_rng(17)
@@ -85,7 +85,7 @@ def test_rope_and_cache_is_bit_exact(backend, dtype):
     qkvd = (hq + 2 * hkv) * d
     qkv = rng.standard_normal((n, qkvd), dtype=np.float32)
     rope = orc.RopeTable(d, 256, 500000.0)
-    kvl = oh.kv_layout(L, nb, bs, hkv, d, oh.BF16 if dtype == "bf16" else oh.F32)
+    kvl = oh.kv_layout(L, nb, bs, hkv, d, oh.BF16 if dtype == "bf16" else oh.F32, head_major)
     esz = 2 if dtype == "bf16" else 4
     arena_el = L * nb * 2 * bs * hkv * d
     darena = backend.alloc(arena_el * esz)
@@ -99,6 +99,8 @@ def test_rope_and_cache_is_bit_exact(backend, dtype):
     q_got = dqo.download(np.float32, (n, hq * d))
     raw = darena.download(np.uint16 if dtype == "bf16" else np.float32, (arena_el,))
     arena_got = oh.bf16_bits_to_f32(raw) if dtype == "bf16" else raw
+    if head_major:  # back to the reference block order [k|v][slot][kv_head][dim]
+        arena_got = arena_got.reshape(L, nb, hkv, 2, bs, d).transpose(0, 1, 3, 4, 2, 5).reshape(-1)
     store = orc.KvStore(L, nb, bs, hkv, d)
     for r in range(n):
         c, s = rope.at(int(positions[r]))

@@ -14,8 +14,7 @@ pytestmark = pytest.mark.gpu
 
 def run_prefill(be, case, hilo):
     n = len(case.positions)
-    kv = oh.kv_layout(1, case.num_blocks, case.bs, case.hkv, case.d,
-                      oh.BF16 if case.dtype == "bf16" else oh.F32)
+    kv = case.kv_layout()
     bufs = [be.to_device(case.arena_device_bytes()), be.to_device(case.q),
             be.to_device(case.row_start), be.to_device(case.row_count),
             be.to_device(case.first_pos), be.to_device(case.bt_offsets),
@@ -48,9 +47,9 @@ def sample_rows(case, per_seq, seed=0):
     return np.array(rows, np.int64)
 
 
-@pytest.mark.parametrize("hilo", [False, True])
-def test_cfg3_full_size_sampled_rows(backend, hilo):
-    case = cfg3()
+@pytest.mark.parametrize("hilo,head_major", [(False, False), (True, False), (False, True)])
+def test_cfg3_full_size_sampled_rows(backend, hilo, head_major):
+    case = cfg3(head_major=head_major)
     got = run_prefill(backend, case, hilo)
     rows = sample_rows(case, 24)
     want = case.oracle_rows(rows)
@@ -67,12 +66,14 @@ def test_cfg3_full_size_sampled_rows(backend, hilo):
     (12, 4, 128, 32), (6, 1, 64, 1), (16, 16, 128, 64),
 ])
 @pytest.mark.parametrize("hilo", [False, True])
-def test_shapes_against_oracle(backend, hq, hkv, d, bs, hilo):
+@pytest.mark.parametrize("head_major", [False, True])
+def test_shapes_against_oracle(backend, hq, hkv, d, bs, hilo, head_major):
     # Prefixes 0 / inside a block / block- and tile-aligned; chunks of 1, 2,
     # a ragged tile and several tiles.
     prefixes = [0, 0, 5, 16, 63, 64, 200, 1000]
     chunks = [1, 2, 33, 64, 129, 17, 300, 70]
-    case = PrefillCase(hq * 100 + d + bs, prefixes, chunks, hq, hkv, d, bs)
+    case = PrefillCase(hq * 100 + d + bs, prefixes, chunks, hq, hkv, d, bs,
+                       head_major=head_major)
     got = run_prefill(backend, case, hilo)
     want = case.oracle()
     tol = orc.Tolerance(1e-4, 1e-4) if hilo else orc.Tolerance(1e-2, 1e-2)
