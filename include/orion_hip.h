@@ -317,9 +317,16 @@ int orion_hip_rmsnorm(orion_hip_device* dev, const float* d_x, const float* d_we
 /* linear (tensor.rs:96-130): d_out[M,N] = d_x[M,K] * W[N,K]^T (+ bias[N]),
  * W bf16 row-major, x/out f32, f32 accumulation on bf16 MFMA (x is split
  * into two bf16 terms so its f32 value is kept to ~16 mantissa bits).
- * accumulate != 0 adds into d_out (residual connection, transformer.rs:328-332). */
+ * epilogue: ORION_GEMM_STORE writes (+ bias); ORION_GEMM_ACCUMULATE adds into
+ * d_out (residual connection, transformer.rs:328-332); ORION_GEMM_SWIGLU
+ * treats W's rows as gate/up interleaved in groups of 8 ([gate 0..7, up 0..7,
+ * gate 8..15, ...], N a multiple of 16) and writes swiglu(gate, up)
+ * (tensor.rs:175-189) into d_out[M, N/2]. */
+#define ORION_GEMM_STORE 0
+#define ORION_GEMM_ACCUMULATE 1
+#define ORION_GEMM_SWIGLU 2
 int orion_hip_gemm(orion_hip_device* dev, const float* d_x, const uint16_t* d_w,
-                   const float* d_bias, int64_t M, int64_t N, int64_t K, int accumulate,
+                   const float* d_bias, int64_t M, int64_t N, int64_t K, int epilogue,
                    float* d_out);
 
 /* swiglu (tensor.rs:175-189): d_gate = silu(d_gate) * d_up, elementwise. */

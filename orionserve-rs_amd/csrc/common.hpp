@@ -108,4 +108,24 @@ __device__ inline void split_bf16(float x, uint16_t& hi, uint16_t& lo) {
   lo = f32_to_bf16(x - bf16_to_f32(hi));
 }
 
+// global_load_lds_dwordx4: the wave's 64 lanes each fetch 16 bytes from their
+// own global address and the hardware stores them to LDS at lds_wave_base +
+// 16 * lane (lds_wave_base must be wave-uniform).  Written as inline asm so
+// the compiler's wait-count tracking does not treat every later LDS read as
+// a possible reader of the in-flight copy; the kernel orders these copies
+// itself (vmcnt(0) then a workgroup barrier before the tile is read).
+// Nothing else in the kernels that use it touches M0.
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+__device__ inline void lds_load16(const void* src, uint32_t lds_wave_base) {
+  asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, off"
+               :
+               : "s"(lds_wave_base), "v"(src)
+               : "memory", "m0");
+}
+#pragma clang diagnostic pop
+
+// s_waitcnt vmcnt(0) (expcnt and lgkmcnt left at their maxima).
+__device__ inline void wait_vmem_all() { __builtin_amdgcn_s_waitcnt(0x0F70); }
+
 }  // namespace orion

@@ -20,6 +20,7 @@
 #include "kernels.hpp"
 
 #include <algorithm>
+#include <cstdlib>
 
 namespace orion {
 
@@ -179,6 +180,151 @@ __global__ void __launch_bounds__(64 * KW)
   }
 }
 
+// Prefill-shaped (large M) GEMM: 128 x 128 output tile per 256-thread
+// workgroup (2 x 2 waves of 64 x 64), k-steps of 32.  The f32 activation tile
+// (128 x 32) and the bf16 weight tile (128 x 32) are copied HBM -> LDS with
+// global_load_lds (no staging registers), double-buffered so the next
+// k-step's copy is in flight while this one computes.  Each wave splits its A
+// fragments into hi/lo bf16 on the fly (as the skinny kernel does) and issues
+// 4 x 4 x 2 MFMAs per k-step; B fragments are reused by the 4 row tiles and A
+// fragments by the 4 column tiles.  LDS rows are XOR-swizzled in 16-byte
+// chunks (conflict-free 16-byte fragment reads; the DMA writes stay linear).
+namespace {
+constexpr int kTM = 128, kTN = 128, kTK = 32;
+// A tile row r: 8 chunks of 4 floats; chunk c stored at c ^ swz_a(r).
+__device__ inline int swz_a(int r) {
+  return ((r >> 2) & 1) | (((r >> 1) & 1) << 1) | (((r >> 3) & 1) << 2);
+}
+// B tile row n: 4 chunks of 8 bf16; chunk c stored at c ^ swz_b(n).
+__device__ inline int swz_b(int n) { return (n >> 2) & 3; }
+}  // namespace
+
+__global__ void __launch_bounds__(256)
+    gemm_tiled_kernel(const float* __restrict__ x, const uint16_t* __restrict__ w,
+                      const float* __restrict__ bias, int M, int N, int K, int ep,
+                      float* __restrict__ out) {
+  __shared__ __attribute__((aligned(1024))) float As[2][kTM * kTK];
+  __shared__ __attribute__((aligned(1024))) uint16_t Bs[2][kTN * kTK];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = wave >> 1, wn = wave & 1;
+  const int l16 = lane & 15, grp = lane >> 4;
+  const int m0 = blockIdx.y * kTM, n0 = blockIdx.x * kTN;
+
+  // ---- DMA addressing: A = 4 wave instructions (8 rows x 128 B each),
+  // B = 2 wave instructions (16 rows x 64 B each). ----
+  const float* a_src[4];
+  const uint16_t* b_src[2];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int r = (wave * 4 + j) * 8 + (lane >> 3);
+    const int c = (lane & 7) ^ swz_a(r);
+    a_src[j] = x + (int64_t)min(m0 + r, M - 1) * K + c * 4;
+  }
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    const int r = (wave * 2 + j) * 16 + (lane >> 2);
+    const int c = (lane & 3) ^ swz_b(r);
+    b_src[j] = w + (int64_t)min(n0 + r, N - 1) * K + c * 8;
+  }
+  const uint32_t as_base = (uint32_t)(uintptr_t)&As[0][0];
+  const uint32_t bs_base = (uint32_t)(uintptr_t)&Bs[0][0];
+  auto load_tile = [&](int ks, int buf) {
+    const int k0 = ks * kTK;
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      lds_load16(a_src[j] + k0, as_base + (uint32_t)(buf * kTM * kTK * 4 + (wave * 4 + j) * 1024));
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+      lds_load16(b_src[j] + k0, bs_base + (uint32_t)(buf * kTN * kTK * 2 + (wave * 2 + j) * 1024));
+  };
+
+  // ---- fragment read addresses (bytes, buffer 0) ----
+  typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+  typedef __attribute__((address_space(3))) u32x4 lds_u32x4;
+  uint32_t a_rd0[4], a_rd1[4], b_rd[4];
+#pragma unroll
+  for (int mt = 0; mt < 4; ++mt) {
+    const int r = wm * 64 + mt * 16 + l16;
+    a_rd0[mt] = as_base + (uint32_t)(r * kTK + (((2 * grp) ^ swz_a(r)) * 4)) * 4;
+    a_rd1[mt] = as_base + (uint32_t)(r * kTK + (((2 * grp + 1) ^ swz_a(r)) * 4)) * 4;
+  }
+#pragma unroll
+  for (int nt = 0; nt < 4; ++nt) {
+    const int n = wn * 64 + nt * 16 + l16;
+    b_rd[nt] = bs_base + (uint32_t)(n * kTK + ((grp ^ swz_b(n)) * 8)) * 2;
+  }
+
+  f32x4 acc[4][4];
+#pragma unroll
+  for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+    for (int nt = 0; nt < 4; ++nt) acc[mt][nt] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  const int ksteps = K / kTK;
+  load_tile(0, 0);
+  wait_vmem_all();
+  __syncthreads();
+  for (int ks = 0; ks < ksteps; ++ks) {
+    const int buf = ks & 1;
+    if (ks + 1 < ksteps) load_tile(ks + 1, buf ^ 1);
+    const uint32_t aoff = (uint32_t)(buf * kTM * kTK * 4);
+    const uint32_t boff = (uint32_t)(buf * kTN * kTK * 2);
+    bf16x8 bw[4];
+#pragma unroll
+    for (int nt = 0; nt < 4; ++nt)
+      bw[nt] = __builtin_bit_cast(bf16x8, *(const lds_u32x4*)(uintptr_t)(b_rd[nt] + boff));
+#pragma unroll
+    for (int mt = 0; mt < 4; ++mt) {
+      const u32x4 lo4 = *(const lds_u32x4*)(uintptr_t)(a_rd0[mt] + aoff);
+      const u32x4 hi4 = *(const lds_u32x4*)(uintptr_t)(a_rd1[mt] + aoff);
+      const float a[8] = {__uint_as_float(lo4.x), __uint_as_float(lo4.y),
+                          __uint_as_float(lo4.z), __uint_as_float(lo4.w),
+                          __uint_as_float(hi4.x), __uint_as_float(hi4.y),
+                          __uint_as_float(hi4.z), __uint_as_float(hi4.w)};
+      bf16x8 ahi, alo;
+      split8(a, ahi, alo);
+#pragma unroll
+      for (int nt = 0; nt < 4; ++nt) {
+        acc[mt][nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ahi, bw[nt], acc[mt][nt], 0, 0, 0);
+        acc[mt][nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(alo, bw[nt], acc[mt][nt], 0, 0, 0);
+      }
+    }
+    wait_vmem_all();
+    __syncthreads();
+  }
+
+  // ---- epilogue: acc[mt][nt][i] = C[m0 + wm*64 + mt*16 + 4*grp + i][n0 + wn*64 + nt*16 + l16] ----
+#pragma unroll
+  for (int mt = 0; mt < 4; ++mt) {
+#pragma unroll
+    for (int nt = 0; nt < 4; ++nt) {
+      const int col = n0 + wn * 64 + nt * 16 + l16;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int row = m0 + wm * 64 + mt * 16 + 4 * grp + i;
+        const float v = acc[mt][nt][i];
+        if (ep == (int)Epilogue::kSwiGLU) {
+          // Tile columns [0, 8) are gate rows of W, [8, 16) the matching up rows.
+          const float u = __shfl_xor(v, 8);
+          if (l16 < 8 && row < M && col < N) {
+            const float act = v / (1.0f + __expf(-v)) * u;
+            out[(int64_t)row * (N >> 1) + ((n0 + wn * 64 + nt * 16) >> 1) + l16] = act;
+          }
+        } else if (row < M && col < N) {
+          float* op = out + (int64_t)row * N + col;
+          if (ep == (int)Epilogue::kAccumulate)
+            *op += v;
+          else
+            *op = bias ? v + bias[col] : v;
+        }
+      }
+    }
+  }
+}
+
 template <int MT, int NT, int UNR>
 static void launch_skinny(int KW, dim3 grid, hipStream_t st, const float* x, const uint16_t* w,
                           const float* bias, int M, int N, int K, int ep, float* out) {
@@ -207,6 +353,18 @@ hipError_t launch_gemm(hipStream_t st, const float* x, const uint16_t* w, const 
   if (M == 0 || N == 0) return hipSuccess;
   if (K % 32 != 0 || K == 0) return hipErrorInvalidValue;
   if (ep == Epilogue::kSwiGLU && N % 16 != 0) return hipErrorInvalidValue;
+  // ORION_GEMM_TILED_MIN_M: smallest M that takes the LDS-tiled kernel.
+  static const int64_t tiled_min_m = [] {
+    const char* e = getenv("ORION_GEMM_TILED_MIN_M");
+    return e ? (int64_t)atoll(e) : (int64_t)256;
+  }();
+  if (M >= tiled_min_m) {
+    if (M > (int64_t)65535 * kTM || N > INT32_MAX || K > INT32_MAX) return hipErrorInvalidValue;
+    dim3 grid((unsigned)((N + kTN - 1) / kTN), (unsigned)((M + kTM - 1) / kTM));
+    hipLaunchKernelGGL(gemm_tiled_kernel, grid, dim3(256), 0, st, x, w, bias, (int)M, (int)N,
+                       (int)K, (int)ep, out);
+    return hipGetLastError();
+  }
   // Rows per tile (MT x 16) and columns per tile (NT x 16): wide column tiles
   // only when there are many of them.  Waves per tile (KW, splitting K): as
   // many as it takes for each wave's whole k-range (<= UNR steps of 32) to be

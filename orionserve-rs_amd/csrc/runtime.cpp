@@ -1212,15 +1212,23 @@ ORION_EXPORT int orion_hip_rmsnorm(orion_hip_device* dev, const float* d_x, cons
 
 ORION_EXPORT int orion_hip_gemm(orion_hip_device* dev, const float* d_x, const uint16_t* d_w,
                                 const float* d_bias, int64_t M, int64_t N, int64_t K,
-                                int accumulate, float* d_out) {
+                                int epilogue, float* d_out) {
   const char* st = "gemm";
   if (K % 32 != 0 || K <= 0)
     return set_err(ORION_HIP_ERR_BACKEND, st, "K must be a positive multiple of 32, got %lld",
                    (long long)K);
-  if (accumulate && d_bias) return internal(st, "bias is not supported with accumulate");
+  if (epilogue < ORION_GEMM_STORE || epilogue > ORION_GEMM_SWIGLU)
+    return internal(st, "unknown epilogue %d", epilogue);
+  if (epilogue != ORION_GEMM_STORE && d_bias)
+    return internal(st, "bias is only supported with the store epilogue");
+  if (epilogue == ORION_GEMM_SWIGLU && N % 16 != 0)
+    return internal(st, "SwiGLU needs N (gate/up rows) to be a multiple of 16, got %lld",
+                    (long long)N);
   HIP_TRY(st, hipSetDevice(dev->ordinal));
-  HIP_TRY(st, launch_gemm(dev->stream, d_x, d_w, d_bias, M, N, K,
-                          accumulate ? Epilogue::kAccumulate : Epilogue::kStore, d_out));
+  const Epilogue ep = epilogue == ORION_GEMM_ACCUMULATE ? Epilogue::kAccumulate
+                      : epilogue == ORION_GEMM_SWIGLU   ? Epilogue::kSwiGLU
+                                                        : Epilogue::kStore;
+  HIP_TRY(st, launch_gemm(dev->stream, d_x, d_w, d_bias, M, N, K, ep, d_out));
   return ORION_HIP_OK;
 }
 

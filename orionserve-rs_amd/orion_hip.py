@@ -584,8 +584,13 @@ def rmsnorm(be: HipBackend, x: int, w: int, rows: int, cols: int, eps: float, ou
     _check(be.lib.orion_hip_rmsnorm(be.handle, x, w, rows, cols, eps, out))
 
 
+GEMM_STORE, GEMM_ACCUMULATE, GEMM_SWIGLU = 0, 1, 2
+
+
 def gemm(be: HipBackend, x: int, w: int, bias: Optional[int], M: int, N: int, K: int,
-         accumulate: bool, out: int) -> None:
+         accumulate, out: int) -> None:
+    """orion_hip_gemm; `accumulate` is a bool (store / accumulate) or one of
+    GEMM_STORE, GEMM_ACCUMULATE, GEMM_SWIGLU."""
     _check(be.lib.orion_hip_gemm(be.handle, x, w, bias, M, N, K, int(accumulate), out))
 
 

@@ -33,7 +33,10 @@ def gemm_case(be, M, N, K, bias=False, accumulate=False, seed=0):
 
 
 @pytest.mark.parametrize("M,N,K", [(1, 16, 32), (7, 40, 64), (32, 2560, 2048), (64, 512, 5632),
-                                   (65, 96, 256), (130, 2048, 512), (32, 32000, 2048)])
+                                   (65, 96, 256), (130, 2048, 512), (32, 32000, 2048),
+                                   # LDS-tiled (prefill) kernel: M >= 256, ragged M/N edges
+                                   (256, 128, 32), (300, 96, 256), (1000, 2560, 2048),
+                                   (777, 2048, 5632), (513, 32000, 2048)])
 def test_gemm_matches_linear(backend, M, N, K):
     got, want, ref64 = gemm_case(backend, M, N, K, seed=M + N + K)
     scale = np.abs(ref64).max()
@@ -42,11 +45,37 @@ def test_gemm_matches_linear(backend, M, N, K):
     assert np.abs(got - want).max() <= 2e-5 * scale + 1e-6
 
 
-def test_gemm_bias_and_accumulate_epilogues(backend):
-    got, want, ref64 = gemm_case(backend, 33, 272, 384, bias=True, seed=1)
+@pytest.mark.parametrize("M", [33, 400])
+def test_gemm_bias_and_accumulate_epilogues(backend, M):
+    got, want, ref64 = gemm_case(backend, M, 272, 384, bias=True, seed=1)
     assert np.abs(got - ref64).max() <= 1e-4
-    got, want, ref64 = gemm_case(backend, 33, 272, 384, accumulate=True, seed=2)
+    got, want, ref64 = gemm_case(backend, M, 272, 384, accumulate=True, seed=2)
     assert np.abs(got - ref64).max() <= 1e-4
+
+
+@pytest.mark.parametrize("M,F,K", [(5, 48, 64), (32, 5632, 2048), (300, 176, 256), (600, 5632, 2048)])
+def test_gemm_swiglu_epilogue(backend, M, F, K):
+    # Gate and up rows interleaved in groups of 8 (the model's fused W_gu
+    # layout); the epilogue returns swiglu(x.Wg^T, x.Wu^T) (tensor.rs:175-189).
+    rng = np.random.default_rng(M + F)
+    x = rng.standard_normal((M, K), dtype=np.float32)
+    wg = bf16_round(rng.standard_normal((F, K), dtype=np.float32) * 0.05)
+    wu = bf16_round(rng.standard_normal((F, K), dtype=np.float32) * 0.05)
+    w = np.empty((2 * F, K), np.float32)
+    for g in range(F // 8):
+        w[16 * g:16 * g + 8] = wg[8 * g:8 * g + 8]
+        w[16 * g + 8:16 * g + 16] = wu[8 * g:8 * g + 8]
+    dx, dw = backend.to_device(x), backend.to_device(oh.f32_to_bf16_bits(w))
+    dout = backend.alloc(M * F * 4)
+    print(f"[gemm-swiglu] M={M} F={F} K={K}", flush=True)
+    oh.gemm(backend, dx.ptr, dw.ptr, None, M, 2 * F, K, oh.GEMM_SWIGLU, dout.ptr)
+    got = dout.download(np.float32, (M, F))
+    g64 = x.astype(np.float64) @ wg.T.astype(np.float64)
+    u64 = x.astype(np.float64) @ wu.T.astype(np.float64)
+    want = g64 / (1 + np.exp(-g64)) * u64
+    assert np.abs(got - want).max() <= 3e-5 * max(np.abs(want).max(), 1.0)
+    for b in (dx, dw, dout):
+        b.free()
 
 
 @pytest.mark.parametrize("rows,cols", [(1, 64), (5, 2048), (33, 3584), (3, 100)])
