@@ -325,6 +325,169 @@ __global__ void __launch_bounds__(256)
   }
 }
 
+// Decode-shaped (M <= 64) weight-streaming GEMM, split over K across
+// workgroups.  Workgroup (256 threads) = 4 waves x NT column tiles of 16 =
+// 64*NT output columns, over one K slice of KSTEPS k-steps (32 k each).
+//   1. Every wave issues all of its slice's weight loads at once
+//      (KSTEPS x NT 16-byte loads per lane straight into MFMA B fragments),
+//      so a wave keeps KSTEPS*NT KiB in flight.
+//   2. Meanwhile the workgroup stages the activation slice x[0:M, slice] in
+//      LDS once, already split into hi/lo bf16 A fragments (lane-major), so
+//      the 4 waves share one read of x instead of one read per 16 columns.
+//   3. MFMAs; with one K slice the epilogue is applied directly.  With
+//      several, each workgroup writes its partial tile to the scratch and a
+//      second kernel sums the slices in slice order (deterministic) and
+//      applies the epilogue.
+template <int MT, int NT, int KSTEPS>
+__global__ void __launch_bounds__(256)
+    gemm_gemv_kernel(const float* __restrict__ x, const uint16_t* __restrict__ w,
+                     const float* __restrict__ bias, int M, int N, int K, int ep,
+                     float* __restrict__ out, float* __restrict__ partial) {
+  constexpr int BN = 64 * NT;
+  __shared__ __attribute__((aligned(16))) uint4 xs[2][MT * KSTEPS * 64];  // [hi|lo][frag][lane]
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int l16 = lane & 15, grp = lane >> 4;
+  const int n0 = blockIdx.x * BN;
+  const int kslices = gridDim.y;
+  const int k0 = blockIdx.y * KSTEPS * 32;
+  const int nsteps = min(KSTEPS, (K - k0) >> 5);
+
+  // 1. weight loads (clamped column and k-step: unconditional loads)
+  bf16x8 bw[KSTEPS][NT];
+#pragma unroll
+  for (int nt = 0; nt < NT; ++nt) {
+    const int n = min(n0 + (wave * NT + nt) * 16 + l16, N - 1);
+    const uint16_t* wp = w + (int64_t)n * K + k0 + grp * 8;
+#pragma unroll
+    for (int s2 = 0; s2 < KSTEPS; ++s2)
+      bw[s2][nt] = __builtin_bit_cast(
+          bf16x8, *reinterpret_cast<const uint4*>(wp + min(s2, nsteps - 1) * 32));
+  }
+
+  // 2. activation slice -> LDS hi/lo fragments: fragment f = (mt, step),
+  //    lane l holds row mt*16 + l%16, k = step*32 + (l/16)*8 .. +8.
+  for (int idx = tid; idx < MT * KSTEPS * 64; idx += 256) {
+    const int fl = idx & 63, f = idx >> 6;
+    const int mt = f / KSTEPS, s2 = f - mt * KSTEPS;
+    const int row = mt * 16 + (fl & 15);
+    float a[8];
+    if (row < M && s2 < nsteps) {
+      const float* xp = x + (int64_t)row * K + k0 + s2 * 32 + (fl >> 4) * 8;
+      const float4 x0 = *reinterpret_cast<const float4*>(xp);
+      const float4 x1 = *reinterpret_cast<const float4*>(xp + 4);
+      a[0] = x0.x; a[1] = x0.y; a[2] = x0.z; a[3] = x0.w;
+      a[4] = x1.x; a[5] = x1.y; a[6] = x1.z; a[7] = x1.w;
+    } else {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) a[e] = 0.f;
+    }
+    uint4 hv, lv;
+    split2_trunc(a[0], a[1], hv.x, lv.x);
+    split2_trunc(a[2], a[3], hv.y, lv.y);
+    split2_trunc(a[4], a[5], hv.z, lv.z);
+    split2_trunc(a[6], a[7], hv.w, lv.w);
+    xs[0][idx] = hv;
+    xs[1][idx] = lv;
+  }
+  __syncthreads();
+
+  // 3. MFMAs
+  f32x4 acc[MT][NT];
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) acc[mt][nt] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int s2 = 0; s2 < KSTEPS; ++s2) {
+    if (s2 < nsteps) {
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) {
+        const bf16x8 ahi = __builtin_bit_cast(bf16x8, xs[0][(mt * KSTEPS + s2) * 64 + lane]);
+        const bf16x8 alo = __builtin_bit_cast(bf16x8, xs[1][(mt * KSTEPS + s2) * 64 + lane]);
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt) {
+          acc[mt][nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ahi, bw[s2][nt], acc[mt][nt], 0, 0, 0);
+          acc[mt][nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(alo, bw[s2][nt], acc[mt][nt], 0, 0, 0);
+        }
+      }
+    }
+  }
+
+  // C fragment: acc[mt][nt][i] = C[mt*16 + 4*grp + i][n0 + (wave*NT + nt)*16 + l16]
+  auto epilogue = [&](int row, int tile_col0, float v) {
+    const int col = tile_col0 + l16;
+    if (ep == (int)Epilogue::kSwiGLU) {
+      const float u = __shfl_xor(v, 8);
+      if (l16 < 8 && row < M && col < N)
+        out[(int64_t)row * (N >> 1) + (tile_col0 >> 1) + l16] = v / (1.0f + __expf(-v)) * u;
+    } else if (row < M && col < N) {
+      float* op = out + (int64_t)row * N + col;
+      if (ep == (int)Epilogue::kAccumulate)
+        *op += v;
+      else
+        *op = bias ? v + bias[col] : v;
+    }
+  };
+  if (kslices == 1) {
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+      for (int nt = 0; nt < NT; ++nt)
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          epilogue(mt * 16 + 4 * grp + i, n0 + (wave * NT + nt) * 16, acc[mt][nt][i]);
+    return;
+  }
+  // Partial tile of this K slice: partial[slice][tile][row][BN], rows < 16*MT;
+  // gemm_gemv_reduce_kernel sums the slices in order (a kernel boundary
+  // orders the two; XCD L2s are not coherent within a kernel).
+  const int64_t tile_elems = (int64_t)MT * 16 * BN;
+  float* mine = partial + ((int64_t)blockIdx.y * gridDim.x + blockIdx.x) * tile_elems;
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt)
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        mine[(mt * 16 + 4 * grp + i) * BN + (wave * NT + nt) * 16 + l16] = acc[mt][nt][i];
+}
+
+// Sums the K-slice partials of gemm_gemv_kernel in slice order and applies
+// the epilogue.  One thread per (row, 16-column tile lane); SwiGLU pairs lanes
+// 8 apart within a 16-column tile.
+template <int MT, int NT>
+__global__ void __launch_bounds__(256)
+    gemm_gemv_reduce_kernel(const float* __restrict__ partial, int kslices, int n_tiles,
+                            const float* __restrict__ bias, int M, int N, int ep,
+                            float* __restrict__ out) {
+  constexpr int BN = 64 * NT;
+  const int64_t tile_elems = (int64_t)MT * 16 * BN;
+  const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;  // over n_tiles * M * BN
+  const int64_t per_tile = (int64_t)M * BN;
+  if (idx >= (int64_t)n_tiles * per_tile) return;  // whole 16-lane groups exit together
+  const int tile = (int)(idx / per_tile);
+  const int rem = (int)(idx - tile * per_tile);
+  const int row = rem / BN, c = rem - row * BN;
+  float v = 0.f;
+  for (int ks = 0; ks < kslices; ++ks)
+    v += partial[((int64_t)ks * n_tiles + tile) * tile_elems + row * BN + c];
+  const int col = tile * BN + c;
+  if (ep == (int)Epilogue::kSwiGLU) {
+    const float u = __shfl_xor(v, 8);
+    if ((c & 15) < 8 && col < N)
+      out[(int64_t)row * (N >> 1) + ((col & ~15) >> 1) + (c & 7)] = v / (1.0f + __expf(-v)) * u;
+  } else if (col < N) {
+    float* op = out + (int64_t)row * N + col;
+    if (ep == (int)Epilogue::kAccumulate)
+      *op += v;
+    else
+      *op = bias ? v + bias[col] : v;
+  }
+}
+
 template <int MT, int NT, int UNR>
 static void launch_skinny(int KW, dim3 grid, hipStream_t st, const float* x, const uint16_t* w,
                           const float* bias, int M, int N, int K, int ep, float* out) {
@@ -348,8 +511,50 @@ static void launch_skinny(int KW, dim3 grid, hipStream_t st, const float* x, con
   }
 }
 
+namespace {
+constexpr int kGemvNT = 2, kGemvKSteps = 8;
+struct GemvShape {
+  int mt, n_tiles, kslices;
+  size_t ws_bytes;
+};
+GemvShape gemv_shape(int64_t M, int64_t N, int64_t K) {
+  GemvShape g;
+  g.mt = (int)((M + 15) / 16);
+  g.n_tiles = (int)((N + 64 * kGemvNT - 1) / (64 * kGemvNT));
+  g.kslices = (int)((K + kGemvKSteps * 32 - 1) / (kGemvKSteps * 32));
+  g.ws_bytes = g.kslices > 1 ? (size_t)g.kslices * g.n_tiles * g.mt * 16 * 64 * kGemvNT * 4 : 0;
+  return g;
+}
+template <int MT>
+void launch_gemv(const GemvShape& g, hipStream_t st, const float* x, const uint16_t* w,
+                 const float* bias, int M, int N, int K, int ep, float* out,
+                 const GemmScratch* sc) {
+  hipLaunchKernelGGL((gemm_gemv_kernel<MT, kGemvNT, kGemvKSteps>),
+                     dim3((unsigned)g.n_tiles, (unsigned)g.kslices), dim3(256), 0, st, x, w, bias,
+                     M, N, K, ep, out, sc ? sc->ws : nullptr);
+  if (g.kslices > 1) {
+    const int64_t threads = (int64_t)g.n_tiles * M * 64 * kGemvNT;
+    hipLaunchKernelGGL((gemm_gemv_reduce_kernel<MT, kGemvNT>),
+                       dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, st, sc->ws,
+                       g.kslices, g.n_tiles, bias, M, N, ep, out);
+  }
+}
+}  // namespace
+
+void gemm_scratch_need(int64_t M, int64_t N, int64_t K, size_t* ws_bytes, int64_t* counters) {
+  if (M < 1 || M > 64 || K % 32 != 0) {
+    *ws_bytes = 0;
+    *counters = 0;
+    return;
+  }
+  const GemvShape g = gemv_shape(M, N, K);
+  *ws_bytes = g.ws_bytes;
+  *counters = 0;
+}
+
 hipError_t launch_gemm(hipStream_t st, const float* x, const uint16_t* w, const float* bias,
-                       int64_t M, int64_t N, int64_t K, Epilogue ep, float* out) {
+                       int64_t M, int64_t N, int64_t K, Epilogue ep, float* out,
+                       const GemmScratch* scratch) {
   if (M == 0 || N == 0) return hipSuccess;
   if (K % 32 != 0 || K == 0) return hipErrorInvalidValue;
   if (ep == Epilogue::kSwiGLU && N % 16 != 0) return hipErrorInvalidValue;
@@ -358,6 +563,22 @@ hipError_t launch_gemm(hipStream_t st, const float* x, const uint16_t* w, const 
     const char* e = getenv("ORION_GEMM_TILED_MIN_M");
     return e ? (int64_t)atoll(e) : (int64_t)256;
   }();
+  // Decode-shaped M: split-K weight streaming (needs the scratch when K spans
+  // several slices).
+  if (M <= 64 && N <= INT32_MAX && K <= INT32_MAX) {
+    const GemvShape g = gemv_shape(M, N, K);
+    const bool fits = g.kslices == 1 || (scratch && scratch->ws_bytes >= g.ws_bytes);
+    if (fits && g.kslices <= 65535) {
+      const int m = (int)M, n = (int)N, k = (int)K, e = (int)ep;
+      switch (g.mt) {
+        case 1: launch_gemv<1>(g, st, x, w, bias, m, n, k, e, out, scratch); break;
+        case 2: launch_gemv<2>(g, st, x, w, bias, m, n, k, e, out, scratch); break;
+        case 3: launch_gemv<3>(g, st, x, w, bias, m, n, k, e, out, scratch); break;
+        default: launch_gemv<4>(g, st, x, w, bias, m, n, k, e, out, scratch); break;
+      }
+      return hipGetLastError();
+    }
+  }
   if (M >= tiled_min_m) {
     if (M > (int64_t)65535 * kTM || N > INT32_MAX || K > INT32_MAX) return hipErrorInvalidValue;
     dim3 grid((unsigned)((N + kTN - 1) / kTN), (unsigned)((M + kTM - 1) / kTM));

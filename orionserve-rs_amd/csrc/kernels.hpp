@@ -97,8 +97,19 @@ enum class Epilogue : int {
   kSwiGLU = 2,      // W rows interleaved in groups of 8 gate / 8 up rows;
                     // out[:, N/2] = silu(gate) * up
 };
+// Scratch for split-K decode GEMMs: partial tiles and per-column-tile
+// arrival counters (zero between calls; the kernel re-arms them).
+struct GemmScratch {
+  float* ws = nullptr;
+  size_t ws_bytes = 0;
+  unsigned int* counters = nullptr;
+  int64_t num_counters = 0;
+};
+// Scratch a launch_gemm of this shape needs (0 / 0: none).
+void gemm_scratch_need(int64_t M, int64_t N, int64_t K, size_t* ws_bytes, int64_t* counters);
 hipError_t launch_gemm(hipStream_t st, const float* x, const uint16_t* w, const float* bias,
-                       int64_t M, int64_t N, int64_t K, Epilogue ep, float* out);
+                       int64_t M, int64_t N, int64_t K, Epilogue ep, float* out,
+                       const GemmScratch* scratch = nullptr);
 
 // ---- elementwise / normalisation -------------------------------------------
 hipError_t launch_embed(hipStream_t st, const uint32_t* tokens, int64_t n, const uint16_t* table,

@@ -141,6 +141,9 @@ struct orion_hip_device {
   hipEvent_t ev_start = nullptr, ev_stop = nullptr;
   std::string name;
   int64_t wave_slots = 2048;  // resident decode waves: CUs x 4 SIMDs x 2
+  // Split-K GEMM scratch (partials + zeroed arrival counters), shared by
+  // every call on this device's stream.
+  DevBuf gemm_ws, gemm_cnt;
   // Per-kernel timing (orion_hip_kernel_timing): event pairs per kernel
   // index, resolved when read.
   bool ktiming = false;
@@ -294,6 +297,8 @@ ORION_EXPORT void orion_hip_device_close(orion_hip_device* dev) {
   (void)hipEventDestroy(dev->ev_stop);
   dev->recycle_events();
   for (hipEvent_t e : dev->event_pool) (void)hipEventDestroy(e);
+  dev->gemm_ws.release();
+  dev->gemm_cnt.release();
   (void)hipStreamDestroy(dev->stream);
   delete dev;
 }
@@ -413,6 +418,39 @@ static hipError_t timed_launch(orion_hip_device* dev, int k, F&& launch) {
   }
   dev->kevents[k].push_back({a, b});
   return hipSuccess;
+}
+
+// The split-K GEMM scratch for a call of this shape, grown on demand (new
+// counter memory is zeroed; the kernels leave counters at zero).
+static hipError_t gemm_scratch(orion_hip_device* dev, int64_t M, int64_t N, int64_t K,
+                               GemmScratch* sc) {
+  size_t ws = 0;
+  int64_t cnt = 0;
+  gemm_scratch_need(M, N, K, &ws, &cnt);
+  if (ws > dev->gemm_ws.bytes) {
+    hipError_t e = dev->gemm_ws.reserve(ws);
+    if (e != hipSuccess) return e;
+  }
+  if ((size_t)cnt * 4 > dev->gemm_cnt.bytes) {
+    hipError_t e = dev->gemm_cnt.reserve((size_t)cnt * 4);
+    if (e != hipSuccess) return e;
+    e = hipMemsetAsync(dev->gemm_cnt.ptr, 0, dev->gemm_cnt.bytes, dev->stream);
+    if (e != hipSuccess) return e;
+  }
+  sc->ws = dev->gemm_ws.as<float>();
+  sc->ws_bytes = dev->gemm_ws.bytes;
+  sc->counters = dev->gemm_cnt.as<unsigned int>();
+  sc->num_counters = (int64_t)(dev->gemm_cnt.bytes / 4);
+  return hipSuccess;
+}
+
+static hipError_t gemm_on(orion_hip_device* dev, const float* x, const uint16_t* w,
+                          const float* bias, int64_t M, int64_t N, int64_t K, Epilogue ep,
+                          float* out) {
+  GemmScratch sc;
+  hipError_t e = gemm_scratch(dev, M, N, K, &sc);
+  if (e != hipSuccess) return e;
+  return launch_gemm(dev->stream, x, w, bias, M, N, K, ep, out, &sc);
 }
 
 // ---------------------------------------------------------------------------
@@ -1015,7 +1053,7 @@ ORION_EXPORT int orion_hip_model_forward(orion_hip_model* m, const orion_hip_bat
   for (int64_t l = 0; l < d.num_layers; ++l) {
     const LayerDev& L = m->layers[l];
     HIP_TRY(st, launch_rmsnorm(stream, hidden, nullptr, L.input_norm, n, H, d.rms_norm_eps, xn));
-    HIP_TRY(st, launch_gemm(stream, xn, L.w_qkv, L.b_qkv, n, m->qkvd, H, Epilogue::kStore, qkv));
+    HIP_TRY(st, gemm_on(m->dev, xn, L.w_qkv, L.b_qkv, n, m->qkvd, H, Epilogue::kStore, qkv));
     HIP_TRY(st, launch_rope_and_cache(stream, m->kv, m->arena, l, n, Hq, qkv, m->qkvd, qrot,
                                       qkv + m->qd, m->qkvd, qkv + m->qd + m->kvd, m->qkvd, d_pos,
                                       d_rs, d_btoff, d_btids, m->rope_cos, m->rope_sin));
@@ -1025,11 +1063,11 @@ ORION_EXPORT int orion_hip_model_forward(orion_hip_model* m, const orion_hip_bat
       HIP_TRY(st, launch_paged_prefill(stream, m->kv, m->arena, l, qrot, Hq, npf, d_pfstart,
                                        d_pfcount, d_pfpos, d_pfoff, d_btids, pf_max_rows,
                                        hb.max_position, /*hilo=*/true, attn));
-    HIP_TRY(st, launch_gemm(stream, attn, L.w_o, nullptr, n, H, m->qd, Epilogue::kAccumulate,
+    HIP_TRY(st, gemm_on(m->dev, attn, L.w_o, nullptr, n, H, m->qd, Epilogue::kAccumulate,
                             hidden));
     HIP_TRY(st, launch_rmsnorm(stream, hidden, nullptr, L.post_norm, n, H, d.rms_norm_eps, xn));
-    HIP_TRY(st, launch_gemm(stream, xn, L.w_gu, nullptr, n, 2 * F, H, Epilogue::kSwiGLU, act));
-    HIP_TRY(st, launch_gemm(stream, act, L.w_down, nullptr, n, H, F, Epilogue::kAccumulate,
+    HIP_TRY(st, gemm_on(m->dev, xn, L.w_gu, nullptr, n, 2 * F, H, Epilogue::kSwiGLU, act));
+    HIP_TRY(st, gemm_on(m->dev, act, L.w_down, nullptr, n, H, F, Epilogue::kAccumulate,
                             hidden));
   }
   // Final norm on the last row of each sequence only (norm is row-wise, so
@@ -1037,7 +1075,7 @@ ORION_EXPORT int orion_hip_model_forward(orion_hip_model* m, const orion_hip_bat
   HIP_TRY(st, launch_rmsnorm(stream, hidden, d_last, m->final_norm, S, H, d.rms_norm_eps, xn));
   const uint16_t* head = m->w_lm ? m->w_lm : m->w_embed;
   float* logits = m->logits.as<float>();
-  HIP_TRY(st, launch_gemm(stream, xn, head, nullptr, S, V, H, Epilogue::kStore, logits));
+  HIP_TRY(st, gemm_on(m->dev, xn, head, nullptr, S, V, H, Epilogue::kStore, logits));
   if (argmax_out) {
     HIP_TRY(st, launch_argmax(stream, logits, S, V, m->argmax.as<int64_t>()));
     HIP_TRY(st, hipMemcpyAsync(argmax_out, m->argmax.ptr, S * 8, hipMemcpyDeviceToHost, stream));
@@ -1228,7 +1266,7 @@ ORION_EXPORT int orion_hip_gemm(orion_hip_device* dev, const float* d_x, const u
   const Epilogue ep = epilogue == ORION_GEMM_ACCUMULATE ? Epilogue::kAccumulate
                       : epilogue == ORION_GEMM_SWIGLU   ? Epilogue::kSwiGLU
                                                         : Epilogue::kStore;
-  HIP_TRY(st, launch_gemm(dev->stream, d_x, d_w, d_bias, M, N, K, ep, d_out));
+  HIP_TRY(st, gemm_on(dev, d_x, d_w, d_bias, M, N, K, ep, d_out));
   return ORION_HIP_OK;
 }
 
