@@ -204,6 +204,122 @@ def decode_e2e(steps=64, seqs=32, seed=20261204, cpu=True):
     return res
 
 
+QWEN2_7B_LAYER = dict(H=3584, hq=28, hkv=4, d=128, F=18944, V=1024, eps=1e-6, theta=1000000.0,
+                      max_pos=16640)
+
+
+def mixed_cfg5(steps=10, warmup=2, seed=20261205):
+    """one Qwen2-7B-shape layer (hidden 3584, 28q/4kv heads,
+    d 128, ffn 18944, QKV bias; bf16 weights synthetic N(0,0.02), RoPE theta
+    1e6) over a mixed continuous batch: 8 prefill chunks of 256 tokens + 192
+    decode rows, half the sequences sharing a 2048-token prefix through
+    identical leading block ids, other context lognormal (median 1024) capped
+    at 16384, block 16.  The KV cache (bf16) is filled with N(0,1) values.
+    The LM head is cut to a 1024-token vocabulary so the figure is the layer's
+    (the real 152k-row head would dominate).  Also times the two attention
+    kernels alone on the same cache: decode rows against unique and logical
+    K/V bytes, prefill chunks in TFLOP/s."""
+    import orion_hip as oh
+    from paged_cases import cfg5_batch
+
+    cfg = QWEN2_7B_LAYER
+    b = cfg5_batch(cfg["V"], seed)
+    be = oh.HipBackend(0)
+    meta = oh.ModelMetadata(hidden_size=cfg["H"], num_layers=1, num_attention_heads=cfg["hq"],
+                            num_kv_heads=cfg["hkv"], head_dim=cfg["d"], vocab_size=cfg["V"],
+                            intermediate_size=cfg["F"], max_position_embeddings=cfg["max_pos"],
+                            rope_theta=cfg["theta"], rms_norm_eps=cfg["eps"],
+                            architecture="qwen2")
+    model = oh.HipTransformerModel(meta, b.num_blocks, b.bs, be, oh.BF16)
+    model.init_synthetic(seed, 0.02)
+    arena_ptr, arena_bytes = model.kv_arena()
+    rng = np.random.default_rng(seed + 1)
+    chunk = 1 << 26  # bf16 elements per upload
+    for off in range(0, arena_bytes // 2, chunk):
+        n = min(chunk, arena_bytes // 2 - off)
+        bits = oh.f32_to_bf16_bits(rng.standard_normal(n, dtype=np.float32))
+        oh._check(be.lib.orion_hip_memcpy_h2d(be.handle, arena_ptr + off * 2, bits.ctypes.data,
+                                              bits.nbytes))
+    batch = oh.ForwardBatch(b.tokens.tolist(), b.positions.tolist(), list(range(b.S)),
+                            b.counts.tolist(), b.ctx.tolist(), [t.tolist() for t in b.tables],
+                            True)
+    for _ in range(warmup):
+        model.forward(batch, want_logits=False, want_argmax=True)
+    be.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        model.forward(batch, want_logits=False, want_argmax=True)
+    be.synchronize()
+    layer_ms = (time.perf_counter() - t0) / steps * 1e3
+    n_rows = len(b.positions)
+
+    # attention kernels alone, same cache and tables
+    kv = model.kv_layout()
+    hq, hkv, d = cfg["hq"], cfg["hkv"], cfg["d"]
+    offs = np.zeros(b.S + 1, np.int64)
+    offs[1:] = np.cumsum([len(t) for t in b.tables])
+    ids = np.concatenate(b.tables)
+    dec = np.nonzero(~b.is_prefill)[0]
+    pos_d = (b.ctx[dec] - 1).astype(np.uint32)
+    rs_d = dec.astype(np.int32)
+    q_d = rng.standard_normal((len(dec), hq * d), dtype=np.float32)
+    pf = np.nonzero(b.is_prefill)[0]
+    q_p = rng.standard_normal((len(pf) * 256, hq * d), dtype=np.float32)
+    bufs = dict(bo=be.to_device(offs), bi=be.to_device(ids), qd=be.to_device(q_d),
+                pos=be.to_device(pos_d), rs=be.to_device(rs_d), od=be.alloc(q_d.nbytes),
+                qp=be.to_device(q_p), op=be.alloc(q_p.nbytes),
+                pst=be.to_device((np.arange(len(pf)) * 256).astype(np.int32)),
+                pcnt=be.to_device(np.full(len(pf), 256, np.int32)),
+                pfp=be.to_device(b.cached[pf].astype(np.uint32)),
+                pbo=be.to_device(offs[pf].astype(np.int64)))
+    plan = oh.DecodePlan(be, pos_d, rs_d, offs, ids, hq, hkv, d, b.bs)
+
+    def attn():
+        oh.paged_attention_decode(be, kv, arena_ptr, 0, bufs["qd"].ptr, len(dec), hq,
+                                  bufs["pos"].ptr, bufs["rs"].ptr, bufs["bo"].ptr, bufs["bi"].ptr,
+                                  plan, bufs["od"].ptr)
+        oh.paged_attention_prefill(be, kv, arena_ptr, 0, bufs["qp"].ptr, hq, len(pf),
+                                   bufs["pst"].ptr, bufs["pcnt"].ptr, bufs["pfp"].ptr,
+                                   bufs["pbo"].ptr, bufs["bi"].ptr, 256, int(b.ctx.max()),
+                                   bufs["op"].ptr, hilo=False)
+    for _ in range(warmup):
+        attn()
+    be.kernel_timing(True)
+    for _ in range(steps):
+        attn()
+    split_ms = be.kernel_timing_read(be.K_DECODE_SPLIT)[0] / steps
+    merge_ms = be.kernel_timing_read(be.K_DECODE_MERGE)[0] / steps
+    pre_ms = be.kernel_timing_read(be.K_PREFILL)[0] / steps
+    be.kernel_timing(False)
+    uniq, logical = b.kv_bytes(hkv, d)
+    pf_flops = 4 * hq * d * int(sum(256 * int(b.cached[s]) + 256 * 257 // 2 for s in pf))
+    dec_ms = split_ms + merge_ms
+    res = {
+        "workload": "Qwen2-7B-shape layer (hidden 3584, 28q/4kv, d 128, ffn 18944, QKV bias; "
+                    "vocab cut to 1024), bf16 weights N(0,0.02) + bf16 KV N(0,1); 8 prefill "
+                    "chunks x 256 + 192 decodes, 50% share a 2048-token prefix, rest lognormal "
+                    "(median 1024, sigma 1.0) capped 16384, block 16",
+        "rows": n_rows,
+        "layer_ms": round(layer_ms, 4),
+        "layer_rows_per_s": round(n_rows / (layer_ms * 1e-3), 1),
+        "decode_attention": {
+            "rows": int(len(dec)), "ms": round(dec_ms, 5), "split_ms": round(split_ms, 5),
+            "unique_kv_bytes": uniq, "logical_kv_bytes": logical,
+            "unique_GBps": round(uniq / (dec_ms * 1e-3) / 1e9, 1),
+            "logical_GBps": round(logical / (dec_ms * 1e-3) / 1e9, 1),
+            "unique_frac_of_hbm_peak": round(uniq / (dec_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)},
+        "prefill_attention": {
+            "chunks": int(len(pf)), "ms": round(pre_ms, 5), "flops": pf_flops,
+            "tflops": round(pf_flops / (pre_ms * 1e-3) / 1e12, 1)},
+    }
+    plan.close()
+    for v in bufs.values():
+        v.free()
+    model.close()
+    be.close()
+    return res
+
+
 def cpu_decode_step(cfg, lens, tables, num_blocks, seqs):
     """The oracle (C++ restatement of the reference CPU TransformerModel) on one
     decode step of the same shapes.  Weights are a constant (the oracle's
@@ -246,6 +362,7 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU oracle baseline")
     ap.add_argument("--no-e2e", action="store_true", help="skip the config-4 decode step")
     ap.add_argument("--no-prefill", action="store_true", help="skip the config-3 prefill kernel")
+    ap.add_argument("--no-mixed", action="store_true", help="skip the config-5 mixed batch")
     ap.add_argument("--kv-layout", choices=["head-major", "reference"], default="reference",
                     help="block-internal order of the KV arena (reference = attention.rs order)")
     ap.add_argument("--copy-calibration", action="store_true",
@@ -364,6 +481,8 @@ def main():
     be.close()
     if not a.no_e2e:
         result["decode_e2e"] = decode_e2e(cpu=not a.no_cpu)
+    if not a.no_mixed:
+        result["mixed_cfg5"] = mixed_cfg5()
     print(json.dumps(result))
 
 

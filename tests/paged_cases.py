@@ -139,3 +139,77 @@ def cfg3(seed=20261203, head_major=False):
     prefixes = rng.integers(0, 7681, size=8)
     return PrefillCase(seed + 1, prefixes, [512] * 8, 32, 8, 128, 16, dtype="bf16",
                        head_major=head_major)
+
+
+class MixedBatch:
+    """A continuous batch mixing prefill chunks and decode rows, with prefix
+    sharing (BASELINE config 5's structure).  Sequence s has `cached[s]`
+    tokens in the cache before this step and contributes `counts[s]` new rows
+    at positions cached[s] .. cached[s] + counts[s] - 1.  Sharing sequences
+    start with the same `prefix` tokens, stored once: their tables begin with
+    the same block ids (refcount > 1 in orion-kv-cache terms).  The rest of
+    each context is lognormal (median `median`, shape `sigma`), capped so the
+    whole context stays <= `cap`."""
+
+    def __init__(self, seed, n_prefill, chunk, n_decode, share_frac, prefix, median, sigma, cap,
+                 block_size, vocab):
+        rng = np.random.default_rng(seed)
+        S = n_prefill + n_decode
+        self.S, self.bs = S, block_size
+        order = rng.permutation(S)
+        is_prefill = np.zeros(S, bool)
+        is_prefill[order[:n_prefill]] = True
+        shares = np.zeros(S, bool)
+        shares[rng.permutation(S)[:int(round(share_frac * S))]] = True
+        own = np.minimum(np.round(rng.lognormal(np.log(median), sigma, S)).astype(np.int64), cap)
+        self.counts = np.where(is_prefill, chunk, 1).astype(np.int64)
+        base = np.where(shares, prefix, 0)
+        self.cached = np.minimum(base + own, cap - self.counts)
+        self.cached = np.maximum(self.cached, base)  # a sharing context keeps the whole prefix
+        self.ctx = self.cached + self.counts
+        self.is_prefill, self.shares = is_prefill, shares
+        # block tables: the shared prefix blocks first, then private blocks
+        nshared = -(-prefix // block_size)
+        shared_ids = np.arange(nshared, dtype=np.uint32)
+        nxt = nshared
+        tables = []
+        for s in range(S):
+            need = -(-int(self.ctx[s]) // block_size)
+            if shares[s]:
+                priv = need - nshared
+                t = np.concatenate([shared_ids, np.arange(nxt, nxt + priv, dtype=np.uint32)])
+                nxt += priv
+            else:
+                t = np.arange(nxt, nxt + need, dtype=np.uint32)
+                nxt += need
+            tables.append(t)
+        # scatter the private blocks over the pool (the shared ones stay put)
+        self.num_blocks = int(nxt)
+        perm = np.concatenate([shared_ids, nshared + rng.permutation(nxt - nshared)]).astype(np.uint32)
+        self.tables = [perm[t] for t in tables]
+        self.positions = np.concatenate(
+            [np.arange(self.cached[s], self.ctx[s], dtype=np.uint32) for s in range(S)])
+        self.tokens = rng.integers(0, vocab, len(self.positions)).astype(np.uint32)
+        self.row_seq = np.repeat(np.arange(S, dtype=np.int32), self.counts)
+
+    def decode_rows(self):
+        starts = np.concatenate([[0], np.cumsum(self.counts)[:-1]])
+        return starts[~self.is_prefill]
+
+    def kv_bytes(self, hkv, d, esz=2):
+        """(unique, logical) K+V bytes one layer's attention reads for the
+        decode rows: blocks touched counted once vs every attended token."""
+        blk = hkv * d * 2 * esz * self.bs
+        dec = ~self.is_prefill
+        uniq = set()
+        for s in np.nonzero(dec)[0]:
+            uniq.update(self.tables[s][:-(-int(self.ctx[s]) // self.bs)].tolist())
+        logical = int(self.ctx[dec].sum()) * hkv * d * 2 * esz
+        return len(uniq) * blk, logical
+
+
+def cfg5_batch(vocab, seed=20261205):
+    """8 prefill chunks of 256 + 192 decodes; half of the
+    200 sequences share a 2048-token prefix; other context lognormal (median
+    1024; shape 1.0, not given by the config) capped at 16384; block 16."""
+    return MixedBatch(seed, 8, 256, 192, 0.5, 2048, 1024, 1.0, 16384, 16, vocab)

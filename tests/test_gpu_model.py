@@ -265,3 +265,56 @@ def test_prefill_route_matches_decode_route(backend, hq, hkv, d, monkeypatch):
                     assert np.abs(a - b).max() <= 2e-2 * np.abs(b).max()
     ga.close()
     gb.close()
+
+
+def test_mixed_batch_with_prefix_sharing(backend, monkeypatch):
+    # Config-5 structure at test size on a Qwen2-style layer (QKV bias, 7:1
+    # GQA, d 128): step 1 prefills every sequence's cached context (sharing
+    # sequences carry the same prefix tokens into the same shared blocks);
+    # step 2 is the mixed batch of prefill chunks and single decode rows.
+    # GPU vs oracle (bf16 KV: a dtype change, 2e-2), and prefill-kernel route
+    # vs decode-kernel route (f32-class agreement).
+    from paged_cases import MixedBatch
+    rng = np.random.default_rng(37)
+    spec = Spec(1, 256, 14, 2, 128, 512, 300, max_pos=1024, bias=True, tied=False,
+                num_blocks=0, block_size=16)
+    mb = MixedBatch(5, 3, 40, 9, 0.5, 64, 60, 0.7, 400, 16, spec.V)
+    spec.num_blocks = mb.num_blocks
+    W = random_weights(spec, rng, std=0.05)
+    ga = gpu_model(backend, spec, W, oh.BF16)
+    gb = gpu_model(backend, spec, W, oh.BF16)
+    om = oracle_model(spec, W)
+    prefix_tok = rng.integers(0, spec.V, 64)
+    # step 1: cached contexts
+    toks1, pos1 = [], []
+    for s in range(mb.S):
+        n = int(mb.cached[s])
+        t = rng.integers(0, spec.V, n)
+        if mb.shares[s]:
+            t[:64] = prefix_tok
+        toks1.append(t)
+        pos1.append(np.arange(n))
+    toks1, pos1 = np.concatenate(toks1), np.concatenate(pos1)
+    c1 = mb.cached.tolist()
+    b1 = batch(toks1, pos1, c1, mb.tables)
+    print(f"[mixed] step1 rows={len(toks1)}", flush=True)
+    la = ga.forward(b1).logits
+    o1 = om.forward(toks1, pos1, c1, c1, mb.tables)
+    assert rel_err(la, o1) <= 2e-2, rel_err(la, o1)
+    monkeypatch.setenv("ORION_PREFILL_ROUTE", "0")
+    lb = gb.forward(b1).logits
+    monkeypatch.delenv("ORION_PREFILL_ROUTE")
+    assert rel_err(la, lb) <= 2e-4, rel_err(la, lb)
+    # step 2: the mixed batch
+    c2 = mb.counts.tolist()
+    b2 = batch(mb.tokens, mb.positions, c2, mb.tables, mb.ctx.tolist())
+    print(f"[mixed] step2 rows={len(mb.tokens)} prefill={int(mb.is_prefill.sum())}", flush=True)
+    la = ga.forward(b2).logits
+    o2 = om.forward(mb.tokens, mb.positions, c2, mb.ctx.tolist(), mb.tables)
+    assert rel_err(la, o2) <= 2e-2, rel_err(la, o2)
+    monkeypatch.setenv("ORION_PREFILL_ROUTE", "0")
+    lb = gb.forward(b2).logits
+    monkeypatch.delenv("ORION_PREFILL_ROUTE")
+    assert rel_err(la, lb) <= 2e-4, rel_err(la, lb)
+    ga.close()
+    gb.close()
