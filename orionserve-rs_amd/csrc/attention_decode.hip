@@ -278,6 +278,20 @@ __device__ __forceinline__ void decode_wave_mfma2(
   const int l16 = lane & 15;  // token (K load) / head (scores, output)
   const int grp = lane >> 4;  // 16-lane group
 
+  // The query loads go out first (they are the first data the item needs),
+  // then the table slice; the first K/V step is issued before either is
+  // waited on (its block id travels in the work record).
+  constexpr int KCH_ = D / 32;
+  const int kd_ = grp * 8;
+  float4 qr[2 * KCH_];
+  {
+    const float* qp = q + ((int64_t)row * num_q_heads + (int64_t)kvh * G + min(l16, G - 1)) * D + kd_;
+#pragma unroll
+    for (int j = 0; j < KCH_; ++j) {
+      qr[2 * j] = *reinterpret_cast<const float4*>(qp + 32 * j);
+      qr[2 * j + 1] = *reinterpret_cast<const float4*>(qp + 32 * j + 4);
+    }
+  }
   const int first_blk = start >> bs_log2;
   const int nblk = ((end - 1) >> bs_log2) - first_blk + 1;
   const int my_blk = lane < nblk ? (int)tbl[lane] : 0;
@@ -322,6 +336,12 @@ __device__ __forceinline__ void decode_wave_mfma2(
     }
   };
 
+  // Register sets of the K/V pipeline; the first step is issued now.
+  uint4 ka[KCH], va_[RV], kb[KCH], vb[RV];
+  const int nsteps = (end - start + 15) >> 4;
+  auto step_base = [&](int i) { return min(start + 16 * i, end - 1) & ~15; };
+  issue(ka, va_, step_base(0), BIG_BLOCKS ? blk0 : -1);
+
   // ---- query group as the B operand of S = K . Q^T (hi/lo bf16) ----
   // Kept in a small per-wave LDS tile [hi|lo][G][D + 8] rather than in 32
   // VGPRs.  B-operand column l16 >= G reads head l16 % G: those columns of S
@@ -329,24 +349,13 @@ __device__ __forceinline__ void decode_wave_mfma2(
   constexpr int QROW = D + 8;
   const int qh = l16 % G;
   {
-    const float* qp = q + ((int64_t)row * num_q_heads + (int64_t)kvh * G + l16) * D + kd;
 #pragma unroll
     for (int j = 0; j < KCH; ++j) {
-      float a[8];
-      if (l16 < G) {
-        const float4 x0 = *reinterpret_cast<const float4*>(qp + 32 * j);
-        const float4 x1 = *reinterpret_cast<const float4*>(qp + 32 * j + 4);
-        a[0] = x0.x; a[1] = x0.y; a[2] = x0.z; a[3] = x0.w;
-        a[4] = x1.x; a[5] = x1.y; a[6] = x1.z; a[7] = x1.w;
-      } else {
-#pragma unroll
-        for (int e = 0; e < 8; ++e) a[e] = 0.f;
-      }
       uint4 hv, lv;
-      split2_trunc(a[0], a[1], hv.x, lv.x);
-      split2_trunc(a[2], a[3], hv.y, lv.y);
-      split2_trunc(a[4], a[5], hv.z, lv.z);
-      split2_trunc(a[6], a[7], hv.w, lv.w);
+      split2_trunc(qr[2 * j].x, qr[2 * j].y, hv.x, lv.x);
+      split2_trunc(qr[2 * j].z, qr[2 * j].w, hv.y, lv.y);
+      split2_trunc(qr[2 * j + 1].x, qr[2 * j + 1].y, hv.z, lv.z);
+      split2_trunc(qr[2 * j + 1].z, qr[2 * j + 1].w, hv.w, lv.w);
       if (l16 < G) {
         *reinterpret_cast<uint4*>(&QL[l16 * QROW + 32 * j + kd]) = hv;
         *reinterpret_cast<uint4*>(&QL[(G + l16) * QROW + 32 * j + kd]) = lv;
@@ -441,10 +450,6 @@ __device__ __forceinline__ void decode_wave_mfma2(
   // indices clamped into the chunk), so the compiler's wait counts are exact,
   // and a full pair of steps is one basic block, so one step's softmax and
   // P.V overlap the next step's Q.K^T.  LDS buffer parity = step parity.
-  uint4 ka[KCH], va_[RV], kb[KCH], vb[RV];
-  const int nsteps = (end - start + 15) >> 4;
-  auto step_base = [&](int i) { return min(start + 16 * i, end - 1) & ~15; };
-  issue(ka, va_, step_base(0), BIG_BLOCKS ? blk0 : -1);
   int i = 0;
   for (; i + 2 <= nsteps; i += 2) {
     issue(kb, vb, step_base(i + 1), -1);
