@@ -204,6 +204,45 @@ def decode_e2e(steps=64, seqs=32, seed=20261204, cpu=True):
     return res
 
 
+def gemm_shapes(reps=5):
+    """The projection GEMMs of the config-4 model at prefill M (the 17,526-token
+    prefill of decode_e2e) and decode M (32 rows), through orion_hip_gemm on
+    zero-filled operands (timing only).  Prefill shapes report algorithmic
+    TFLOP/s (2*M*N*K; the MFMA work issued is twice that, hi/lo activations);
+    decode shapes report weight-streaming GB/s (N*K*2 bytes of bf16 weights)."""
+    import orion_hip as oh
+
+    be = oh.HipBackend(0)
+    out = []
+    shapes = [("qkv", 2560, 2048, oh.GEMM_STORE), ("o", 2048, 2048, oh.GEMM_ACCUMULATE),
+              ("gate_up", 11264, 2048, oh.GEMM_SWIGLU), ("down", 2048, 5632, oh.GEMM_ACCUMULATE),
+              ("lm_head", 32000, 2048, oh.GEMM_STORE)]
+    for M in (17526, 32):
+        for name, N, K, ep in shapes:
+            if M > 64 and name == "lm_head":
+                continue  # the forward runs the head on the last rows only
+            x, w, o = be.alloc(M * K * 4), be.alloc(N * K * 2), be.alloc(M * N * 4)
+            for buf, n in ((x, M * K * 4), (w, N * K * 2), (o, M * N * 4)):
+                oh._check(be.lib.orion_hip_memset(be.handle, buf.ptr, 0, n))
+            for _ in range(2):
+                oh.gemm(be, x.ptr, w.ptr, None, M, N, K, ep, o.ptr)
+            be.synchronize()
+            be.timer_start()
+            for _ in range(reps):
+                oh.gemm(be, x.ptr, w.ptr, None, M, N, K, ep, o.ptr)
+            ms = be.timer_stop() / reps
+            rec = {"gemm": name, "M": M, "N": N, "K": K, "us": round(ms * 1e3, 1)}
+            if M > 64:
+                rec["tflops"] = round(2 * M * N * K / (ms * 1e-3) / 1e12, 1)
+            else:
+                rec["weight_GBps"] = round(N * K * 2 / (ms * 1e-3) / 1e9, 1)
+            out.append(rec)
+            for buf in (x, w, o):
+                buf.free()
+    be.close()
+    return out
+
+
 QWEN2_7B_LAYER = dict(H=3584, hq=28, hkv=4, d=128, F=18944, V=1024, eps=1e-6, theta=1000000.0,
                       max_pos=16640)
 
@@ -363,6 +402,7 @@ def main():
     ap.add_argument("--no-e2e", action="store_true", help="skip the config-4 decode step")
     ap.add_argument("--no-prefill", action="store_true", help="skip the config-3 prefill kernel")
     ap.add_argument("--no-mixed", action="store_true", help="skip the config-5 mixed batch")
+    ap.add_argument("--no-gemm", action="store_true", help="skip the GEMM shape timings")
     ap.add_argument("--kv-layout", choices=["head-major", "reference"], default="reference",
                     help="block-internal order of the KV arena (reference = attention.rs order)")
     ap.add_argument("--copy-calibration", action="store_true",
@@ -483,6 +523,8 @@ def main():
         result["decode_e2e"] = decode_e2e(cpu=not a.no_cpu)
     if not a.no_mixed:
         result["mixed_cfg5"] = mixed_cfg5()
+    if not a.no_gemm:
+        result["gemm"] = gemm_shapes()
     print(json.dumps(result))
 
 
