@@ -70,6 +70,10 @@ __device__ inline void store_kv<float>(float* p, float v) { *p = v; }
 template <>
 __device__ inline void store_kv<uint16_t>(uint16_t* p, float v) { *p = f32_to_bf16(v); }
 
+// One workgroup per (row, head): heads [0, hq) are Q, [hq, hq + hkv) K and
+// the rest V, which are also the column ranges of the fused QKV output, so
+// head u covers columns [u * D, (u + 1) * D).  Thread i holds element i and
+// takes its rotate-half partner (i +- D/2) from LDS.
 template <typename T>
 __global__ void __launch_bounds__(256)
     rope_cache_kernel(T* __restrict__ kv_layer, int64_t blk_stride, int64_t v_off,
@@ -80,42 +84,47 @@ __global__ void __launch_bounds__(256)
                       int64_t v_stride, const uint32_t* __restrict__ positions,
                       const int32_t* __restrict__ row_seq, const int64_t* __restrict__ bt_off,
                       const uint32_t* __restrict__ bt_ids, const float* __restrict__ cos_t,
-                      const float* __restrict__ sin_t) {
+                      const float* __restrict__ sin_t, GemmPartials qkv) {
 #pragma clang fp contract(off)
+  __shared__ float xs[256];
   const int64_t row = blockIdx.x;
-  const int half = D >> 1;
+  const int unit = blockIdx.y;
+  const int i = threadIdx.x;
+  const bool is_q = unit < hq, is_k = !is_q && unit < hq + hkv;
+  const int h = is_q ? unit : is_k ? unit - hq : unit - hq - hkv;
   const uint32_t pos = positions[row];
-  const float* cs = cos_t + (int64_t)pos * half;
-  const float* sn = sin_t + (int64_t)pos * half;
   const int seq = row_seq[row];
   const uint32_t blk = bt_ids[bt_off[seq] + (pos >> bs_log2)];
   const int64_t slot = pos & ((1u << bs_log2) - 1);
-  T* kdst = kv_layer + (int64_t)blk * blk_stride + slot * slot_stride;
-  T* vdst = kdst + v_off;
+  T* kdst = kv_layer + (int64_t)blk * blk_stride + slot * slot_stride + h * head_stride;
 
-  const int pairs_q = hq * half;
-  const int pairs_k = hkv * half;
-  for (int idx = threadIdx.x; idx < pairs_q + pairs_k; idx += blockDim.x) {
-    if (idx < pairs_q) {
-      const int h = idx / half, i = idx - h * half;
-      const float* src = q_in + row * q_stride + h * D;
-      const float x0 = src[i], x1 = src[i + half];
-      float* dst = q_out + row * (int64_t)hq * D + h * D;
-      dst[i] = x0 * cs[i] - x1 * sn[i];
-      dst[i + half] = x0 * sn[i] + x1 * cs[i];
-    } else {
-      const int kk = idx - pairs_q;
-      const int h = kk / half, i = kk - h * half;
-      const float* src = k + row * k_stride + h * D;
-      const float x0 = src[i], x1 = src[i + half];
-      store_kv<T>(kdst + h * head_stride + i, x0 * cs[i] - x1 * sn[i]);
-      store_kv<T>(kdst + h * head_stride + i + half, x0 * sn[i] + x1 * cs[i]);
-    }
+  // Inputs come from the q/k/v buffers, or straight from the QKV GEMM's
+  // unreduced partials.
+  float x = 0.f;
+  if (i < D) {
+    if (qkv.ws)
+      x = partial_sum(qkv, row, (int64_t)unit * D + i);
+    else
+      x = is_q ? q_in[row * q_stride + h * D + i]
+          : is_k ? k[row * k_stride + h * D + i]
+                 : v[row * v_stride + h * D + i];
   }
-  for (int idx = threadIdx.x; idx < hkv * D; idx += blockDim.x) {
-    const int h = idx / D;
-    store_kv<T>(vdst + h * head_stride + (idx - h * D), v[row * v_stride + idx]);
+  if (!is_q && !is_k) {  // uniform over the workgroup
+    if (i < D) store_kv<T>(kdst + v_off + i, x);
+    return;
   }
+  xs[i] = x;
+  __syncthreads();
+  if (i >= D) return;
+  const int half = D >> 1;
+  const int j = i < half ? i : i - half;
+  const float c = cos_t[(int64_t)pos * half + j], sn = sin_t[(int64_t)pos * half + j];
+  // out[j] = x0 cos - x1 sin, out[j + half] = x0 sin + x1 cos (x0 = x[j], x1 = x[j + half])
+  const float y = i < half ? x * c - xs[i + half] * sn : xs[j] * sn + x * c;
+  if (is_q)
+    q_out[row * (int64_t)hq * D + h * D + i] = y;
+  else
+    store_kv<T>(kdst + i, y);
 }
 
 hipError_t launch_rope_and_cache(hipStream_t st, const KvGeom& kv, void* arena, int64_t layer,
@@ -123,23 +132,30 @@ hipError_t launch_rope_and_cache(hipStream_t st, const KvGeom& kv, void* arena, 
                                  float* q_out, const float* k, int64_t k_stride, const float* v,
                                  int64_t v_stride, const uint32_t* positions,
                                  const int32_t* row_seq, const int64_t* bt_off,
-                                 const uint32_t* bt_ids, const float* cos_t, const float* sin_t) {
+                                 const uint32_t* bt_ids, const float* cos_t, const float* sin_t,
+                                 const GemmPartials* qkv_partials) {
   if (rows == 0) return hipSuccess;
+  const GemmPartials qp = qkv_partials ? *qkv_partials : GemmPartials{};
   int bs_log2 = 0;
   while ((1 << bs_log2) < kv.block_size) ++bs_log2;
   const ArenaStrides a = arena_strides(kv);
+  if (kv.head_dim > 256 || kv.head_dim % 2 || hq + 2 * kv.num_kv_heads > 65535 ||
+      rows > INT32_MAX)
+    return hipErrorInvalidValue;
+  const dim3 grid((unsigned)rows, (unsigned)(hq + 2 * kv.num_kv_heads));
+  const dim3 block((unsigned)((kv.head_dim + 63) & ~63));
   if (kv.dtype_bf16) {
     uint16_t* base = static_cast<uint16_t*>(arena) + layer * a.layer;
-    hipLaunchKernelGGL(rope_cache_kernel<uint16_t>, dim3((unsigned)rows), dim3(256), 0, st, base,
+    hipLaunchKernelGGL(rope_cache_kernel<uint16_t>, grid, block, 0, st, base,
                        a.blk, a.v_off, a.slot, a.head, bs_log2, (int)hq, (int)kv.num_kv_heads,
                        (int)kv.head_dim, q_in, q_stride, q_out, k, k_stride, v, v_stride,
-                       positions, row_seq, bt_off, bt_ids, cos_t, sin_t);
+                       positions, row_seq, bt_off, bt_ids, cos_t, sin_t, qp);
   } else {
     float* base = static_cast<float*>(arena) + layer * a.layer;
-    hipLaunchKernelGGL(rope_cache_kernel<float>, dim3((unsigned)rows), dim3(256), 0, st, base,
+    hipLaunchKernelGGL(rope_cache_kernel<float>, grid, block, 0, st, base,
                        a.blk, a.v_off, a.slot, a.head, bs_log2, (int)hq, (int)kv.num_kv_heads,
                        (int)kv.head_dim, q_in, q_stride, q_out, k, k_stride, v, v_stride,
-                       positions, row_seq, bt_off, bt_ids, cos_t, sin_t);
+                       positions, row_seq, bt_off, bt_ids, cos_t, sin_t, qp);
   }
   return hipGetLastError();
 }
@@ -162,27 +178,53 @@ hipError_t launch_silu_mul(hipStream_t st, float* gate, const float* up, int64_t
 
 // argmax (runtime/src/sampling.rs:196-207): strict '>' from -inf, so NaN and
 // -inf never win and the lowest index wins a tie; -1 if nothing qualifies.
-__global__ void __launch_bounds__(256)
+// One 1024-thread workgroup per row; each thread scans its float4s in
+// increasing index order, four loads in flight.
+__global__ void __launch_bounds__(1024)
     argmax_kernel(const float* __restrict__ logits, int64_t cols, int64_t* __restrict__ out) {
-  __shared__ float bv[4];
-  __shared__ int64_t bi[4];
+  constexpr int T = 1024;
+  __shared__ float bv[T / 64];
+  __shared__ int64_t bi[T / 64];
   const float* row = logits + (int64_t)blockIdx.x * cols;
   float best = -INFINITY;
   int64_t idx = -1;
-  for (int64_t i = threadIdx.x; i < cols; i += 256) {
-    const float v = row[i];
-    if (v > best) {  // strided scan visits increasing i, so '>' keeps the lowest index
+  auto take = [&](float v, int64_t i) {
+    if (v > best) {  // indices arrive in increasing order: '>' keeps the lowest
       best = v;
       idx = i;
     }
+  };
+  auto take4 = [&](const float4& v, int64_t i4) {
+    take(v.x, 4 * i4);
+    take(v.y, 4 * i4 + 1);
+    take(v.z, 4 * i4 + 2);
+    take(v.w, 4 * i4 + 3);
+  };
+  if ((cols & 3) == 0 && (reinterpret_cast<uintptr_t>(row) & 15) == 0) {
+    const float4* r4 = reinterpret_cast<const float4*>(row);
+    const int64_t n4 = cols >> 2;
+    int64_t i = threadIdx.x;
+    for (; i + 3 * T < n4; i += 4 * T) {
+      const float4 a = r4[i], b = r4[i + T], c = r4[i + 2 * T], d = r4[i + 3 * T];
+      take4(a, i);
+      take4(b, i + T);
+      take4(c, i + 2 * T);
+      take4(d, i + 3 * T);
+    }
+    for (; i < n4; i += T) take4(r4[i], i);
+  } else {
+    for (int64_t i = threadIdx.x; i < cols; i += T) take(row[i], i);
   }
-  for (int off = 32; off > 0; off >>= 1) {
-    const float ov = __shfl_xor(best, off);
-    const int64_t oi = __shfl_xor(idx, off);
+  auto merge = [&](float ov, int64_t oi) {
     if (oi >= 0 && (idx < 0 || ov > best || (ov == best && oi < idx))) {
       best = ov;
       idx = oi;
     }
+  };
+  for (int off = 32; off > 0; off >>= 1) {
+    const float ov = __shfl_xor(best, off);
+    const int64_t oi = __shfl_xor(idx, off);
+    merge(ov, oi);
   }
   if ((threadIdx.x & 63) == 0) {
     bv[threadIdx.x >> 6] = best;
@@ -190,12 +232,7 @@ __global__ void __launch_bounds__(256)
   }
   __syncthreads();
   if (threadIdx.x == 0) {
-    for (int wv = 1; wv < 4; ++wv) {
-      if (bi[wv] >= 0 && (idx < 0 || bv[wv] > best || (bv[wv] == best && bi[wv] < idx))) {
-        best = bv[wv];
-        idx = bi[wv];
-      }
-    }
+    for (int wv = 1; wv < T / 64; ++wv) merge(bv[wv], bi[wv]);
     out[blockIdx.x] = idx;
   }
 }
@@ -203,7 +240,7 @@ __global__ void __launch_bounds__(256)
 hipError_t launch_argmax(hipStream_t st, const float* logits, int64_t rows, int64_t cols,
                          int64_t* out) {
   if (rows == 0) return hipSuccess;
-  hipLaunchKernelGGL(argmax_kernel, dim3((unsigned)rows), dim3(256), 0, st, logits, cols, out);
+  hipLaunchKernelGGL(argmax_kernel, dim3((unsigned)rows), dim3(1024), 0, st, logits, cols, out);
   return hipGetLastError();
 }
 

@@ -342,9 +342,12 @@ template <int MT, int NT, int KSTEPS>
 __global__ void __launch_bounds__(256)
     gemm_gemv_kernel(const float* __restrict__ x, const uint16_t* __restrict__ w,
                      const float* __restrict__ bias, int M, int N, int K, int ep,
-                     float* __restrict__ out, float* __restrict__ partial) {
+                     float* __restrict__ out, float* __restrict__ partial,
+                     const double* __restrict__ nsq, int nslots, const float* __restrict__ nw,
+                     float neps) {
   constexpr int BN = 64 * NT;
   __shared__ __attribute__((aligned(16))) uint4 xs[2][MT * KSTEPS * 64];  // [hi|lo][frag][lane]
+  __shared__ float nscale[MT * 16];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -368,21 +371,58 @@ __global__ void __launch_bounds__(256)
   }
 
   // 2. activation slice -> LDS hi/lo fragments: fragment f = (mt, step),
-  //    lane l holds row mt*16 + l%16, k = step*32 + (l/16)*8 .. +8.
-  for (int idx = tid; idx < MT * KSTEPS * 64; idx += 256) {
+  //    lane l holds row mt*16 + l%16, k = step*32 + (l/16)*8 .. +8.  Every
+  //    fragment load is issued before the norm scales are waited for.
+  constexpr int FR = MT * KSTEPS * 64 / 256;  // fragments per thread
+  static_assert(MT * KSTEPS * 64 % 256 == 0, "fragments must split evenly over the workgroup");
+  float4 xa[FR][2], wa[FR][2];
+#pragma unroll
+  for (int j = 0; j < FR; ++j) {
+    const int idx = tid + j * 256;
     const int fl = idx & 63, f = idx >> 6;
     const int mt = f / KSTEPS, s2 = f - mt * KSTEPS;
     const int row = mt * 16 + (fl & 15);
-    float a[8];
+    const float4 z = {0.f, 0.f, 0.f, 0.f};
+    xa[j][0] = xa[j][1] = wa[j][0] = wa[j][1] = z;
     if (row < M && s2 < nsteps) {
       const float* xp = x + (int64_t)row * K + k0 + s2 * 32 + (fl >> 4) * 8;
-      const float4 x0 = *reinterpret_cast<const float4*>(xp);
-      const float4 x1 = *reinterpret_cast<const float4*>(xp + 4);
-      a[0] = x0.x; a[1] = x0.y; a[2] = x0.z; a[3] = x0.w;
-      a[4] = x1.x; a[5] = x1.y; a[6] = x1.z; a[7] = x1.w;
-    } else {
+      xa[j][0] = *reinterpret_cast<const float4*>(xp);
+      xa[j][1] = *reinterpret_cast<const float4*>(xp + 4);
+      if (nsq) {
+        const float* wp = nw + k0 + s2 * 32 + (fl >> 4) * 8;
+        wa[j][0] = *reinterpret_cast<const float4*>(wp);
+        wa[j][1] = *reinterpret_cast<const float4*>(wp + 4);
+      }
+    }
+  }
+  // Fused RMSNorm of the input rows: scale = 1 / sqrt(mean(x^2) + eps) from
+  // the f64 sum-of-squares slots (as rmsnorm_kernel computes it), then
+  // x * scale * weight with rmsnorm's order of the two products.
+  if (nsq) {
+    if (tid < MT * 16) {
+      float sc = 0.f;
+      if (tid < M) {
+        double t = 0.0;
+        for (int j = 0; j < nslots; ++j) t += nsq[(int64_t)tid * nslots + j];
+        sc = (float)(1.0 / sqrt(t / (double)K + (double)neps));
+      }
+      nscale[tid] = sc;
+    }
+    __syncthreads();
+  }
 #pragma unroll
-      for (int e = 0; e < 8; ++e) a[e] = 0.f;
+  for (int j = 0; j < FR; ++j) {
+    const int idx = tid + j * 256;
+    const int fl = idx & 63, f = idx >> 6;
+    const int row = (f / KSTEPS) * 16 + (fl & 15);
+    float a[8] = {xa[j][0].x, xa[j][0].y, xa[j][0].z, xa[j][0].w,
+                  xa[j][1].x, xa[j][1].y, xa[j][1].z, xa[j][1].w};
+    if (nsq) {
+      const float sc = row < M ? nscale[row] : 0.f;
+      const float wv[8] = {wa[j][0].x, wa[j][0].y, wa[j][0].z, wa[j][0].w,
+                           wa[j][1].x, wa[j][1].y, wa[j][1].z, wa[j][1].w};
+#pragma unroll
+      for (int e = 0; e < 8; ++e) a[e] = a[e] * sc * wv[e];
     }
     uint4 hv, lv;
     split2_trunc(a[0], a[1], hv.x, lv.x);
@@ -462,7 +502,7 @@ template <int MT, int NT>
 __global__ void __launch_bounds__(256)
     gemm_gemv_reduce_kernel(const float* __restrict__ partial, int kslices, int n_tiles,
                             const float* __restrict__ bias, int M, int N, int ep,
-                            float* __restrict__ out) {
+                            float* __restrict__ out, double* __restrict__ sumsq) {
   constexpr int BN = 64 * NT;
   const int64_t tile_elems = (int64_t)MT * 16 * BN;
   const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;  // over n_tiles * M * BN
@@ -479,12 +519,22 @@ __global__ void __launch_bounds__(256)
     const float u = __shfl_xor(v, 8);
     if ((c & 15) < 8 && col < N)
       out[(int64_t)row * (N >> 1) + ((col & ~15) >> 1) + (c & 7)] = v / (1.0f + __expf(-v)) * u;
-  } else if (col < N) {
-    float* op = out + (int64_t)row * N + col;
-    if (ep == (int)Epilogue::kAccumulate)
-      *op += v;
-    else
-      *op = bias ? v + bias[col] : v;
+  } else {
+    float nv = 0.f;
+    if (col < N) {
+      float* op = out + (int64_t)row * N + col;
+      if (ep == (int)Epilogue::kAccumulate)
+        nv = *op + v;
+      else
+        nv = bias ? v + bias[col] : v;
+      *op = nv;
+    }
+    // Sum of squares of the updated row, one f64 slot per (row, 64 columns):
+    // a wave covers 64 consecutive columns of one row.
+    if (sumsq) {
+      const double q = wave_sum_f64((double)nv * (double)nv);
+      if ((threadIdx.x & 63) == 0) sumsq[(int64_t)row * (NT * n_tiles) + tile * NT + (c >> 6)] = q;
+    }
   }
 }
 
@@ -512,34 +562,85 @@ static void launch_skinny(int KW, dim3 grid, hipStream_t st, const float* x, con
 }
 
 namespace {
-constexpr int kGemvNT = 2, kGemvKSteps = 8;
+// Split-K decode GEMM geometry: NT x 64 columns per workgroup (BN) and KS
+// k-steps of 32 per K slice.  ORION_GEMV_NT / ORION_GEMV_KS override the
+// defaults (measurement knobs; NT in {1, 2, 4}, KS in {4, 8, 16}).
+int gemv_knob(const char* name, int def, int a, int b, int c) {
+  const char* e = getenv(name);
+  const int v = e ? atoi(e) : def;
+  return (v == a || v == b || v == c) ? v : def;
+}
+int gemv_nt() {
+  static const int v = gemv_knob("ORION_GEMV_NT", 2, 1, 2, 4);
+  return v;
+}
+int gemv_ks() {
+  static const int v = gemv_knob("ORION_GEMV_KS", 8, 4, 8, 16);
+  return v;
+}
 struct GemvShape {
-  int mt, n_tiles, kslices;
+  int mt, nt, ks, n_tiles, kslices;
   size_t ws_bytes;
 };
 GemvShape gemv_shape(int64_t M, int64_t N, int64_t K) {
   GemvShape g;
   g.mt = (int)((M + 15) / 16);
-  g.n_tiles = (int)((N + 64 * kGemvNT - 1) / (64 * kGemvNT));
-  g.kslices = (int)((K + kGemvKSteps * 32 - 1) / (kGemvKSteps * 32));
-  g.ws_bytes = g.kslices > 1 ? (size_t)g.kslices * g.n_tiles * g.mt * 16 * 64 * kGemvNT * 4 : 0;
+  g.nt = gemv_nt();
+  g.ks = gemv_ks();
+  g.n_tiles = (int)((N + 64 * g.nt - 1) / (64 * g.nt));
+  g.kslices = (int)((K + g.ks * 32 - 1) / (g.ks * 32));
+  g.ws_bytes = g.kslices > 1 ? (size_t)g.kslices * g.n_tiles * g.mt * 16 * 64 * g.nt * 4 : 0;
   return g;
+}
+template <int MT, int NT, int KS>
+void launch_gemv_t(const GemvShape& g, hipStream_t st, const float* x, const uint16_t* w,
+                   const float* bias, int M, int N, int K, int ep, float* out,
+                   const GemmScratch* sc, const GemmFuse& f, bool reduce) {
+  hipLaunchKernelGGL((gemm_gemv_kernel<MT, NT, KS>),
+                     dim3((unsigned)g.n_tiles, (unsigned)g.kslices), dim3(256), 0, st, x, w, bias,
+                     M, N, K, ep, out, sc ? sc->ws : nullptr, f.norm_sumsq, f.norm_slots,
+                     f.norm_weight, f.norm_eps);
+  if (g.kslices > 1 && reduce) {
+    const int64_t threads = (int64_t)g.n_tiles * M * 64 * NT;
+    hipLaunchKernelGGL((gemm_gemv_reduce_kernel<MT, NT>),
+                       dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, st, sc->ws,
+                       g.kslices, g.n_tiles, bias, M, N, ep, out, f.sumsq_out);
+  }
+}
+template <int MT, int NT>
+void launch_gemv_nt(const GemvShape& g, hipStream_t st, const float* x, const uint16_t* w,
+                    const float* bias, int M, int N, int K, int ep, float* out,
+                    const GemmScratch* sc, const GemmFuse& f, bool reduce) {
+  if (g.ks == 4)
+    launch_gemv_t<MT, NT, 4>(g, st, x, w, bias, M, N, K, ep, out, sc, f, reduce);
+  else if (g.ks == 16)
+    launch_gemv_t<MT, NT, 16>(g, st, x, w, bias, M, N, K, ep, out, sc, f, reduce);
+  else
+    launch_gemv_t<MT, NT, 8>(g, st, x, w, bias, M, N, K, ep, out, sc, f, reduce);
 }
 template <int MT>
 void launch_gemv(const GemvShape& g, hipStream_t st, const float* x, const uint16_t* w,
                  const float* bias, int M, int N, int K, int ep, float* out,
-                 const GemmScratch* sc) {
-  hipLaunchKernelGGL((gemm_gemv_kernel<MT, kGemvNT, kGemvKSteps>),
-                     dim3((unsigned)g.n_tiles, (unsigned)g.kslices), dim3(256), 0, st, x, w, bias,
-                     M, N, K, ep, out, sc ? sc->ws : nullptr);
-  if (g.kslices > 1) {
-    const int64_t threads = (int64_t)g.n_tiles * M * 64 * kGemvNT;
-    hipLaunchKernelGGL((gemm_gemv_reduce_kernel<MT, kGemvNT>),
-                       dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, st, sc->ws,
-                       g.kslices, g.n_tiles, bias, M, N, ep, out);
-  }
+                 const GemmScratch* sc, const GemmFuse& f, bool reduce) {
+  if (g.nt == 1)
+    launch_gemv_nt<MT, 1>(g, st, x, w, bias, M, N, K, ep, out, sc, f, reduce);
+  else if (g.nt == 4)
+    launch_gemv_nt<MT, 4>(g, st, x, w, bias, M, N, K, ep, out, sc, f, reduce);
+  else
+    launch_gemv_nt<MT, 2>(g, st, x, w, bias, M, N, K, ep, out, sc, f, reduce);
 }
 }  // namespace
+
+bool gemm_splitk_fusable(int64_t M, int64_t K) {
+  if (M < 1 || M > 64 || K % 32 != 0 || K > INT32_MAX) return false;
+  const int64_t kslices = (K + gemv_ks() * 32 - 1) / (gemv_ks() * 32);
+  return kslices > 1 && kslices <= 65535;
+}
+
+int gemm_sumsq_slots(int64_t N) {
+  const int nt = gemv_nt();
+  return nt * (int)((N + 64 * nt - 1) / (64 * nt));
+}
 
 void gemm_scratch_need(int64_t M, int64_t N, int64_t K, size_t* ws_bytes, int64_t* counters) {
   if (M < 1 || M > 64 || K % 32 != 0) {
@@ -554,7 +655,13 @@ void gemm_scratch_need(int64_t M, int64_t N, int64_t K, size_t* ws_bytes, int64_
 
 hipError_t launch_gemm(hipStream_t st, const float* x, const uint16_t* w, const float* bias,
                        int64_t M, int64_t N, int64_t K, Epilogue ep, float* out,
-                       const GemmScratch* scratch) {
+                       const GemmScratch* scratch, const GemmFuse* fuse) {
+  const GemmFuse f = fuse ? *fuse : GemmFuse{};
+  if (f.defer) *f.defer = GemmPartials{};
+  const bool needs_splitk = f.norm_sumsq || f.sumsq_out;
+  if (needs_splitk && (!gemm_splitk_fusable(M, K) || (f.sumsq_out && ep != Epilogue::kAccumulate) ||
+                       (f.norm_sumsq && (!f.norm_weight || f.norm_slots < 1))))
+    return hipErrorInvalidValue;
   if (M == 0 || N == 0) return hipSuccess;
   if (K % 32 != 0 || K == 0) return hipErrorInvalidValue;
   if (ep == Epilogue::kSwiGLU && N % 16 != 0) return hipErrorInvalidValue;
@@ -568,13 +675,25 @@ hipError_t launch_gemm(hipStream_t st, const float* x, const uint16_t* w, const 
   if (M <= 64 && N <= INT32_MAX && K <= INT32_MAX) {
     const GemvShape g = gemv_shape(M, N, K);
     const bool fits = g.kslices == 1 || (scratch && scratch->ws_bytes >= g.ws_bytes);
+    if (needs_splitk && !fits) return hipErrorInvalidValue;
     if (fits && g.kslices <= 65535) {
       const int m = (int)M, n = (int)N, k = (int)K, e = (int)ep;
+      // A consumer that takes the unreduced partials gets them (no reduce
+      // launch); only for the store / accumulate epilogues.
+      const bool deferred = f.defer && g.kslices > 1 && ep == Epilogue::kStore && !f.sumsq_out;
+      if (deferred) {
+        f.defer->ws = scratch->ws;
+        f.defer->kslices = g.kslices;
+        f.defer->n_tiles = g.n_tiles;
+        f.defer->bn = 64 * g.nt;
+        f.defer->tile_rows = g.mt * 16;
+        f.defer->bias = bias;
+      }
       switch (g.mt) {
-        case 1: launch_gemv<1>(g, st, x, w, bias, m, n, k, e, out, scratch); break;
-        case 2: launch_gemv<2>(g, st, x, w, bias, m, n, k, e, out, scratch); break;
-        case 3: launch_gemv<3>(g, st, x, w, bias, m, n, k, e, out, scratch); break;
-        default: launch_gemv<4>(g, st, x, w, bias, m, n, k, e, out, scratch); break;
+        case 1: launch_gemv<1>(g, st, x, w, bias, m, n, k, e, out, scratch, f, !deferred); break;
+        case 2: launch_gemv<2>(g, st, x, w, bias, m, n, k, e, out, scratch, f, !deferred); break;
+        case 3: launch_gemv<3>(g, st, x, w, bias, m, n, k, e, out, scratch, f, !deferred); break;
+        default: launch_gemv<4>(g, st, x, w, bias, m, n, k, e, out, scratch, f, !deferred); break;
       }
       return hipGetLastError();
     }

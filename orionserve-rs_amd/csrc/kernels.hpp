@@ -97,6 +97,26 @@ enum class Epilogue : int {
   kSwiGLU = 2,      // W rows interleaved in groups of 8 gate / 8 up rows;
                     // out[:, N/2] = silu(gate) * up
 };
+// K-slice partial tiles a split-K decode GEMM left unreduced for its consumer
+// to sum (ws == nullptr: the GEMM wrote its output).  Element (row, col) =
+// bias[col] (if any) + sum over slices ks, in slice order, of
+// ws[((ks * n_tiles + col / bn) * tile_rows + row) * bn + col % bn].
+struct GemmPartials {
+  const float* ws = nullptr;
+  int kslices = 0, n_tiles = 0, bn = 0, tile_rows = 0;
+  const float* bias = nullptr;
+};
+#ifdef __HIPCC__
+__device__ inline float partial_sum(const GemmPartials& p, int64_t row, int64_t col) {
+  const int64_t tile = col / p.bn, c = col - tile * p.bn;
+  const float* e = p.ws + (tile * p.tile_rows + row) * p.bn + c;
+  const int64_t stride = (int64_t)p.n_tiles * p.tile_rows * p.bn;
+  float v = 0.f;
+  for (int ks = 0; ks < p.kslices; ++ks) v += e[ks * stride];
+  return p.bias ? v + p.bias[col] : v;
+}
+#endif
+
 // Scratch for split-K decode GEMMs: partial tiles and per-column-tile
 // arrival counters (zero between calls; the kernel re-arms them).
 struct GemmScratch {
@@ -105,11 +125,33 @@ struct GemmScratch {
   unsigned int* counters = nullptr;
   int64_t num_counters = 0;
 };
+// Fusions a decode-shaped split-K GEMM (gemm_splitk_fusable) performs with
+// its neighbours, so the RMSNorm and residual-add launches between the layer's
+// GEMMs disappear:
+//  - norm_*: x is the residual stream, and the GEMM multiplies
+//    rms_norm(x[row]) * norm_weight, with the row's scale taken from the
+//    per-row f64 sum-of-squares slots [row][norm_slots] a previous GEMM wrote
+//    (summed in slot order) -- the same per-element roundings as rmsnorm;
+//  - sumsq_out (kAccumulate): after out += x W^T, the GEMM writes the f64 sum
+//    of squares of each updated row in gemm_sumsq_slots(N) slots per row;
+//  - defer (kStore): the K-slice partials are left unreduced for the consumer
+//    (launch_rope_and_cache) instead of a reduce launch.
+struct GemmFuse {
+  const double* norm_sumsq = nullptr;
+  int norm_slots = 0;
+  const float* norm_weight = nullptr;
+  float norm_eps = 0.f;
+  double* sumsq_out = nullptr;
+  GemmPartials* defer = nullptr;
+};
+bool gemm_splitk_fusable(int64_t M, int64_t K);
+int gemm_sumsq_slots(int64_t N);
+
 // Scratch a launch_gemm of this shape needs (0 / 0: none).
 void gemm_scratch_need(int64_t M, int64_t N, int64_t K, size_t* ws_bytes, int64_t* counters);
 hipError_t launch_gemm(hipStream_t st, const float* x, const uint16_t* w, const float* bias,
                        int64_t M, int64_t N, int64_t K, Epilogue ep, float* out,
-                       const GemmScratch* scratch = nullptr);
+                       const GemmScratch* scratch = nullptr, const GemmFuse* fuse = nullptr);
 
 // ---- elementwise / normalisation -------------------------------------------
 hipError_t launch_embed(hipStream_t st, const uint32_t* tokens, int64_t n, const uint16_t* table,
@@ -117,12 +159,16 @@ hipError_t launch_embed(hipStream_t st, const uint32_t* tokens, int64_t n, const
 // rows selected by `row_index` (nullptr = identity)
 hipError_t launch_rmsnorm(hipStream_t st, const float* x, const int32_t* row_index,
                           const float* weight, int64_t rows, int64_t cols, float eps, float* out);
+// hidden[r] += (deferred GEMM output)[r], then out = rms_norm(hidden[r]) (the
+// residual add of transformer.rs:328-345 fused with the next norm).  With
+// row_index, only the gathered rows are computed and hidden is not written.
 hipError_t launch_rope_and_cache(hipStream_t st, const KvGeom& kv, void* arena, int64_t layer,
                                  int64_t rows, int64_t hq, const float* q_in, int64_t q_stride,
                                  float* q_out, const float* k, int64_t k_stride, const float* v,
                                  int64_t v_stride, const uint32_t* positions,
                                  const int32_t* row_seq, const int64_t* bt_off,
-                                 const uint32_t* bt_ids, const float* cos_t, const float* sin_t);
+                                 const uint32_t* bt_ids, const float* cos_t, const float* sin_t,
+                                 const GemmPartials* qkv_partials = nullptr);
 hipError_t launch_silu_mul(hipStream_t st, float* gate, const float* up, int64_t count);
 hipError_t launch_argmax(hipStream_t st, const float* logits, int64_t rows, int64_t cols,
                          int64_t* out);

@@ -218,14 +218,15 @@ struct orion_hip_model {
   size_t arena_bytes = 0;
 
   // activations / batch buffers (grown on demand)
-  DevBuf hidden, xn, qkv, qrot, attn, act, logits, argmax, ws;
+  DevBuf hidden, xn, qkv, qrot, attn, act, logits, argmax, ws, sumsq;
   DevBuf b_tokens, b_positions, b_rowseq, b_btoff, b_btids, b_last;
   void* pinned = nullptr;
   size_t pinned_bytes = 0;
 
   ~orion_hip_model() {
     for (void* p : allocations) (void)hipFree(p);
-    for (DevBuf* b : {&hidden, &xn, &qkv, &qrot, &attn, &act, &logits, &argmax, &ws, &b_tokens,
+    for (DevBuf* b : {&hidden, &xn, &qkv, &qrot, &attn, &act, &logits, &argmax, &ws, &sumsq,
+                      &b_tokens,
                       &b_positions, &b_rowseq, &b_btoff, &b_btids, &b_last})
       b->release();
     if (pinned) (void)hipHostFree(pinned);
@@ -446,11 +447,11 @@ static hipError_t gemm_scratch(orion_hip_device* dev, int64_t M, int64_t N, int6
 
 static hipError_t gemm_on(orion_hip_device* dev, const float* x, const uint16_t* w,
                           const float* bias, int64_t M, int64_t N, int64_t K, Epilogue ep,
-                          float* out) {
+                          float* out, const GemmFuse* fuse = nullptr) {
   GemmScratch sc;
   hipError_t e = gemm_scratch(dev, M, N, K, &sc);
   if (e != hipSuccess) return e;
-  return launch_gemm(dev->stream, x, w, bias, M, N, K, ep, out, &sc);
+  return launch_gemm(dev->stream, x, w, bias, M, N, K, ep, out, &sc, fuse);
 }
 
 // ---------------------------------------------------------------------------
@@ -939,6 +940,18 @@ ORION_EXPORT int orion_hip_model_forward(orion_hip_model* m, const orion_hip_bat
   HIP_TRY(st, m->act.reserve(n * F * 4));
   HIP_TRY(st, m->logits.reserve(S * V * 4));
   HIP_TRY(st, m->argmax.reserve(S * 8));
+  // Decode-shaped batches run the layer with the split-K GEMM fusions: each
+  // residual-add GEMM also writes the per-row sums of squares, the next GEMM
+  // applies the RMSNorm to its input, and the QKV partials go straight into
+  // RoPE + cache write.  ORION_GEMM_FUSE=0 runs the separate launches.
+  static const bool allow_fuse = [] {
+    const char* v = getenv("ORION_GEMM_FUSE");
+    return !(v && v[0] == '0');
+  }();
+  const bool fused = allow_fuse && gemm_splitk_fusable(n, H) && gemm_splitk_fusable(n, m->qd) &&
+                     gemm_splitk_fusable(n, F);
+  const int nslots = gemm_sumsq_slots(H);
+  if (fused) HIP_TRY(st, m->sumsq.reserve(n * nslots * 8));
   // Attention routing, shared by every layer.  A sequence whose rows are a
   // chunk of consecutive positions with at least half a prefill tile of
   // (row, query head) pairs goes to the MFMA prefill kernel (bf16 arena);
@@ -1049,14 +1062,38 @@ ORION_EXPORT int orion_hip_model_forward(orion_hip_model* m, const orion_hip_bat
   float* attn = m->attn.as<float>();
   float* act = m->act.as<float>();
 
+  double* sumsq = fused ? m->sumsq.as<double>() : nullptr;
+  // The norm a GEMM applies to its input (fused) / nothing (separate norm).
+  auto norm_in = [&](const float* weight) {
+    GemmFuse f;
+    if (fused) {
+      f.norm_sumsq = sumsq;
+      f.norm_slots = nslots;
+      f.norm_weight = weight;
+      f.norm_eps = d.rms_norm_eps;
+    }
+    return f;
+  };
+  GemmFuse accumulate;  // residual-add GEMMs: out += x W^T (+ row sums of squares)
+  accumulate.sumsq_out = sumsq;
+  GemmPartials part{};
   HIP_TRY(st, launch_embed(stream, d_tok, n, m->w_embed, H, hidden));
   for (int64_t l = 0; l < d.num_layers; ++l) {
     const LayerDev& L = m->layers[l];
-    HIP_TRY(st, launch_rmsnorm(stream, hidden, nullptr, L.input_norm, n, H, d.rms_norm_eps, xn));
-    HIP_TRY(st, gemm_on(m->dev, xn, L.w_qkv, L.b_qkv, n, m->qkvd, H, Epilogue::kStore, qkv));
+    // QKV input: rms_norm(hidden) * input_norm -- a kernel of its own unless
+    // the previous layer's down GEMM left the sums of squares.
+    GemmFuse qkv_f = l > 0 ? norm_in(L.input_norm) : GemmFuse{};
+    const float* qkv_x = hidden;
+    if (!qkv_f.norm_sumsq) {
+      HIP_TRY(st, launch_rmsnorm(stream, hidden, nullptr, L.input_norm, n, H, d.rms_norm_eps, xn));
+      qkv_x = xn;
+    }
+    qkv_f.defer = &part;
+    HIP_TRY(st, gemm_on(m->dev, qkv_x, L.w_qkv, L.b_qkv, n, m->qkvd, H, Epilogue::kStore, qkv,
+                        &qkv_f));
     HIP_TRY(st, launch_rope_and_cache(stream, m->kv, m->arena, l, n, Hq, qkv, m->qkvd, qrot,
                                       qkv + m->qd, m->qkvd, qkv + m->qd + m->kvd, m->qkvd, d_pos,
-                                      d_rs, d_btoff, d_btids, m->rope_cos, m->rope_sin));
+                                      d_rs, d_btoff, d_btids, m->rope_cos, m->rope_sin, &part));
     HIP_TRY(st, launch_paged_decode(stream, m->kv, m->arena, l, qrot, n, Hq, d_pos, d_rs, d_btoff,
                                     d_btids, dplan, attn));
     if (npf)
@@ -1064,11 +1101,14 @@ ORION_EXPORT int orion_hip_model_forward(orion_hip_model* m, const orion_hip_bat
                                        d_pfcount, d_pfpos, d_pfoff, d_btids, pf_max_rows,
                                        hb.max_position, /*hilo=*/true, attn));
     HIP_TRY(st, gemm_on(m->dev, attn, L.w_o, nullptr, n, H, m->qd, Epilogue::kAccumulate,
-                            hidden));
-    HIP_TRY(st, launch_rmsnorm(stream, hidden, nullptr, L.post_norm, n, H, d.rms_norm_eps, xn));
-    HIP_TRY(st, gemm_on(m->dev, xn, L.w_gu, nullptr, n, 2 * F, H, Epilogue::kSwiGLU, act));
-    HIP_TRY(st, gemm_on(m->dev, act, L.w_down, nullptr, n, H, F, Epilogue::kAccumulate,
-                            hidden));
+                        hidden, &accumulate));
+    const GemmFuse gu_f = norm_in(L.post_norm);
+    if (!fused)
+      HIP_TRY(st, launch_rmsnorm(stream, hidden, nullptr, L.post_norm, n, H, d.rms_norm_eps, xn));
+    HIP_TRY(st, gemm_on(m->dev, fused ? hidden : xn, L.w_gu, nullptr, n, 2 * F, H,
+                        Epilogue::kSwiGLU, act, &gu_f));
+    HIP_TRY(st, gemm_on(m->dev, act, L.w_down, nullptr, n, H, F, Epilogue::kAccumulate, hidden,
+                        &accumulate));
   }
   // Final norm on the last row of each sequence only (norm is row-wise, so
   // this equals norming all rows and then gathering), then the LM head.

@@ -167,7 +167,13 @@ def test_argmax_semantics(backend):
     rng = np.random.default_rng(0)
     big = rng.standard_normal((5, 32000)).astype(np.float32)
     big[2, 31999] = big[2, 17] = 100.0  # tie: lowest index wins
-    for arr in (rows, big):
+    big[3, 4 * 4096 + 1] = big[3, 4 * 1024 + 3] = 50.0    # tie across threads / unroll steps
+    big[4, 8] = big[4, 9] = big[4, 10] = 60.0             # tie inside one float4
+    odd = rng.standard_normal((3, 32003)).astype(np.float32)  # unaligned rows: scalar scan
+    odd[1, 32002] = odd[1, 1025] = 9.0
+    odd[2, :] = -np.inf
+    odd[2, 31000] = np.nan
+    for arr in (rows, big, odd):
         dl, do = backend.to_device(arr), backend.alloc(arr.shape[0] * 8)
         oh.argmax(backend, dl.ptr, arr.shape[0], arr.shape[1], do.ptr)
         got = do.download(np.int64, (arr.shape[0],))
