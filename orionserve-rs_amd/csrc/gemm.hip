@@ -358,48 +358,87 @@ __global__ void __launch_bounds__(256)
   const int k0 = blockIdx.y * KSTEPS * 32;
   const int nsteps = min(KSTEPS, (K - k0) >> 5);
 
-  // 1. weight loads (clamped column and k-step: unconditional loads)
-  bf16x8 bw[KSTEPS][NT];
-#pragma unroll
-  for (int nt = 0; nt < NT; ++nt) {
-    const int n = min(n0 + (wave * NT + nt) * 16 + l16, N - 1);
-    const uint16_t* wp = w + (int64_t)n * K + k0 + grp * 8;
-#pragma unroll
-    for (int s2 = 0; s2 < KSTEPS; ++s2)
-      bw[s2][nt] = __builtin_bit_cast(
-          bf16x8, *reinterpret_cast<const uint4*>(wp + min(s2, nsteps - 1) * 32));
-  }
-
-  // 2. activation slice -> LDS hi/lo fragments: fragment f = (mt, step),
-  //    lane l holds row mt*16 + l%16, k = step*32 + (l/16)*8 .. +8.  Every
-  //    fragment load is issued before the norm scales are waited for.
+  // Load order: the activation slice (and norm inputs) first, the weights
+  // last, so staging the activations and the first MFMAs wait only for the
+  // L2-resident inputs while the weight stream is still arriving (a wave's
+  // loads complete in issue order).
+  // 1. activation slice fragments: fragment f = (mt, step), lane l holds row
+  //    mt*16 + l%16, k = step*32 + (l/16)*8 .. +8.
   constexpr int FR = MT * KSTEPS * 64 / 256;  // fragments per thread
   static_assert(MT * KSTEPS * 64 % 256 == 0, "fragments must split evenly over the workgroup");
+  // Every load below is unconditional (clamped address, value selected
+  // afterwards), so the waits can count them in issue order.
   float4 xa[FR][2], wa[FR][2];
+  const float* nwp = nsq ? nw : x;
 #pragma unroll
   for (int j = 0; j < FR; ++j) {
     const int idx = tid + j * 256;
     const int fl = idx & 63, f = idx >> 6;
     const int mt = f / KSTEPS, s2 = f - mt * KSTEPS;
     const int row = mt * 16 + (fl & 15);
-    const float4 z = {0.f, 0.f, 0.f, 0.f};
-    xa[j][0] = xa[j][1] = wa[j][0] = wa[j][1] = z;
-    if (row < M && s2 < nsteps) {
-      const float* xp = x + (int64_t)row * K + k0 + s2 * 32 + (fl >> 4) * 8;
-      xa[j][0] = *reinterpret_cast<const float4*>(xp);
-      xa[j][1] = *reinterpret_cast<const float4*>(xp + 4);
-      if (nsq) {
-        const float* wp = nw + k0 + s2 * 32 + (fl >> 4) * 8;
-        wa[j][0] = *reinterpret_cast<const float4*>(wp);
-        wa[j][1] = *reinterpret_cast<const float4*>(wp + 4);
-      }
+    const int kk = k0 + min(s2, nsteps - 1) * 32 + (fl >> 4) * 8;
+    const float* xp = x + (int64_t)min(row, M - 1) * K + kk;
+    xa[j][0] = *reinterpret_cast<const float4*>(xp);
+    xa[j][1] = *reinterpret_cast<const float4*>(xp + 4);
+    const float* wp = nwp + (nsq ? kk : 0);
+    wa[j][0] = *reinterpret_cast<const float4*>(wp);
+    wa[j][1] = *reinterpret_cast<const float4*>(wp + 4);
+  }
+  // Fused RMSNorm: the row's f64 sum-of-squares slots, TPR threads per row,
+  // each summing up to kSlotsPerThread consecutive slots (larger rows take
+  // the loop below, after the weights).
+  constexpr int TPR = MT == 1 ? 16 : MT == 2 ? 8 : 4, kSlotsPerThread = 8;
+  const bool early_norm = nsq && nslots <= TPR * kSlotsPerThread;
+  const int spt = (nslots + TPR - 1) / TPR;
+  double sq[kSlotsPerThread];
+  {
+    const int row = tid / TPR, j = tid % TPR;
+    // (x stands in as a readable address when there is nothing to load)
+    const double* sp = early_norm ? nsq + (int64_t)min(row, M - 1) * nslots
+                                  : reinterpret_cast<const double*>(x);
+    const int last = early_norm ? nslots - 1 : 0;
+#pragma unroll
+    for (int i = 0; i < kSlotsPerThread; ++i) {
+      const int slot = j * spt + i;
+      const bool use = early_norm && row < M && i < spt && slot < nslots;
+      const double v = sp[min(slot, last)];
+      sq[i] = use ? v : 0.0;
     }
   }
-  // Fused RMSNorm of the input rows: scale = 1 / sqrt(mean(x^2) + eps) from
-  // the f64 sum-of-squares slots (as rmsnorm_kernel computes it), then
-  // x * scale * weight with rmsnorm's order of the two products.
+
+  // 2. weight loads (clamped column and k-step: unconditional loads)
+  //    in k-step order, so the MFMAs of step s wait only for its loads
+  bf16x8 bw[KSTEPS][NT];
+  const uint16_t* wrow[NT];
+#pragma unroll
+  for (int nt = 0; nt < NT; ++nt)
+    wrow[nt] = w + (int64_t)min(n0 + (wave * NT + nt) * 16 + l16, N - 1) * K + k0 + grp * 8;
+#pragma unroll
+  for (int s2 = 0; s2 < KSTEPS; ++s2)
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt)
+      bw[s2][nt] = __builtin_bit_cast(
+          bf16x8, *reinterpret_cast<const uint4*>(wrow[nt] + min(s2, nsteps - 1) * 32));
+  // nothing that waits for a load may be scheduled above this point
+  __builtin_amdgcn_sched_barrier(0);
+
+  // 3. row scales: scale = 1 / sqrt(mean(x^2) + eps), as rmsnorm_kernel
+  //    computes it from the f64 sum; x * scale * weight below keeps rmsnorm's
+  //    order of the two products.
+  {
+    // (computed unconditionally so the slot loads stay ahead of the weights)
+    double t = 0.0;
+#pragma unroll
+    for (int i = 0; i < kSlotsPerThread; ++i) t += sq[i];
+    // TPR consecutive lanes hold one row: fixed-order butterfly
+#pragma unroll
+    for (int o = TPR / 2; o > 0; o >>= 1) t += __shfl_xor(t, o);
+    const int row = tid / TPR;
+    if (early_norm && tid % TPR == 0 && row < MT * 16)
+      nscale[row] = row < M ? (float)(1.0 / sqrt(t / (double)K + (double)neps)) : 0.f;
+  }
   if (nsq) {
-    if (tid < MT * 16) {
+    if (!early_norm && tid < MT * 16) {
       float sc = 0.f;
       if (tid < M) {
         double t = 0.0;
@@ -415,8 +454,11 @@ __global__ void __launch_bounds__(256)
     const int idx = tid + j * 256;
     const int fl = idx & 63, f = idx >> 6;
     const int row = (f / KSTEPS) * 16 + (fl & 15);
+    const bool live = row < M && (f % KSTEPS) < nsteps;
     float a[8] = {xa[j][0].x, xa[j][0].y, xa[j][0].z, xa[j][0].w,
                   xa[j][1].x, xa[j][1].y, xa[j][1].z, xa[j][1].w};
+#pragma unroll
+    for (int e = 0; e < 8; ++e) a[e] = live ? a[e] : 0.f;
     if (nsq) {
       const float sc = row < M ? nscale[row] : 0.f;
       const float wv[8] = {wa[j][0].x, wa[j][0].y, wa[j][0].z, wa[j][0].w,
