@@ -115,6 +115,12 @@ def cpu_baseline(case, seconds_budget=30.0):
         if time.perf_counter() - t0 > min(seconds_budget, 5.0) or reps >= 3:
             break
     dt = (time.perf_counter() - t0) / reps
+    # The reference's own execution model: one thread, one step.
+    orc.set_num_threads(1)
+    t1 = time.perf_counter()
+    case.oracle()
+    dt1 = time.perf_counter() - t1
+    orc.set_num_threads(threads)
     return {
         "value": algorithmic_bytes(case) / dt / 1e9,
         "unit": "GB/s",
@@ -122,6 +128,8 @@ def cpu_baseline(case, seconds_budget=30.0):
         "kind": "port",
         "sample": f"full config-2 step ({case.S} rows, sum ctx {int(case.ctxs.sum())}), "
                   f"{reps} reps, {dt * 1e3:.1f} ms/step, f32 arena holding the same bf16 values",
+        "single_thread": {"value": algorithmic_bytes(case) / dt1 / 1e9, "unit": "GB/s",
+                          "cores": 1, "sample": f"one full step, {dt1:.2f} s"},
     }
 
 
@@ -384,13 +392,23 @@ def cpu_decode_step(cfg, lens, tables, num_blocks, seqs):
                        (orc.W_GATE, F * H), (orc.W_UP, F * H), (orc.W_DOWN, H * F)]:
             m.set_weight(wid, l, c(n))
     pos = [int(n) for n in lens]
+    step = lambda: m.forward([1] * seqs, pos, [1] * seqs, [p + 1 for p in pos], tables)
     t0 = time.perf_counter()
-    m.forward([1] * seqs, pos, [1] * seqs, [p + 1 for p in pos], tables)
+    step()
     dt = time.perf_counter() - t0
+    # The reference's own execution model (single-threaded): a bounded sample,
+    # one decode step at one thread.
+    orc.set_num_threads(1)
+    t1 = time.perf_counter()
+    step()
+    dt1 = time.perf_counter() - t1
+    orc.set_num_threads(threads)
     m.close()
     return {"value": round(seqs / dt, 3), "unit": "tokens/s", "cores": threads, "kind": "port",
             "sample": f"one decode step of the same model shape and batch ({seqs} rows), "
-                      f"{dt:.2f} s/step, constant weights, OpenMP over independent outputs"}
+                      f"{dt:.2f} s/step, constant weights, OpenMP over independent outputs",
+            "single_thread": {"value": round(seqs / dt1, 3), "unit": "tokens/s", "cores": 1,
+                              "sample": f"one decode step, {dt1:.2f} s"}}
 
 
 def main():
