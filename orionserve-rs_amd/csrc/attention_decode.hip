@@ -29,7 +29,6 @@
 #include <algorithm>
 #include <cstdlib>
 #include <functional>
-#include <queue>
 #include <vector>
 
 namespace orion {
@@ -517,7 +516,7 @@ __global__ void __launch_bounds__(256)
                                 int partition, int max_splits, const float* __restrict__ ws_o,
                                 const float* __restrict__ ws_ml, float* __restrict__ out) {
   constexpr int PER = D / 64;
-  constexpr int MAXS = 8;
+  constexpr int MAXS = 16;
   const int lane = threadIdx.x & 63;
   const int64_t slot = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
   if (slot >= (int64_t)num_rows * num_q_heads) return;
@@ -537,25 +536,33 @@ __global__ void __launch_bounds__(256)
   if (nsplit <= 64) {
     const float2 e = lane < nsplit ? *reinterpret_cast<const float2*>(ml + 2 * lane)
                                    : make_float2(-INFINITY, 0.f);
+    // Partial outputs in rounds of MAXS splits, every load of a round issued
+    // before its first use (split indices clamped; the weight of a split past
+    // the end is 0).
     float ov[MAXS][PER];
 #pragma unroll
     for (int j = 0; j < MAXS; ++j)
 #pragma unroll
       for (int i = 0; i < PER; ++i)
-        ov[j][i] = j < nsplit ? ob[(int64_t)j * D + lane + 64 * i] : 0.f;
+        ov[j][i] = ob[(int64_t)min(j, nsplit - 1) * D + lane + 64 * i];
     const float mx = wave_max(e.x);
     const float w = lane < nsplit ? __expf(e.x - mx) : 0.f;
     lsum = wave_sum(w * e.y);
+    for (int base = 0; base < nsplit; base += MAXS) {
+      if (base > 0) {
 #pragma unroll
-    for (int j = 0; j < MAXS; ++j) {
-      const float wj = __shfl(w, j);
+        for (int j = 0; j < MAXS; ++j)
 #pragma unroll
-      for (int i = 0; i < PER; ++i) acc[i] += wj * ov[j][i];
-    }
-    for (int j = MAXS; j < nsplit; ++j) {
-      const float wj = __shfl(w, j);
+          for (int i = 0; i < PER; ++i)
+            ov[j][i] = ob[(int64_t)min(base + j, nsplit - 1) * D + lane + 64 * i];
+      }
 #pragma unroll
-      for (int i = 0; i < PER; ++i) acc[i] += wj * ob[(int64_t)j * D + lane + 64 * i];
+      for (int j = 0; j < MAXS; ++j) {
+        const float wj = __shfl(w, min(base + j, 63));
+        const float wk = base + j < nsplit ? wj : 0.f;
+#pragma unroll
+        for (int i = 0; i < PER; ++i) acc[i] += wk * ov[j][i];
+      }
     }
   } else {
     float mx = -INFINITY;
@@ -581,42 +588,29 @@ __global__ void __launch_bounds__(256)
 
 // Decode work decomposition.  A work item is (row, KV head, chunk of the
 // row's context) and runs on one wave.  All full chunks come first and the
-// partial tail chunks last, longest first (LPT list scheduling), so the final
-// waves to be dispatched are the shortest.  The chunk length is chosen by
-// simulating that schedule on the chip's resident wave slots (greedy: each
-// item goes to the slot that frees up first), with a fixed per-item cost
-// for setup and the split-K merge.
-static int64_t simulate_makespan(const std::vector<int>& lens, int64_t hkv, int C,
-                                 int64_t slots) {
-  std::vector<int> sizes;
+// partial tail chunks last, longest first, so the final waves to be
+// dispatched are the shortest.  The chunk length C is chosen with a fluid
+// model of the split kernel, in token-equivalents of one wave's streaming:
+//   time(C) = max((sum of item sizes + items * kItemOverhead) / wave_slots
+//                 + C / 2,                       (bandwidth-bound, mean tail)
+//                 largest item + kItemOverhead)  (latency-bound: one wave)
+// The per-item overhead (setup, split-K partial write and merge read) and the
+// half-item tail were fitted to the measured config-2 times at C = 128 ...
+// 1024 (best: 256).
+static int64_t estimate_split_time(const std::vector<int>& lens, int64_t hkv, int C,
+                                   int64_t slots) {
+  constexpr int64_t kItemOverhead = 96;
+  int64_t total = 0, items = 0, largest = 0;
   for (int L : lens) {
-    const int full = L / C;
-    for (int64_t h = 0; h < hkv; ++h)
-      for (int s = 0; s < full; ++s) sizes.push_back(C);
+    const int64_t full = L / C, tail = L % C;
+    items += hkv * (full + (tail ? 1 : 0));
+    total += (int64_t)hkv * L;
+    largest = std::max<int64_t>(largest, full ? C : tail);
   }
-  std::vector<int> tails;
-  for (int L : lens)
-    if (L % C)
-      for (int64_t h = 0; h < hkv; ++h) tails.push_back(L % C);
-  std::sort(tails.begin(), tails.end(), std::greater<int>());
-  sizes.insert(sizes.end(), tails.begin(), tails.end());
-  constexpr int kItemOverhead = 48;  // tokens-equivalent per item
-  if ((int64_t)sizes.size() <= slots) {
-    int64_t mx = 0;
-    for (int v : sizes) mx = std::max<int64_t>(mx, v + kItemOverhead);
-    return mx;
-  }
-  std::priority_queue<int64_t, std::vector<int64_t>, std::greater<int64_t>> pq;
-  for (int64_t i = 0; i < slots; ++i) pq.push(0);
-  int64_t mx = 0;
-  for (int v : sizes) {
-    int64_t t = pq.top();
-    pq.pop();
-    t += v + kItemOverhead;
-    mx = std::max(mx, t);
-    pq.push(t);
-  }
-  return mx;
+  if (items == 0) return 0;
+  const int64_t fluid = (total + items * kItemOverhead) / std::max<int64_t>(slots, 1) +
+                        std::min<int64_t>(C, largest) / 2;
+  return std::max(fluid, largest + kItemOverhead);
 }
 
 void build_decode_plan(const uint32_t* positions, const int32_t* row_seq,
@@ -640,7 +634,7 @@ void build_decode_plan(const uint32_t* positions, const int32_t* row_seq,
   int64_t best_t = 0;
   for (int C = 64; C <= 2048; C <<= 1) {
     if (C < block_size || C / block_size > 64) continue;
-    const int64_t t = simulate_makespan(lens, hkv, C, wave_slots);
+    const int64_t t = estimate_split_time(lens, hkv, C, wave_slots);
     if (best_c == 0 || t < best_t) {
       best_c = C;
       best_t = t;
