@@ -262,7 +262,7 @@ __device__ __forceinline__ void decode_wave_mfma2(
     uint32_t slot_stride, uint32_t head_stride, int bs_log2, int num_q_heads, const float* __restrict__ q,
     const uint32_t* __restrict__ tbl, int blk0, int max_splits, float scale,
     float* __restrict__ out, float* __restrict__ ws_o, float* __restrict__ ws_ml, uint16_t* VL,
-    uint16_t* QL, int row, int kvh,
+    uint16_t* QL, uint16_t* KL, int row, int kvh,
     int start, int end, int split, int nsplit) {
   constexpr int KCH = D / 32;     // K . Q^T MFMA k-steps
   constexpr int DT = D / 16;      // output dim tiles of the P.V MFMA
@@ -302,41 +302,34 @@ __device__ __forceinline__ void decode_wave_mfma2(
 
   // blk_hint >= 0 supplies the step's block id directly (the first step uses
   // the plan's copy, so its loads need not wait for the table slice).
-  auto issue = [&](uint4 (&ks)[KCH], uint4 (&vs)[RV], int b, int blk_hint) {
-    const int jk = min(b + l16, end - 1);
+  auto issue = [&](uint4 (&ks)[RV], uint4 (&vs)[RV], int b, int blk_hint) {
     if constexpr (BIG_BLOCKS) {
       const int blk = blk_hint >= 0
                           ? blk_hint
                           : __builtin_amdgcn_readlane(my_blk, (b >> bs_log2) - first_blk);
       const uint16_t* bb = base_k + (uint32_t)blk * blk_stride;
-      const uint16_t* kp = bb + (uint32_t)(jk & bs_mask) * slot_stride + kd;
-#pragma unroll
-      for (int c = 0; c < KCH; ++c) ks[c] = *reinterpret_cast<const uint4*>(kp + 32 * c);
 #pragma unroll
       for (int r = 0; r < RV; ++r) {
         const int jv = min(b + r * TPW + vt, end - 1);
-        vs[r] = *reinterpret_cast<const uint4*>(bb + (uint32_t)(jv & bs_mask) * slot_stride +
-                                                v_off + vc * 8);
+        const uint16_t* rp = bb + (uint32_t)(jv & bs_mask) * slot_stride + vc * 8;
+        ks[r] = *reinterpret_cast<const uint4*>(rp);
+        vs[r] = *reinterpret_cast<const uint4*>(rp + v_off);
       }
     } else {
-      const int bk = __shfl(my_blk, (jk >> bs_log2) - first_blk);
-      const uint16_t* kp =
-          base_k + (uint32_t)bk * blk_stride + (uint32_t)(jk & bs_mask) * slot_stride + kd;
-#pragma unroll
-      for (int c = 0; c < KCH; ++c) ks[c] = *reinterpret_cast<const uint4*>(kp + 32 * c);
 #pragma unroll
       for (int r = 0; r < RV; ++r) {
         const int jv = min(b + r * TPW + vt, end - 1);
         const int bv = __shfl(my_blk, (jv >> bs_log2) - first_blk);
-        vs[r] = *reinterpret_cast<const uint4*>(base_k + (uint32_t)bv * blk_stride +
-                                                (uint32_t)(jv & bs_mask) * slot_stride + v_off +
-                                                vc * 8);
+        const uint16_t* rp = base_k + (uint32_t)bv * blk_stride +
+                             (uint32_t)(jv & bs_mask) * slot_stride + vc * 8;
+        ks[r] = *reinterpret_cast<const uint4*>(rp);
+        vs[r] = *reinterpret_cast<const uint4*>(rp + v_off);
       }
     }
   };
 
   // Register sets of the K/V pipeline; the first step is issued now.
-  uint4 ka[KCH], va_[RV], kb[KCH], vb[RV];
+  uint4 ka[RV], va_[RV], kb[RV], vb[RV];
   const int nsteps = (end - start + 15) >> 4;
   auto step_base = [&](int i) { return min(start + 16 * i, end - 1) & ~15; };
   issue(ka, va_, step_base(0), BIG_BLOCKS ? blk0 : -1);
@@ -377,6 +370,12 @@ __device__ __forceinline__ void decode_wave_mfma2(
   // transposed read (lane 4r + q of a group addresses row 4*grp + r, dims
   // 4q .. 4q+3 of the tile).
   const uint32_t vl_base = (uint32_t)(uintptr_t)VL;
+  // K tile [16 tokens][CH units of 16 bytes]; unit u of token t sits at
+  // t*CH + (u ^ kswz(t)), which keeps both the row writes (a wave writes TPW
+  // whole rows) and the fragment reads (16 tokens x one unit per group) free
+  // of LDS bank conflicts.
+  const uint32_t kl_base = (uint32_t)(uintptr_t)KL;
+  auto kswz = [](int t) { return D == 128 ? (t & 15) : ((t >> 1) & (CH - 1)); };
   const uint32_t w_off = (uint32_t)(vt * VROW + vc * 8) * 2;
   const uint32_t r_off = (uint32_t)((4 * grp + (l16 >> 2)) * VROW + 4 * (l16 & 3)) * 2;
   typedef short v4s __attribute__((ext_vector_type(4)));
@@ -389,20 +388,29 @@ __device__ __forceinline__ void decode_wave_mfma2(
   constexpr float kLazy = 8.0f;
   typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
   typedef __attribute__((address_space(3))) u32x4 lds_u4;
-  auto compute = [&](const uint4 (&ks)[KCH], const uint4 (&vs)[RV], int b, int buf) {
-    // Stage V into LDS (row-major, padded rows).  One buffer per wave: its
-    // LDS operations execute in order, and the fence at the end of the step
-    // keeps the compiler from moving this write above the previous reads.
+  auto compute = [&](const uint4 (&ks)[RV], const uint4 (&vs)[RV], int b, int buf) {
+    // Stage V (row-major, padded rows) and K (swizzled 16-byte units) into
+    // LDS.  One buffer per wave: its LDS operations execute in order, and the
+    // fence at the end of the step keeps the compiler from moving these
+    // writes above the previous reads.
     (void)buf;
     const uint32_t wb = vl_base + w_off;
 #pragma unroll
-    for (int r = 0; r < RV; ++r)
+    for (int r = 0; r < RV; ++r) {
       *(lds_u4*)(uintptr_t)(wb + r * TPW * VROW * 2) = __builtin_bit_cast(u32x4, vs[r]);
-    // S = K . Q^T
+      const int tt = r * TPW + vt;
+      *(lds_u4*)(uintptr_t)(kl_base + (uint32_t)(tt * CH + (vc ^ kswz(tt))) * 16) =
+          __builtin_bit_cast(u32x4, ks[r]);
+    }
+    wave_lds_sync();
+    // S = K . Q^T, the A fragments (token l16, dims 32c + 8grp .. +8) read
+    // back from the K tile
     f32x4 sh = {0.f, 0.f, 0.f, 0.f}, sl = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int c = 0; c < KCH; ++c) {
-      const bf16x8 ka = __builtin_bit_cast(bf16x8, ks[c]);
+      const bf16x8 ka = __builtin_bit_cast(
+          bf16x8, *(const lds_u4*)(uintptr_t)(kl_base +
+                                              (uint32_t)(l16 * CH + ((4 * c + grp) ^ kswz(l16))) * 16));
       sh = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ka, qb(c, 0), sh, 0, 0, 0);
       sl = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ka, qb(c, 1), sl, 0, 0, 0);
     }
@@ -432,7 +440,6 @@ __device__ __forceinline__ void decode_wave_mfma2(
     split2_trunc(pv[2], pv[3], hi2.y, lo2.y);
     const v4s pb_hi = __builtin_bit_cast(v4s, hi2);
     const v4s pb_lo = __builtin_bit_cast(v4s, lo2);
-    wave_lds_sync();
     // O^T += V^T . P^T
     const uint32_t rb = vl_base + r_off;
 #pragma unroll
@@ -480,7 +487,7 @@ __device__ __forceinline__ void decode_wave_mfma2(
 }
 
 template <int D, int G, int NS, bool BIG_BLOCKS>
-__global__ void __launch_bounds__(256)
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3)))
     paged_decode_mfma2_kernel(const uint16_t* __restrict__ kv_layer, uint32_t blk_stride,
                               uint32_t v_off, uint32_t slot_stride,
                               uint32_t head_stride, int bs_log2, int num_kv_heads,
@@ -493,6 +500,7 @@ __global__ void __launch_bounds__(256)
                               float* __restrict__ ws_ml) {
   __shared__ __attribute__((aligned(16))) uint16_t lds_v[4][16 * (D + 8)];
   __shared__ __attribute__((aligned(16))) uint16_t lds_q[4][2 * G * (D + 8)];
+  __shared__ __attribute__((aligned(16))) uint16_t lds_k[4][16 * D];
   const int wv = threadIdx.x >> 6;
   const int w = blockIdx.x * 4 + wv;
   if (w >= num_work) return;
@@ -501,7 +509,7 @@ __global__ void __launch_bounds__(256)
   decode_wave_mfma2<D, G, NS, BIG_BLOCKS>(kv_layer, blk_stride, v_off, slot_stride, head_stride,
                                           bs_log2,
                                           num_q_heads, q, bt_ids + wk.tbl_off, wk.blk0, max_splits,
-                                          scale, out, ws_o, ws_ml, lds_v[wv], lds_q[wv], row, kvh,
+                                          scale, out, ws_o, ws_ml, lds_v[wv], lds_q[wv], lds_k[wv], row, kvh,
                                           wk.start, wk.end, wk.start / chunk, wk.nsplit);
 }
 
