@@ -55,6 +55,9 @@ struct DecodePlanHost {
   int max_splits = 0;  // chunks of the longest row
   std::vector<DecodeWork> work;
   std::vector<int32_t> rows;  // rows covered when a skip mask was given (else all)
+  // No block is attended by two planned rows: K/V are then read once and
+  // streamed past the caches; shared (prefix) blocks keep cached loads.
+  bool stream_kv = true;
 };
 struct DecodePlanDev {
   const DecodeWork* work = nullptr;
@@ -65,6 +68,7 @@ struct DecodePlanDev {
   size_t ws_bytes = 0;
   const int32_t* rows = nullptr;  // rows to merge (nullptr: every row)
   int num_rows = 0;
+  bool stream_kv = true;  // DecodePlanHost::stream_kv
 };
 void build_decode_plan(const uint32_t* positions, const int32_t* row_seq,
                        const int64_t* bt_offsets, const uint32_t* bt_ids, int64_t rows,

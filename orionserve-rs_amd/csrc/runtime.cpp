@@ -187,6 +187,7 @@ struct orion_hip_decode_plan {
     d.max_splits = host.max_splits;
     d.ws = ws.as<float>();
     d.ws_bytes = ws.bytes;
+    d.stream_kv = host.stream_kv;
     return d;
   }
 };
@@ -1046,6 +1047,7 @@ ORION_EXPORT int orion_hip_model_forward(orion_hip_model* m, const orion_hip_bat
   dplan.max_splits = plan.max_splits;
   dplan.ws = m->ws.as<float>();
   dplan.ws_bytes = m->ws.bytes;
+  dplan.stream_kv = plan.stream_kv;
   if (npf) {
     dplan.rows = reinterpret_cast<const int32_t*>(dp + o_drows);
     dplan.num_rows = (int)plan.rows.size();
