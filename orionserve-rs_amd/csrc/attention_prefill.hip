@@ -46,10 +46,12 @@ typedef __attribute__((address_space(3))) v4s lds_v4s;
 typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 typedef float f32x2 __attribute__((ext_vector_type(2)));
 
-constexpr int kWaves = 4;
+constexpr int kWaves = 8;
+constexpr int kThreads = kWaves * 64;
 constexpr int kNR = 2;                      // 16-row MFMA tiles per wave
 constexpr int kBM = kWaves * 16 * kNR;      // packed rows per workgroup
 constexpr int kBN = 64;                     // keys per tile
+constexpr int kStages = 3;                  // K/V tiles resident in LDS (2 in flight)
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kLazy = 8.0f;               // log2 units: weights stay <= 2^8
 
@@ -60,6 +62,14 @@ __device__ inline uint32_t pack_bf16_rne(float a, float b) {
 }
 
 __device__ inline bf16x8 u4_bf16x8(uint4 v) { return __builtin_bit_cast(bf16x8, v); }
+
+// s_waitcnt vmcnt(N) with the other counters untouched (gfx9 encoding:
+// vmcnt bits [3:0] and [15:14]).
+template <int N>
+__device__ inline void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | 0x0F70);
+}
 
 
 }  // namespace
@@ -82,7 +92,7 @@ __device__ inline int swz_v(int r) {
 }
 
 template <int D, bool HILO, bool BIG>
-__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2)))
+__global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2)))
     paged_prefill_kernel(const uint16_t* __restrict__ kv_layer, uint32_t blk_stride,
                          uint32_t v_off, uint32_t slot_stride, uint32_t head_stride,
                          int bs_log2, int num_kv_heads,
@@ -101,7 +111,7 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2)))
   constexpr int TILE = kBN * D;         // one K or V tile, elements
   static_assert(LPW >= 1 && RPI * LPW * kWaves == kBN, "tile shape");
 
-  __shared__ __attribute__((aligned(1024))) uint16_t lds[2][2][TILE];  // [buf][k|v]
+  __shared__ __attribute__((aligned(1024))) uint16_t lds[kStages][2][TILE];  // [buf][k|v]
 
   const int seq = blockIdx.x / num_kv_heads;
   const int kvh = blockIdx.x - seq * num_kv_heads;
@@ -177,7 +187,9 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2)))
   auto load_ids = [&](int t, uint32_t (&ids)[NID]) {
     const int tt = min(t, ntiles - 1);
     if constexpr (BIG) {
-      ids[0] = tbl[min(tt * kBN + wave_u * RPI * LPW, kv_len - 1) >> bs_log2];
+      // uniform index: a scalar load, counted apart from the tile loads
+      ids[0] = tbl[__builtin_amdgcn_readfirstlane(
+          min(tt * kBN + wave_u * RPI * LPW, kv_len - 1) >> bs_log2)];
     } else {
 #pragma unroll
       for (int j = 0; j < LPW; ++j) ids[j] = tbl[key_of(tt, j) >> bs_log2];
@@ -196,14 +208,27 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2)))
     }
   };
 
-  // ---- prologue: tile 0 into LDS buffer 0, ids of tile 1 ready ----
+  // Tile-load accounting: a wave's tile loads are 2*LPW global_load_lds
+  // (counted by vmcnt, completing in issue order); with small blocks the
+  // per-row block ids are LPW vector loads issued after them.
+  constexpr int kTileOps = 2 * LPW;
+  constexpr int kIdOps = BIG ? 0 : LPW;
+
+  // ---- prologue: tiles 0 and 1 into LDS buffers 0 and 1, ids of tile 2 ----
   {
     uint32_t ids0[NID];
     load_ids(0, ids0);
     load_tile(0, 0, ids0);
-    load_ids(1, ids_next);
+    if (ntiles > 1) {
+      load_ids(1, ids0);
+      load_tile(1, 1, ids0);
+    }
+    load_ids(2, ids_next);
   }
-  __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): this wave's LDS loads have landed
+  if (ntiles > 1)
+    wait_vmcnt<kTileOps + kIdOps>();  // tile 0 has landed (tile 1 and the ids may not)
+  else
+    wait_vmcnt<0>();
   __syncthreads();
 
   float m[kNR];                 // running max of raw scores (q.k), per query
@@ -240,11 +265,12 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2)))
   auto step = [&](int t, auto buf_tag) {
     constexpr int BUF = decltype(buf_tag)::value;
     constexpr uint32_t kBufOff = BUF * 2 * TILE * 2;
-    const bool more = t + 1 < ntiles;
+    // Tile t + 2 goes into the buffer tile t - 1 used (every wave passed the
+    // barrier that ended step t - 1, so its reads are done).
+    const bool more = t + 2 < ntiles;
     if (more) {
-      __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): the block ids are in
-      load_tile(t + 1, BUF ^ 1, ids_next);
-      load_ids(t + 2, ids_next);
+      load_tile(t + 2, (BUF + 2) % kStages, ids_next);
+      load_ids(t + 3, ids_next);
     }
 
     // S^T[rt][kt]: raw scores of keys t*64 + kt*16 + 4*grp + i, query l16.
@@ -378,13 +404,19 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2)))
       }
     }
 
-    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): next tile's LDS loads have landed
+    // Tile t + 1 must have landed; tile t + 2 (and its successor's ids) may
+    // still be in flight.
+    if (more)
+      wait_vmcnt<kTileOps + kIdOps>();
+    else
+      wait_vmcnt<0>();
     __syncthreads();
   };
 
-  for (int t = 0; t < ntiles; t += 2) {
+  for (int t = 0; t < ntiles; t += kStages) {
     step(t, std::integral_constant<int, 0>{});
     if (t + 1 < ntiles) step(t + 1, std::integral_constant<int, 1>{});
+    if (t + 2 < ntiles) step(t + 2, std::integral_constant<int, 2>{});
   }
 
   // ---- normalise and store: lane holds dims 16d + 4*grp .. +3 of query l16 ----
@@ -429,7 +461,7 @@ hipError_t launch_paged_prefill(hipStream_t st, const KvGeom& kv, const void* ar
   const float scale_log2 = kLog2e / sqrtf((float)D);
   const dim3 grid((unsigned)(num_seqs * hkv), (unsigned)tiles);
 #define ORION_PREFILL_B(DD, HH, BB)                                                             \
-  hipLaunchKernelGGL((paged_prefill_kernel<DD, HH, BB>), grid, dim3(256), 0, st, base,              \
+  hipLaunchKernelGGL((paged_prefill_kernel<DD, HH, BB>), grid, dim3(kThreads), 0, st, base,         \
                      (uint32_t)a.blk, (uint32_t)a.v_off, (uint32_t)a.slot, (uint32_t)a.head,   \
                      bs_log2,                                                                  \
                      (int)hkv, (int)hq, q, row_start, row_count, first_pos, bt_offsets, bt_ids, \

@@ -971,7 +971,7 @@ ORION_EXPORT int orion_hip_model_forward(orion_hip_model* m, const orion_hip_bat
     int64_t r0 = 0;
     for (int64_t s = 0; s < S; ++s) {
       const int64_t c = b->slot_token_counts[s];
-      bool chunk = c * G >= prefill_tile_rows() / 2;
+      bool chunk = c * G >= 64;  // enough (row, head) pairs to fill MFMA row tiles
       for (int64_t i = 1; chunk && i < c; ++i)
         chunk = b->positions[r0 + i] == b->positions[r0] + (uint32_t)i;
       if (chunk) {
