@@ -111,7 +111,9 @@ __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2
   constexpr int TILE = kBN * D;         // one K or V tile, elements
   static_assert(LPW >= 1 && RPI * LPW * kWaves == kBN, "tile shape");
 
-  __shared__ __attribute__((aligned(1024))) uint16_t lds[kStages][2][TILE];  // [buf][k|v]
+  // [k|v][buf]: every K or V read is a per-lane base (K or V region) plus an
+  // immediate offset below 64 KiB.
+  __shared__ __attribute__((aligned(1024))) uint16_t lds[2][kStages][TILE];
 
   const int seq = blockIdx.x / num_kv_heads;
   const int kvh = blockIdx.x - seq * num_kv_heads;
@@ -202,9 +204,10 @@ __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2
       const uint32_t off = __umul24(ids[BIG ? 0 : j], blk_stride) +
                            __umul24((uint32_t)(key_of(t, j) & bs_mask), slot_stride);
       const uint32_t dk =
-          lds_base + (uint32_t)((buf * 2 * TILE + (wave_u * LPW + j) * RPI * D) * 2);
+          lds_base + (uint32_t)((buf * TILE + (wave_u * LPW + j) * RPI * D) * 2);
       lds_load16(head_base + off + ld_off_k[j], __builtin_amdgcn_readfirstlane(dk));
-      lds_load16(head_base + off + ld_off_v[j], __builtin_amdgcn_readfirstlane(dk + TILE * 2));
+      lds_load16(head_base + off + ld_off_v[j],
+                 __builtin_amdgcn_readfirstlane(dk + kStages * TILE * 2));
     }
   };
 
@@ -256,7 +259,7 @@ __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2
     k_addr[c] = lds_base + (uint32_t)(l16 * D + (((4 * c + grp) ^ swz_k<D>(l16)) * 8)) * 2;
 #pragma unroll
   for (int d = 0; d < DT; ++d)
-    v_addr[d] = lds_base + (uint32_t)(TILE + vr * D +
+    v_addr[d] = lds_base + (uint32_t)(kStages * TILE + vr * D +
                                       ((2 * d + (vcc >> 1)) ^ swz_v<D>(vr)) * 8 + (vcc & 1) * 4) * 2;
   const float lazy_raw = kLazy / scale_log2;
 
@@ -264,7 +267,7 @@ __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2
   // so every LDS read is a loop-invariant address plus an immediate offset.
   auto step = [&](int t, auto buf_tag) {
     constexpr int BUF = decltype(buf_tag)::value;
-    constexpr uint32_t kBufOff = BUF * 2 * TILE * 2;
+    constexpr uint32_t kBufOff = BUF * TILE * 2;
     // Tile t + 2 goes into the buffer tile t - 1 used (every wave passed the
     // barrier that ended step t - 1, so its reads are done).
     const bool more = t + 2 < ntiles;
