@@ -33,7 +33,10 @@
 #include "common.hpp"
 #include "kernels.hpp"
 
+#include <algorithm>
 #include <type_traits>
+#include <utility>
+#include <vector>
 
 namespace orion {
 
@@ -97,11 +100,12 @@ __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2
                          uint32_t v_off, uint32_t slot_stride, uint32_t head_stride,
                          int bs_log2, int num_kv_heads,
                          int num_q_heads, const float* __restrict__ q,
+                         const PrefillTile* __restrict__ order,
                          const int32_t* __restrict__ row_start,
                          const int32_t* __restrict__ row_count,
                          const uint32_t* __restrict__ first_pos,
                          const int64_t* __restrict__ bt_offsets,
-                         const uint32_t* __restrict__ bt_ids, int max_tiles, float scale_log2,
+                         const uint32_t* __restrict__ bt_ids, float scale_log2,
                          float* __restrict__ out) {
   constexpr int KCH = D / 32;           // S^T k-steps
   constexpr int DT = D / 16;            // O^T dim tiles
@@ -115,9 +119,10 @@ __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2
   // immediate offset below 64 KiB.
   __shared__ __attribute__((aligned(1024))) uint16_t lds[2][kStages][TILE];
 
-  const int seq = blockIdx.x / num_kv_heads;
-  const int kvh = blockIdx.x - seq * num_kv_heads;
-  const int tile = max_tiles - 1 - (int)blockIdx.y;  // longest tiles first
+  const int item = blockIdx.x / num_kv_heads;  // the kv heads of one tile are adjacent
+  const int kvh = blockIdx.x - item * num_kv_heads;
+  const PrefillTile pt = order[item];
+  const int seq = pt.seq, tile = pt.tile;
   const int G = num_q_heads / num_kv_heads;
   const int cnt = row_count[seq];
   const int P = cnt * G;
@@ -439,36 +444,47 @@ __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2
   }
 }
 
-int prefill_tile_rows() { return kBM; }
+void build_prefill_order(const int32_t* row_count, const uint32_t* first_pos, int64_t num_seqs,
+                         int64_t group, std::vector<PrefillTile>* order) {
+  std::vector<std::pair<int64_t, PrefillTile>> items;
+  for (int64_t s = 0; s < num_seqs; ++s) {
+    const int64_t packed = (int64_t)row_count[s] * group;
+    for (int64_t t = 0; t * kBM < packed; ++t) {
+      const int64_t last_row = std::min(packed, (t + 1) * kBM) / group;  // rows, exclusive
+      items.push_back({(int64_t)first_pos[s] + last_row, PrefillTile{(int32_t)s, (int32_t)t}});
+    }
+  }
+  std::stable_sort(items.begin(), items.end(),
+                   [](const auto& a, const auto& b) { return a.first > b.first; });
+  order->clear();
+  for (const auto& it : items) order->push_back(it.second);
+}
 
 hipError_t launch_paged_prefill(hipStream_t st, const KvGeom& kv, const void* arena,
-                                int64_t layer, const float* q, int64_t hq, int64_t num_seqs,
+                                int64_t layer, const float* q, int64_t hq,
+                                const PrefillTile* order, int64_t num_tiles,
                                 const int32_t* row_start, const int32_t* row_count,
                                 const uint32_t* first_pos, const int64_t* bt_offsets,
-                                const uint32_t* bt_ids, int64_t max_rows, int64_t max_position,
-                                bool hilo, float* out) {
-  (void)max_position;
-  if (num_seqs == 0 || max_rows == 0) return hipSuccess;
+                                const uint32_t* bt_ids, bool hilo, float* out) {
+  if (num_tiles == 0) return hipSuccess;
   if (!kv.dtype_bf16) return hipErrorNotSupported;
   const int64_t hkv = kv.num_kv_heads, D = kv.head_dim;
   if (hkv <= 0 || hq % hkv != 0 || (D != 64 && D != 128)) return hipErrorInvalidValue;
-  const int64_t G = hq / hkv;
   int bs_log2 = 0;
   while ((1 << bs_log2) < kv.block_size) ++bs_log2;
   const ArenaStrides a = arena_strides(kv);
   const int64_t layer_elems = a.layer;
   if (layer_elems > (int64_t)UINT32_MAX) return hipErrorInvalidValue;
   const uint16_t* base = static_cast<const uint16_t*>(arena) + layer * layer_elems;
-  const int64_t tiles = (max_rows * G + kBM - 1) / kBM;
-  if (tiles > 65535 || num_seqs * hkv > INT32_MAX) return hipErrorInvalidValue;
+  if (num_tiles * hkv > INT32_MAX) return hipErrorInvalidValue;
   const float scale_log2 = kLog2e / sqrtf((float)D);
-  const dim3 grid((unsigned)(num_seqs * hkv), (unsigned)tiles);
+  const dim3 grid((unsigned)(num_tiles * hkv));
 #define ORION_PREFILL_B(DD, HH, BB)                                                             \
   hipLaunchKernelGGL((paged_prefill_kernel<DD, HH, BB>), grid, dim3(kThreads), 0, st, base,         \
                      (uint32_t)a.blk, (uint32_t)a.v_off, (uint32_t)a.slot, (uint32_t)a.head,   \
                      bs_log2,                                                                  \
-                     (int)hkv, (int)hq, q, row_start, row_count, first_pos, bt_offsets, bt_ids, \
-                     (int)tiles, scale_log2, out)
+                     (int)hkv, (int)hq, q, order, row_start, row_count, first_pos, bt_offsets, \
+                     bt_ids, scale_log2, out)
 #define ORION_PREFILL(DD, HH)        \
   do {                               \
     if (big)                         \

@@ -85,14 +85,22 @@ hipError_t launch_paged_decode(hipStream_t st, const KvGeom& kv, const void* are
                                const DecodePlanDev& plan, float* out,
                                DecodePhase phase = DecodePhase::kBoth);
 
+// Prefill work list: one entry per (sequence, tile of packed rows), longest
+// first (by the keys its last row attends), so the longest workgroups are
+// dispatched first.  Built on the host from the chunk lengths and first
+// positions; the device copy is what launch_paged_prefill takes.
+struct PrefillTile {
+  int32_t seq, tile;
+};
+void build_prefill_order(const int32_t* row_count, const uint32_t* first_pos, int64_t num_seqs,
+                         int64_t group, std::vector<PrefillTile>* order);
 hipError_t launch_paged_prefill(hipStream_t st, const KvGeom& kv, const void* arena,
-                                int64_t layer, const float* q, int64_t hq, int64_t num_seqs,
+                                int64_t layer, const float* q, int64_t hq,
+                                const PrefillTile* order, int64_t num_tiles,
                                 const int32_t* row_start, const int32_t* row_count,
                                 const uint32_t* first_pos, const int64_t* bt_off,
-                                const uint32_t* bt_ids, int64_t max_rows, int64_t max_position,
-                                bool hilo, float* out);
+                                const uint32_t* bt_ids, bool hilo, float* out);
 // Packed (row, query head) rows per prefill workgroup tile.
-int prefill_tile_rows();
 
 // ---- GEMM -------------------------------------------------------------------
 enum class Epilogue : int {

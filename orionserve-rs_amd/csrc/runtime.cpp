@@ -144,6 +144,7 @@ struct orion_hip_device {
   // Split-K GEMM scratch (partials + zeroed arrival counters), shared by
   // every call on this device's stream.
   DevBuf gemm_ws, gemm_cnt;
+  DevBuf prefill_order;  // op-level prefill work list
   // Per-kernel timing (orion_hip_kernel_timing): event pairs per kernel
   // index, resolved when read.
   bool ktiming = false;
@@ -301,6 +302,7 @@ ORION_EXPORT void orion_hip_device_close(orion_hip_device* dev) {
   for (hipEvent_t e : dev->event_pool) (void)hipEventDestroy(e);
   dev->gemm_ws.release();
   dev->gemm_cnt.release();
+  dev->prefill_order.release();
   (void)hipStreamDestroy(dev->stream);
   delete dev;
 }
@@ -962,7 +964,6 @@ ORION_EXPORT int orion_hip_model_forward(orion_hip_model* m, const orion_hip_bat
   std::vector<int32_t> pf_start, pf_count;
   std::vector<uint32_t> pf_pos;
   std::vector<int64_t> pf_btoff;
-  int64_t pf_max_rows = 0;
   // ORION_PREFILL_ROUTE=0 sends every row to the decode kernel (read per
   // call; lets tests compare the two routes on one batch).
   const char* route = getenv("ORION_PREFILL_ROUTE");
@@ -979,13 +980,14 @@ ORION_EXPORT int orion_hip_model_forward(orion_hip_model* m, const orion_hip_bat
         pf_count.push_back((int32_t)c);
         pf_pos.push_back(b->positions[r0]);
         pf_btoff.push_back(b->block_table_offsets[s]);
-        pf_max_rows = std::max(pf_max_rows, c);
         std::fill(skip.begin() + r0, skip.begin() + r0 + c, (uint8_t)1);
       }
       r0 += c;
     }
   }
   const int64_t npf = (int64_t)pf_start.size();
+  std::vector<PrefillTile> pf_order;
+  if (npf) build_prefill_order(pf_count.data(), pf_pos.data(), npf, G, &pf_order);
   // Decode plan (longest-first chunk list) over the remaining rows.
   DecodePlanHost plan;
   build_decode_plan(b->positions, hb.row_seq.data(), b->block_table_offsets, b->block_table_ids, n,
@@ -1006,7 +1008,8 @@ ORION_EXPORT int orion_hip_model_forward(orion_hip_model* m, const orion_hip_bat
   const size_t o_pfcount = o_pfstart + npf * 4;
   const size_t o_pfpos = o_pfcount + npf * 4;
   const size_t o_drows = o_pfpos + npf * 4;
-  const size_t total = o_drows + plan.rows.size() * 4;
+  const size_t o_pforder = (o_drows + plan.rows.size() * 4 + 7) & ~(size_t)7;
+  const size_t total = o_pforder + pf_order.size() * sizeof(PrefillTile);
   if (total > m->pinned_bytes) {
     if (m->pinned) {
       HIP_TRY(st, hipStreamSynchronize(stream));
@@ -1032,6 +1035,7 @@ ORION_EXPORT int orion_hip_model_forward(orion_hip_model* m, const orion_hip_bat
   std::memcpy(hp + o_pfcount, pf_count.data(), npf * 4);
   std::memcpy(hp + o_pfpos, pf_pos.data(), npf * 4);
   std::memcpy(hp + o_drows, plan.rows.data(), plan.rows.size() * 4);
+  std::memcpy(hp + o_pforder, pf_order.data(), pf_order.size() * sizeof(PrefillTile));
   char* dp = m->b_tokens.as<char>();
   HIP_TRY(st, hipMemcpyAsync(dp, hp, total, hipMemcpyHostToDevice, stream));
   const uint32_t* d_tok = reinterpret_cast<const uint32_t*>(dp + o_tok);
@@ -1056,6 +1060,7 @@ ORION_EXPORT int orion_hip_model_forward(orion_hip_model* m, const orion_hip_bat
   const int32_t* d_pfstart = reinterpret_cast<const int32_t*>(dp + o_pfstart);
   const int32_t* d_pfcount = reinterpret_cast<const int32_t*>(dp + o_pfcount);
   const uint32_t* d_pfpos = reinterpret_cast<const uint32_t*>(dp + o_pfpos);
+  const PrefillTile* d_pforder = reinterpret_cast<const PrefillTile*>(dp + o_pforder);
 
   float* hidden = m->hidden.as<float>();
   float* xn = m->xn.as<float>();
@@ -1099,9 +1104,9 @@ ORION_EXPORT int orion_hip_model_forward(orion_hip_model* m, const orion_hip_bat
     HIP_TRY(st, launch_paged_decode(stream, m->kv, m->arena, l, qrot, n, Hq, d_pos, d_rs, d_btoff,
                                     d_btids, dplan, attn));
     if (npf)
-      HIP_TRY(st, launch_paged_prefill(stream, m->kv, m->arena, l, qrot, Hq, npf, d_pfstart,
-                                       d_pfcount, d_pfpos, d_pfoff, d_btids, pf_max_rows,
-                                       hb.max_position, /*hilo=*/true, attn));
+      HIP_TRY(st, launch_paged_prefill(stream, m->kv, m->arena, l, qrot, Hq, d_pforder,
+                                       (int64_t)pf_order.size(), d_pfstart, d_pfcount, d_pfpos,
+                                       d_pfoff, d_btids, /*hilo=*/true, attn));
     HIP_TRY(st, gemm_on(m->dev, attn, L.w_o, nullptr, n, H, m->qd, Epilogue::kAccumulate,
                         hidden, &accumulate));
     const GemmFuse gu_f = norm_in(L.post_norm);
@@ -1255,11 +1260,33 @@ ORION_EXPORT int orion_hip_paged_attention_prefill(
   if (g.num_kv_heads <= 0 || num_q_heads % g.num_kv_heads)
     return internal(st, "query heads cannot be grouped over kv heads");
   HIP_TRY(st, hipSetDevice(dev->ordinal));
+  (void)max_rows;
+  (void)max_position;
+  // The work list is built on the host: fetch the chunk lengths and first
+  // positions (a synchronous copy; this entry point is for tests and timing,
+  // the model forward builds the list from host data).
+  std::vector<int32_t> h_count(num_seqs > 0 ? num_seqs : 0);
+  std::vector<uint32_t> h_first(h_count.size());
+  if (num_seqs > 0) {
+    HIP_TRY(st, hipMemcpyAsync(h_count.data(), d_row_count, num_seqs * 4, hipMemcpyDeviceToHost,
+                               dev->stream));
+    HIP_TRY(st, hipMemcpyAsync(h_first.data(), d_first_pos, num_seqs * 4, hipMemcpyDeviceToHost,
+                               dev->stream));
+    HIP_TRY(st, hipStreamSynchronize(dev->stream));
+  }
+  std::vector<PrefillTile> order;
+  build_prefill_order(h_count.data(), h_first.data(), num_seqs, num_q_heads / g.num_kv_heads,
+                      &order);
+  HIP_TRY(st, dev->prefill_order.reserve(std::max<size_t>(order.size(), 1) * sizeof(PrefillTile)));
+  if (!order.empty())
+    HIP_TRY(st, hipMemcpyAsync(dev->prefill_order.ptr, order.data(),
+                               order.size() * sizeof(PrefillTile), hipMemcpyHostToDevice,
+                               dev->stream));
   HIP_TRY(st, timed_launch(dev, 2, [&] {
             return launch_paged_prefill(dev->stream, g, d_arena, layer, d_q, num_q_heads,
-                                        num_seqs, d_row_start, d_row_count, d_first_pos,
-                                        d_bt_offsets, d_bt_ids, max_rows, max_position,
-                                        hilo != 0, d_out);
+                                        dev->prefill_order.as<const PrefillTile>(),
+                                        (int64_t)order.size(), d_row_start, d_row_count,
+                                        d_first_pos, d_bt_offsets, d_bt_ids, hilo != 0, d_out);
           }));
   return ORION_HIP_OK;
 }
