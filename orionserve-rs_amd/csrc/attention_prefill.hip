@@ -49,12 +49,8 @@ typedef __attribute__((address_space(3))) v4s lds_v4s;
 typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 typedef float f32x2 __attribute__((ext_vector_type(2)));
 
-constexpr int kWaves = 8;
-constexpr int kThreads = kWaves * 64;
 constexpr int kNR = 2;                      // 16-row MFMA tiles per wave
-constexpr int kBM = kWaves * 16 * kNR;      // packed rows per workgroup
 constexpr int kBN = 64;                     // keys per tile
-constexpr int kStages = 3;                  // K/V tiles resident in LDS (2 in flight)
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kLazy = 8.0f;               // log2 units: weights stay <= 2^8
 
@@ -94,8 +90,10 @@ __device__ inline int swz_v(int r) {
   else return r & 7;
 }
 
-template <int D, bool HILO, bool BIG>
-__global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2)))
+// WAVES waves per workgroup (16 * kNR packed rows each); STAGES K/V tiles
+// resident in LDS, STAGES - 1 of them in flight.
+template <int D, bool HILO, bool BIG, int WAVES, int STAGES>
+__global__ void __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu(2)))
     paged_prefill_kernel(const uint16_t* __restrict__ kv_layer, uint32_t blk_stride,
                          uint32_t v_off, uint32_t slot_stride, uint32_t head_stride,
                          int bs_log2, int num_kv_heads,
@@ -107,6 +105,10 @@ __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2
                          const int64_t* __restrict__ bt_offsets,
                          const uint32_t* __restrict__ bt_ids, float scale_log2,
                          float* __restrict__ out) {
+  constexpr int kWaves = WAVES;
+  constexpr int kBM = kWaves * 16 * kNR;  // packed rows per workgroup
+  constexpr int kStages = STAGES;
+  static_assert(kStages >= 2 && kStages <= 3, "LDS stages");
   constexpr int KCH = D / 32;           // S^T k-steps
   constexpr int DT = D / 16;            // O^T dim tiles
   constexpr int CPR = D / 8;            // 16-byte chunks per key row
@@ -222,19 +224,24 @@ __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2
   constexpr int kTileOps = 2 * LPW;
   constexpr int kIdOps = BIG ? 0 : LPW;
 
-  // ---- prologue: tiles 0 and 1 into LDS buffers 0 and 1, ids of tile 2 ----
+  constexpr int kAhead = kStages - 1;  // tiles in flight while one computes
+  constexpr int kBehind = (kAhead - 1) * (kTileOps + kIdOps);  // loads after the next tile's
+
+  // ---- prologue: tiles 0 .. kAhead-1 into LDS buffers 0 .. kAhead-1, ids of
+  // tile kAhead ----
   {
     uint32_t ids0[NID];
-    load_ids(0, ids0);
-    load_tile(0, 0, ids0);
-    if (ntiles > 1) {
-      load_ids(1, ids0);
-      load_tile(1, 1, ids0);
+#pragma unroll
+    for (int i = 0; i < kAhead; ++i) {
+      if (i < ntiles) {
+        load_ids(i, ids0);
+        load_tile(i, i, ids0);
+      }
     }
-    load_ids(2, ids_next);
+    load_ids(kAhead, ids_next);
   }
-  if (ntiles > 1)
-    wait_vmcnt<kTileOps + kIdOps>();  // tile 0 has landed (tile 1 and the ids may not)
+  if (ntiles >= kAhead)
+    wait_vmcnt<kBehind>();  // tile 0 has landed (the later ones and the ids may not)
   else
     wait_vmcnt<0>();
   __syncthreads();
@@ -273,12 +280,11 @@ __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2
   auto step = [&](int t, auto buf_tag) {
     constexpr int BUF = decltype(buf_tag)::value;
     constexpr uint32_t kBufOff = BUF * TILE * 2;
-    // Tile t + 2 goes into the buffer tile t - 1 used (every wave passed the
-    // barrier that ended step t - 1, so its reads are done).
-    const bool more = t + 2 < ntiles;
-    if (more) {
-      load_tile(t + 2, (BUF + 2) % kStages, ids_next);
-      load_ids(t + 3, ids_next);
+    // Tile t + kAhead goes into the buffer tile t - 1 used (every wave passed
+    // the barrier that ended step t - 1, so its reads are done).
+    if (t + kAhead < ntiles) {
+      load_tile(t + kAhead, (BUF + kAhead) % kStages, ids_next);
+      load_ids(t + kAhead + 1, ids_next);
     }
 
     // S^T[rt][kt]: raw scores of keys t*64 + kt*16 + 4*grp + i, query l16.
@@ -412,10 +418,10 @@ __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2
       }
     }
 
-    // Tile t + 1 must have landed; tile t + 2 (and its successor's ids) may
+    // Tile t + 1 must have landed; the tiles after it (and their ids) may
     // still be in flight.
-    if (more)
-      wait_vmcnt<kTileOps + kIdOps>();
+    if (t + kAhead < ntiles)
+      wait_vmcnt<kBehind>();
     else
       wait_vmcnt<0>();
     __syncthreads();
@@ -424,7 +430,8 @@ __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2
   for (int t = 0; t < ntiles; t += kStages) {
     step(t, std::integral_constant<int, 0>{});
     if (t + 1 < ntiles) step(t + 1, std::integral_constant<int, 1>{});
-    if (t + 2 < ntiles) step(t + 2, std::integral_constant<int, 2>{});
+    if constexpr (kStages > 2)
+      if (t + 2 < ntiles) step(t + 2, std::integral_constant<int, 2>{});
   }
 
   // ---- normalise and store: lane holds dims 16d + 4*grp .. +3 of query l16 ----
@@ -444,8 +451,22 @@ __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2
   }
 }
 
+// Workgroup shape: 8 waves with a 3-stage K/V ring (one workgroup per CU,
+// 96 KiB of LDS at d = 128), or 4 waves with 2 stages (two per CU).
+// ORION_PREFILL_WAVES=4 selects the latter (measurement knob).
+static int prefill_waves() {
+  static const int w = [] {
+    const char* e = getenv("ORION_PREFILL_WAVES");
+    return (e && atoi(e) == 4) ? 4 : 8;
+  }();
+  return w;
+}
+
+int prefill_tile_rows() { return prefill_waves() * 16 * kNR; }
+
 void build_prefill_order(const int32_t* row_count, const uint32_t* first_pos, int64_t num_seqs,
                          int64_t group, std::vector<PrefillTile>* order) {
+  const int64_t kBM = prefill_tile_rows();
   std::vector<std::pair<int64_t, PrefillTile>> items;
   for (int64_t s = 0; s < num_seqs; ++s) {
     const int64_t packed = (int64_t)row_count[s] * group;
@@ -479,12 +500,20 @@ hipError_t launch_paged_prefill(hipStream_t st, const KvGeom& kv, const void* ar
   if (num_tiles * hkv > INT32_MAX) return hipErrorInvalidValue;
   const float scale_log2 = kLog2e / sqrtf((float)D);
   const dim3 grid((unsigned)(num_tiles * hkv));
-#define ORION_PREFILL_B(DD, HH, BB)                                                             \
-  hipLaunchKernelGGL((paged_prefill_kernel<DD, HH, BB>), grid, dim3(kThreads), 0, st, base,         \
+  const int waves = prefill_waves();
+#define ORION_PREFILL_W(DD, HH, BB, WW, SS)                                                      \
+  hipLaunchKernelGGL((paged_prefill_kernel<DD, HH, BB, WW, SS>), grid, dim3(WW * 64), 0, st, base, \
                      (uint32_t)a.blk, (uint32_t)a.v_off, (uint32_t)a.slot, (uint32_t)a.head,   \
                      bs_log2,                                                                  \
                      (int)hkv, (int)hq, q, order, row_start, row_count, first_pos, bt_offsets, \
                      bt_ids, scale_log2, out)
+#define ORION_PREFILL_B(DD, HH, BB)           \
+  do {                                        \
+    if (waves == 4)                           \
+      ORION_PREFILL_W(DD, HH, BB, 4, 2);      \
+    else                                      \
+      ORION_PREFILL_W(DD, HH, BB, 8, 3);      \
+  } while (0)
 #define ORION_PREFILL(DD, HH)        \
   do {                               \
     if (big)                         \
@@ -500,6 +529,7 @@ hipError_t launch_paged_prefill(hipStream_t st, const KvGeom& kv, const void* ar
   }
 #undef ORION_PREFILL
 #undef ORION_PREFILL_B
+#undef ORION_PREFILL_W
   return hipGetLastError();
 }
 

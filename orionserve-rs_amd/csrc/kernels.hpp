@@ -92,6 +92,7 @@ hipError_t launch_paged_decode(hipStream_t st, const KvGeom& kv, const void* are
 struct PrefillTile {
   int32_t seq, tile;
 };
+int prefill_tile_rows();  // packed rows per prefill workgroup
 void build_prefill_order(const int32_t* row_count, const uint32_t* first_pos, int64_t num_seqs,
                          int64_t group, std::vector<PrefillTile>* order);
 hipError_t launch_paged_prefill(hipStream_t st, const KvGeom& kv, const void* arena,
