@@ -178,6 +178,36 @@ int orion_hip_model_init_synthetic(orion_hip_model* model, uint64_t seed, float 
  * (`which`, `layer`), as f32 (for matrices: already rounded to bf16). */
 float orion_hip_synthetic_value(uint64_t seed, int which, int layer, uint64_t index, float std);
 
+/* ---- Safetensors checkpoints (crates/orion-models/src/loader.rs) ----------
+ * A host-side handle over every `*.safetensors` file of a directory, memory-
+ * mapped; names resolve to the first file (sorted paths) holding them
+ * (CheckpointLoader::open, loader.rs:113-164).  Errors name the reference's
+ * ModelError kind in the message: "path not found", "missing file",
+ * "malformed", "tensor not found", "shape mismatch", "unsupported dtype". */
+typedef struct orion_hip_checkpoint orion_hip_checkpoint;
+int orion_hip_checkpoint_open(const char* dir, orion_hip_checkpoint** out);
+void orion_hip_checkpoint_close(orion_hip_checkpoint* ck);
+/* Distinct tensor names (CheckpointLoader::len, loader.rs:166-169). */
+int orion_hip_checkpoint_num_tensors(const orion_hip_checkpoint* ck, int64_t* count);
+/* Tensor `index` in sorted-name order (CheckpointLoader::names, :180-185):
+ * its name (NUL-terminated, truncated to name_len), dtype (ORION_DTYPE_F32,
+ * F16, BF16, or -1 for any other safetensors dtype), rank and shape
+ * (up to 8 dimensions). */
+int orion_hip_checkpoint_tensor_info(const orion_hip_checkpoint* ck, int64_t index, char* name,
+                                     size_t name_len, int32_t* dtype, int32_t* ndim,
+                                     int64_t* shape8);
+/* Copies tensor `name` widened to f32 (CheckpointLoader::tensor, :188-202),
+ * `count` must equal its element count.  Test hook. */
+int orion_hip_checkpoint_read_f32(const orion_hip_checkpoint* ck, const char* name, float* out,
+                                  size_t count);
+/* Uploads every weight the model needs, by the Llama/Qwen2 names
+ * (ModelWeights::load, transformer.rs:62-120), straight from the mapping in
+ * the file's dtype: shapes are checked against the model description, Q/K/V
+ * biases are read when the model has them (absent ones stay zero, as the
+ * reference's optional_vector), and an untied model whose checkpoint has no
+ * `lm_head.weight` gets the embedding as its head (transformer.rs:108-112). */
+int orion_hip_model_load_checkpoint(orion_hip_model* model, const orion_hip_checkpoint* ck);
+
 /* Reads one weight back as f32 (count elements).  Test hook. */
 int orion_hip_model_download_weight(orion_hip_model* model, int which, int layer, float* host,
                                     size_t count);

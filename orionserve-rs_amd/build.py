@@ -20,6 +20,7 @@ SOURCES = [
     "gemm.hip",
     "elementwise.hip",
     "runtime.cpp",
+    "checkpoint.cpp",
 ]
 
 CFLAGS = [

@@ -15,6 +15,7 @@
 #include <vector>
 
 #include "../../include/orion_hip.h"
+#include "checkpoint.hpp"
 #include "kernels.hpp"
 
 #define ORION_EXPORT extern "C" __attribute__((visibility("default")))
@@ -639,10 +640,9 @@ ORION_EXPORT int orion_hip_model_upload_weight(orion_hip_model* model, int which
   HIP_TRY(st, hipSetDevice(model->dev->ordinal));
   // Convert on the host (loader.rs:74-98 widens to f32; device matrices are bf16).
   if (s.bf16) {
+    if (dtype == ORION_DTYPE_BF16) return upload_rows(model, s, host, 2, st);
     std::vector<uint16_t> conv(count);
-    if (dtype == ORION_DTYPE_BF16) {
-      std::memcpy(conv.data(), host, count * 2);
-    } else if (dtype == ORION_DTYPE_F32) {
+    if (dtype == ORION_DTYPE_F32) {
       const float* f = static_cast<const float*>(host);
       for (size_t i = 0; i < count; ++i) conv[i] = host_f32_to_bf16(f[i]);
     } else {
@@ -662,6 +662,171 @@ ORION_EXPORT int orion_hip_model_upload_weight(orion_hip_model* model, int which
     for (size_t i = 0; i < count; ++i) conv[i] = host_f16_to_f32(h[i]);
   }
   return upload_rows(model, s, conv.data(), 4, st);
+}
+
+// ---------------------------------------------------------------------------
+// Safetensors checkpoints
+// ---------------------------------------------------------------------------
+
+struct orion_hip_checkpoint {
+  std::unique_ptr<Checkpoint> ck;
+};
+
+ORION_EXPORT int orion_hip_checkpoint_open(const char* dir, orion_hip_checkpoint** out) {
+  const char* st = "checkpoint_open";
+  if (!dir || !out) return internal(st, "null argument");
+  *out = nullptr;
+  Checkpoint::Error kind;
+  std::string err;
+  std::unique_ptr<Checkpoint> ck = Checkpoint::open(dir, &kind, &err);
+  if (!ck) return internal(st, "%s", err.c_str());
+  *out = new orion_hip_checkpoint{std::move(ck)};
+  return ORION_HIP_OK;
+}
+
+ORION_EXPORT void orion_hip_checkpoint_close(orion_hip_checkpoint* ck) { delete ck; }
+
+ORION_EXPORT int orion_hip_checkpoint_num_tensors(const orion_hip_checkpoint* ck,
+                                                  int64_t* count) {
+  if (!ck || !count) return internal("checkpoint_num_tensors", "null argument");
+  *count = (int64_t)ck->ck->names().size();
+  return ORION_HIP_OK;
+}
+
+ORION_EXPORT int orion_hip_checkpoint_tensor_info(const orion_hip_checkpoint* ck, int64_t index,
+                                                  char* name, size_t name_len, int32_t* dtype,
+                                                  int32_t* ndim, int64_t* shape8) {
+  const char* st = "checkpoint_tensor_info";
+  if (!ck) return internal(st, "null checkpoint");
+  const auto& names = ck->ck->names();
+  if (index < 0 || index >= (int64_t)names.size())
+    return internal(st, "tensor index %lld out of range (have %zu)", (long long)index,
+                    names.size());
+  const CheckpointTensor* t = ck->ck->find(names[index]);
+  if (t->shape.size() > 8) return internal(st, "tensor `%s` has rank > 8", t->name.c_str());
+  if (name && name_len) {
+    const size_t n = std::min(name_len - 1, t->name.size());
+    std::memcpy(name, t->name.data(), n);
+    name[n] = '\0';
+  }
+  if (dtype) *dtype = t->dtype;
+  if (ndim) *ndim = (int32_t)t->shape.size();
+  if (shape8)
+    for (size_t i = 0; i < t->shape.size(); ++i) shape8[i] = t->shape[i];
+  return ORION_HIP_OK;
+}
+
+namespace {
+
+int64_t numel(const CheckpointTensor& t) {
+  int64_t n = 1;
+  for (int64_t d : t.shape) n *= d;
+  return n;
+}
+
+std::string shape_str(const std::vector<int64_t>& v) {
+  std::string s = "[";
+  for (size_t i = 0; i < v.size(); ++i) s += (i ? ", " : "") + std::to_string(v[i]);
+  return s + "]";
+}
+
+// Looks a tensor up with the reference's checks (loader.rs:188-235): present,
+// the expected shape, a dtype the device path reads.
+int checked_tensor(const Checkpoint& ck, const std::string& name,
+                   const std::vector<int64_t>& shape, const char* st,
+                   const CheckpointTensor** out) {
+  const CheckpointTensor* t = ck.find(name);
+  if (!t) return internal(st, "tensor not found: %s", name.c_str());
+  if (t->shape != shape)
+    return internal(st, "shape mismatch for `%s`: expected %s, got %s", name.c_str(),
+                    shape_str(shape).c_str(), shape_str(t->shape).c_str());
+  if (t->dtype < 0)
+    return internal(st, "unsupported dtype %s (tensor `%s`)", t->dtype_name.c_str(),
+                    name.c_str());
+  *out = t;
+  return ORION_HIP_OK;
+}
+
+}  // namespace
+
+ORION_EXPORT int orion_hip_checkpoint_read_f32(const orion_hip_checkpoint* ck, const char* name,
+                                               float* out, size_t count) {
+  const char* st = "checkpoint_read_f32";
+  if (!ck || !name || !out) return internal(st, "null argument");
+  const CheckpointTensor* t = ck->ck->find(name);
+  if (!t) return internal(st, "tensor not found: %s", name);
+  if (t->dtype < 0)
+    return internal(st, "unsupported dtype %s (tensor `%s`)", t->dtype_name.c_str(), name);
+  if ((int64_t)count != numel(*t))
+    return internal(st, "tensor `%s` has %lld elements, asked for %zu", name,
+                    (long long)numel(*t), count);
+  for (size_t i = 0; i < count; ++i) {
+    if (t->dtype == ORION_DTYPE_F32) {
+      std::memcpy(&out[i], static_cast<const char*>(t->data) + 4 * i, 4);
+    } else {
+      uint16_t h;
+      std::memcpy(&h, static_cast<const char*>(t->data) + 2 * i, 2);
+      out[i] = t->dtype == ORION_DTYPE_BF16 ? host_bf16_to_f32(h) : host_f16_to_f32(h);
+    }
+  }
+  return ORION_HIP_OK;
+}
+
+ORION_EXPORT int orion_hip_model_load_checkpoint(orion_hip_model* model,
+                                                 const orion_hip_checkpoint* ck) {
+  const char* st = "load_checkpoint";
+  if (!model || !ck) return internal(st, "null argument");
+  const auto& d = model->desc;
+  const int64_t H = d.hidden_size, F = d.intermediate_size, V = d.vocab_size;
+  const int64_t qd = (int64_t)d.num_attention_heads * d.head_dim;
+  const int64_t kvd = (int64_t)d.num_kv_heads * d.head_dim;
+  const Checkpoint& c = *ck->ck;
+  auto put = [&](int which, int layer, const std::string& name,
+                 const std::vector<int64_t>& shape) -> int {
+    const CheckpointTensor* t = nullptr;
+    if (int rc = checked_tensor(c, name, shape, st, &t)) return rc;
+    return orion_hip_model_upload_weight(model, which, layer, t->data, t->dtype,
+                                         (size_t)numel(*t));
+  };
+  if (int rc = put(ORION_W_EMBED, -1, "model.embed_tokens.weight", {V, H})) return rc;
+  for (int l = 0; l < d.num_layers; ++l) {
+    const std::string p = "model.layers." + std::to_string(l);
+    struct Item {
+      int which;
+      const char* suffix;
+      std::vector<int64_t> shape;
+    };
+    const Item items[] = {
+        {ORION_W_INPUT_NORM, ".input_layernorm.weight", {H}},
+        {ORION_W_Q, ".self_attn.q_proj.weight", {qd, H}},
+        {ORION_W_K, ".self_attn.k_proj.weight", {kvd, H}},
+        {ORION_W_V, ".self_attn.v_proj.weight", {kvd, H}},
+        {ORION_W_O, ".self_attn.o_proj.weight", {H, qd}},
+        {ORION_W_POST_NORM, ".post_attention_layernorm.weight", {H}},
+        {ORION_W_GATE, ".mlp.gate_proj.weight", {F, H}},
+        {ORION_W_UP, ".mlp.up_proj.weight", {F, H}},
+        {ORION_W_DOWN, ".mlp.down_proj.weight", {H, F}},
+    };
+    for (const Item& it : items)
+      if (int rc = put(it.which, l, p + it.suffix, it.shape)) return rc;
+    if (d.has_qkv_bias) {
+      // Optional (loader.rs:226-235): absent biases stay zero; a present one
+      // of the wrong shape is an error.
+      const Item biases[] = {{ORION_W_Q_BIAS, ".self_attn.q_proj.bias", {qd}},
+                             {ORION_W_K_BIAS, ".self_attn.k_proj.bias", {kvd}},
+                             {ORION_W_V_BIAS, ".self_attn.v_proj.bias", {kvd}}};
+      for (const Item& it : biases)
+        if (c.find(p + it.suffix))
+          if (int rc = put(it.which, l, p + it.suffix, it.shape)) return rc;
+    }
+  }
+  if (int rc = put(ORION_W_FINAL_NORM, -1, "model.norm.weight", {H})) return rc;
+  if (!d.tied_lm_head) {
+    const char* head = c.find("lm_head.weight") ? "lm_head.weight" : "model.embed_tokens.weight";
+    if (int rc = put(ORION_W_LM_HEAD, -1, head, {V, H})) return rc;
+  }
+  HIP_TRY(st, hipStreamSynchronize(model->dev->stream));
+  return ORION_HIP_OK;
 }
 
 ORION_EXPORT int orion_hip_model_download_weight(orion_hip_model* model, int which, int layer,

@@ -42,6 +42,9 @@ EXPORTED = [
     "orion_hip_kernel_timing", "orion_hip_kernel_timing_read",
     "orion_hip_model_create", "orion_hip_model_destroy", "orion_hip_model_upload_weight",
     "orion_hip_model_init_synthetic", "orion_hip_synthetic_value",
+    "orion_hip_checkpoint_open", "orion_hip_checkpoint_close", "orion_hip_checkpoint_num_tensors",
+    "orion_hip_checkpoint_tensor_info", "orion_hip_checkpoint_read_f32",
+    "orion_hip_model_load_checkpoint",
     "orion_hip_model_download_weight", "orion_hip_model_forward", "orion_hip_model_kv_read",
     "orion_hip_model_kv_write", "orion_hip_model_kv_arena", "orion_hip_model_kv_layout", "orion_hip_decode_plan_create",
     "orion_hip_decode_plan_destroy", "orion_hip_decode_plan_info", "orion_hip_paged_attention_decode",
@@ -138,6 +141,13 @@ def load_library(path: str = LIB_PATH) -> C.CDLL:
         "orion_hip_model_upload_weight": ([vp, C.c_int, C.c_int, vp, C.c_int, sz], C.c_int),
         "orion_hip_model_init_synthetic": ([vp, u64, f32], C.c_int),
         "orion_hip_synthetic_value": ([u64, C.c_int, C.c_int, u64, f32], f32),
+        "orion_hip_checkpoint_open": ([C.c_char_p, P(vp)], C.c_int),
+        "orion_hip_checkpoint_close": ([vp], None),
+        "orion_hip_checkpoint_num_tensors": ([vp, P(i64)], C.c_int),
+        "orion_hip_checkpoint_tensor_info": ([vp, i64, C.c_char_p, sz, P(i32), P(i32), P(i64)],
+                                             C.c_int),
+        "orion_hip_checkpoint_read_f32": ([vp, C.c_char_p, vp, sz], C.c_int),
+        "orion_hip_model_load_checkpoint": ([vp, vp], C.c_int),
         "orion_hip_model_download_weight": ([vp, C.c_int, C.c_int, vp, sz], C.c_int),
         "orion_hip_model_forward": ([vp, P(BatchDesc), vp, vp], C.c_int),
         "orion_hip_model_kv_read": ([vp, i64, u32, i64, i64, C.c_int, vp], C.c_int),
@@ -409,6 +419,82 @@ class ModelMetadata:
         return self.architecture == "qwen2"
 
 
+def _model_error(e: InternalError):
+    """The reference's ModelError variant for a checkpoint failure, from the
+    kind the library's message starts with."""
+    import hf_config as hc
+
+    msg = str(e)
+    for prefix, cls in (("path not found", hc.PathNotFound), ("missing file", hc.MissingFile),
+                        ("malformed", hc.Malformed), ("tensor not found", hc.TensorNotFound),
+                        ("shape mismatch", hc.ShapeMismatch),
+                        ("unsupported dtype", hc.UnsupportedDtype)):
+        if msg.startswith(prefix):
+            return cls(msg)
+    return e
+
+
+class Checkpoint:
+    """CheckpointLoader (crates/orion-models/src/loader.rs:102-236) over the
+    library's memory-mapped safetensors reader; host-side, needs no GPU."""
+
+    def __init__(self, directory: str):
+        lib = load_library()
+        h = C.c_void_p()
+        try:
+            _check(lib.orion_hip_checkpoint_open(os.fsencode(directory), C.byref(h)))
+        except InternalError as e:
+            raise _model_error(e) from None
+        self.handle = h.value
+        self._lib = lib
+
+    def __len__(self) -> int:
+        n = C.c_int64()
+        _check(self._lib.orion_hip_checkpoint_num_tensors(self.handle, C.byref(n)))
+        return n.value
+
+    def info(self, index: int):
+        """(name, dtype code or -1, shape) of tensor `index` in name order."""
+        buf = C.create_string_buffer(1024)
+        dt, nd = C.c_int32(), C.c_int32()
+        shape = (C.c_int64 * 8)()
+        _check(self._lib.orion_hip_checkpoint_tensor_info(self.handle, index, buf, 1024,
+                                                          C.byref(dt), C.byref(nd), shape))
+        return buf.value.decode(), dt.value, [shape[i] for i in range(nd.value)]
+
+    def names(self) -> List[str]:
+        return [self.info(i)[0] for i in range(len(self))]
+
+    def contains(self, name: str) -> bool:
+        return name in self.names()
+
+    def tensor(self, name: str):
+        """(f32 values, shape), CheckpointLoader::tensor (loader.rs:188-202)."""
+        for i in range(len(self)):
+            n, dt, shape = self.info(i)
+            if n == name:
+                out = np.empty(int(np.prod(shape, dtype=np.int64)), dtype=np.float32)
+                try:
+                    _check(self._lib.orion_hip_checkpoint_read_f32(
+                        self.handle, name.encode(), out.ctypes.data, out.size))
+                except InternalError as e:
+                    raise _model_error(e) from None
+                return out, shape
+        import hf_config as hc
+        raise hc.TensorNotFound(f"tensor not found: {name}")
+
+    def close(self) -> None:
+        if self.handle:
+            self._lib.orion_hip_checkpoint_close(self.handle)
+            self.handle = None
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
+
+
 class HipTransformerModel:
     """`LanguageModel` (traits.rs:297-309) over the reference's TransformerModel
     (transformer.rs:137-443), executing on one MI355X."""
@@ -428,6 +514,33 @@ class HipTransformerModel:
         h = C.c_void_p()
         _check(backend.lib.orion_hip_model_create(backend.handle, C.byref(d), C.byref(h)))
         self.handle = h.value
+
+    @classmethod
+    def from_directory(cls, directory: str, num_blocks: int, block_size: int,
+                       backend: HipBackend, kv_dtype: int = BF16) -> "HipTransformerModel":
+        """TransformerModel::from_directory (transformer.rs:180-204): config.json
+        through HfConfig, then every weight straight from the safetensors
+        mapping to the device in the file's dtype."""
+        import hf_config as hc
+
+        cfg = hc.HfConfig.load(directory)
+        name = os.path.basename(os.path.normpath(directory)) or "model"
+        meta = cfg.to_metadata(name)
+        with Checkpoint(directory) as ck:
+            model = cls(meta, num_blocks, block_size, backend, kv_dtype)
+            try:
+                model.load_checkpoint(ck)
+            except BaseException:
+                model.close()
+                raise
+        return model
+
+    def load_checkpoint(self, ck: Checkpoint) -> None:
+        """ModelWeights::load (transformer.rs:62-120) from an open checkpoint."""
+        try:
+            _check(self._backend.lib.orion_hip_model_load_checkpoint(self.handle, ck.handle))
+        except InternalError as e:
+            raise _model_error(e) from None
 
     def metadata(self) -> ModelMetadata:
         return self.meta
