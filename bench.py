@@ -251,6 +251,44 @@ def gemm_shapes(reps=5):
     return out
 
 
+def sampling_bench(rows=32, vocab=32000, reps=10, seed=20261206):
+    """The device sampler (runtime/src/sampling.rs DefaultSampler) on the
+    config-4 decode batch's logits shape, per call including the token copy
+    back, against the oracle's restatement on the host for the same rows."""
+    import oracle as orc
+    import orion_hip as oh
+
+    rng = np.random.default_rng(seed)
+    logits = (rng.standard_normal((rows, vocab)) * 2.0).astype(np.float32)
+    prev = [rng.integers(0, vocab, 64).tolist() for _ in range(rows)]
+    uni = rng.random(rows, dtype=np.float32).tolist()
+    cases = {"greedy": oh.SamplingParams(temperature=0.0),
+             "top_k50_top_p0.9": oh.SamplingParams(temperature=0.8, top_k=50, top_p=0.9,
+                                                   repetition_penalty=1.1),
+             "top_p0.95_full_vocab": oh.SamplingParams(temperature=1.0, top_p=0.95)}
+    be = oh.HipBackend(0)
+    d = be.alloc(rows * vocab * 4)
+    out = {"rows": rows, "vocab": vocab}
+    for name, p in cases.items():
+        times = []
+        for _ in range(reps + 2):
+            d.upload(logits)
+            be.synchronize()
+            t0 = time.perf_counter()
+            oh.sample(be, d.ptr, rows, vocab, [p] * rows, prev, uni)
+            times.append(time.perf_counter() - t0)
+        t0 = time.perf_counter()
+        for r in range(rows):
+            orc.sample(logits[r], prev[r], p.temperature, p.top_k, p.top_p,
+                       p.repetition_penalty, uni[r])
+        cpu = time.perf_counter() - t0
+        out[name] = {"device_ms": round(float(np.median(times[2:])) * 1e3, 3),
+                     "oracle_1thread_ms": round(cpu * 1e3, 2)}
+    d.free()
+    be.close()
+    return out
+
+
 QWEN2_7B_LAYER = dict(H=3584, hq=28, hkv=4, d=128, F=18944, V=1024, eps=1e-6, theta=1000000.0,
                       max_pos=16640)
 
@@ -421,6 +459,7 @@ def main():
     ap.add_argument("--no-prefill", action="store_true", help="skip the config-3 prefill kernel")
     ap.add_argument("--no-mixed", action="store_true", help="skip the config-5 mixed batch")
     ap.add_argument("--no-gemm", action="store_true", help="skip the GEMM shape timings")
+    ap.add_argument("--no-sampling", action="store_true", help="skip the device sampler timing")
     ap.add_argument("--kv-layout", choices=["head-major", "reference"], default="reference",
                     help="block-internal order of the KV arena (reference = attention.rs order)")
     ap.add_argument("--copy-calibration", action="store_true",
@@ -543,6 +582,8 @@ def main():
         result["mixed_cfg5"] = mixed_cfg5()
     if not a.no_gemm:
         result["gemm"] = gemm_shapes()
+    if not a.no_sampling:
+        result["sampling"] = sampling_bench()
     print(json.dumps(result))
 
 

@@ -208,6 +208,34 @@ int orion_hip_checkpoint_read_f32(const orion_hip_checkpoint* ck, const char* na
  * `lm_head.weight` gets the embedding as its head (transformer.rs:108-112). */
 int orion_hip_model_load_checkpoint(orion_hip_model* model, const orion_hip_checkpoint* ck);
 
+/* ---- Sampling on the device (runtime/src/sampling.rs DefaultSampler) -------
+ * Per-row parameters, as SamplingParams (orion-core/src/sampling.rs:22-70)
+ * holds them; each is validated as SamplingParams::validate does (:84-106) and
+ * a violation is an ORION_HIP_ERR_INTERNAL naming the field. */
+typedef struct orion_hip_sampling_params {
+  float temperature;        /* 0 = greedy */
+  int32_t top_k;            /* 0 = off */
+  float top_p;              /* (0, 1]; 1 = off */
+  float repetition_penalty; /* > 0; 1 = off */
+} orion_hip_sampling_params;
+
+/* Sampler::sample for every row of d_logits [rows, vocab] (device memory,
+ * filtered in place as the reference's &mut logits): repetition penalty over
+ * the row's previous tokens (host CSR: prev_offsets[rows + 1], prev_tokens),
+ * then argmax for greedy rows, else temperature, top-k, top-p, softmax and the
+ * draw with the row's uniform r in [0, 1) (host, h_uniform[rows]; the
+ * reference draws it from the request's ChaCha8Rng).  Writes one token per
+ * row to host memory.  vocab <= 262144. */
+int orion_hip_sample(orion_hip_device* dev, float* d_logits, int64_t rows, int64_t vocab,
+                     const orion_hip_sampling_params* params, const int64_t* prev_offsets,
+                     const uint32_t* prev_tokens, const float* h_uniform, int32_t* h_tokens);
+
+/* The same over the logits of the model's last forward (one row per sequence),
+ * which then never leave the device. */
+int orion_hip_model_sample(orion_hip_model* model, const orion_hip_sampling_params* params,
+                           const int64_t* prev_offsets, const uint32_t* prev_tokens,
+                           const float* h_uniform, int32_t* h_tokens);
+
 /* Reads one weight back as f32 (count elements).  Test hook. */
 int orion_hip_model_download_weight(orion_hip_model* model, int which, int layer, float* host,
                                     size_t count);

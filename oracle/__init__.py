@@ -16,6 +16,9 @@ Pinning status (what checks each function besides its own restatement):
   model forward .......................... reference fixture model invariants +
                                            float64 numpy restatement of the forward
   argmax, validate ....................... reference KATs
+  DefaultSampler (sample) ................ reference KATs (sampling.rs:296-552) + an
+                                           independent float64 numpy restatement on
+                                           small rows (tests/test_oracle_sampling.py)
 """
 from __future__ import annotations
 
@@ -87,6 +90,7 @@ def lib() -> C.CDLL:
         "oracle_paged_attention_rows": ([vp, i64, i64, i64, i64, i64, i64, i64, i64, vp, vp,
                                          vp, vp, vp, vp], C.c_int),
         "oracle_argmax": ([vp, i64], i64),
+        "oracle_sample": ([vp, i64, vp, i64, f32, i64, f32, f32, f32, C.POINTER(f32)], i64),
         "oracle_validate": ([vp, vp, i64, f32, f32, C.POINTER(f32), C.POINTER(f32),
                              C.POINTER(i64)], i64),
         "oracle_model_create": ([C.POINTER(OracleModelDesc)], vp),
@@ -279,6 +283,20 @@ def argmax(logits) -> Optional[int]:
     x = _f32(logits)
     r = lib().oracle_argmax(x.ctypes.data, x.size)
     return None if r < 0 else r
+
+
+def sample(logits, previous=(), temperature=1.0, top_k=0, top_p=1.0, repetition_penalty=1.0,
+           r=0.5):
+    """DefaultSampler::sample (runtime/src/sampling.rs:266-293) with the draw's
+    uniform `r` given.  Returns (token or None, filtered logits, margin of r
+    to the nearest cumulative boundary)."""
+    x = _f32(logits).copy()
+    prev = np.ascontiguousarray(previous, dtype=np.uint32)
+    m = C.c_float()
+    t = lib().oracle_sample(x.ctypes.data, x.size, prev.ctypes.data if prev.size else None,
+                            prev.size, temperature, top_k, top_p, repetition_penalty, r,
+                            C.byref(m))
+    return (None if t < 0 else int(t)), x, m.value
 
 
 class Tolerance:

@@ -28,6 +28,7 @@
 //     results (expf/powf/cosf/sinf) is unpinned: the oracle calls glibc, which
 //     is what Rust's f32 methods lower to on linux-gnu.
 
+#include <algorithm>
 #include <cmath>
 #include <cstdint>
 #include <cstdio>
@@ -422,6 +423,136 @@ ORACLE_API int64_t oracle_argmax(const float* logits, int64_t len) {
     }
   }
   return best;
+}
+
+// ---- DefaultSampler (runtime/src/sampling.rs) -----------------------------
+// The filters in the reference's order (sampling.rs:9-23): repetition
+// penalty, then (unless greedy) temperature, top-k, top-p, softmax and the
+// draw.  The draw takes the uniform r the reference's ChaCha8Rng would give
+// (`rng.random::<f32>()`, sampling.rs:209-210) as an input: the RNG stream is
+// the caller's.  Also reports how close r lies to the nearest cumulative
+// boundary, so a caller can tell draws that any f32 rounding difference of
+// the probabilities could move.
+static const float kMasked = -1.0e30f;  // sampling.rs:36
+
+// sampling.rs:46-60: sign-aware, once per distinct token, out-of-range ignored.
+static void oracle_repetition_penalty(float* logits, int64_t len, const uint32_t* prev,
+                                      int64_t nprev, float penalty) {
+  if (penalty == 1.0f) return;
+  std::vector<uint32_t> seen(prev, prev + nprev);
+  std::sort(seen.begin(), seen.end());
+  seen.erase(std::unique(seen.begin(), seen.end()), seen.end());
+  for (uint32_t t : seen) {
+    if ((int64_t)t >= len) continue;
+    const float l = logits[t];
+    logits[t] = l > 0.0f ? l / penalty : l * penalty;
+  }
+}
+
+// sampling.rs:67-75
+static void oracle_temperature(float* logits, int64_t len, float temperature) {
+  if (temperature == 1.0f) return;
+  const float inv = 1.0f / temperature;
+  for (int64_t i = 0; i < len; ++i) logits[i] *= inv;
+}
+
+// sampling.rs:82-99: the k-th largest value is the threshold; strictly
+// smaller logits are masked (ties with the threshold survive).
+static void oracle_top_k(float* logits, int64_t len, int64_t k) {
+  if (k == 0 || k >= len) return;
+  std::vector<float> sorted(logits, logits + len);
+  std::nth_element(sorted.begin(), sorted.begin() + (k - 1), sorted.end(),
+                   [](float a, float b) { return a > b; });
+  const float threshold = sorted[k - 1];
+  for (int64_t i = 0; i < len; ++i)
+    if (logits[i] < threshold) logits[i] = kMasked;
+}
+
+// sampling.rs:160-190: max over all, exp of the unmasked, sequential sum,
+// per-element division; uniform when everything is masked or the sum is 0.
+static void oracle_sampling_softmax(const float* logits, int64_t len, float* out) {
+  float mx = -std::numeric_limits<float>::infinity();
+  for (int64_t i = 0; i < len; ++i)
+    if (logits[i] > mx) mx = logits[i];
+  if (!std::isfinite(mx) || mx <= kMasked) {
+    for (int64_t i = 0; i < len; ++i) out[i] = 1.0f / (float)len;
+    return;
+  }
+  float sum = 0.0f;
+  for (int64_t i = 0; i < len; ++i) {
+    out[i] = 0.0f;
+    if (logits[i] <= kMasked) continue;
+    const float e = expf(logits[i] - mx);
+    out[i] = e;
+    sum += e;
+  }
+  if (sum > 0.0f) {
+    for (int64_t i = 0; i < len; ++i) out[i] /= sum;
+  } else {
+    for (int64_t i = 0; i < len; ++i) out[i] = 1.0f / (float)len;
+  }
+}
+
+// sampling.rs:108-144.  The reference's sort is unstable; equal
+// probabilities are ordered here by index (the device does the same).
+static void oracle_top_p(float* logits, int64_t len, float p) {
+  if (p >= 1.0f) return;
+  std::vector<float> probs(len);
+  oracle_sampling_softmax(logits, len, probs.data());
+  std::vector<std::pair<int64_t, float>> cand;
+  for (int64_t i = 0; i < len; ++i)
+    if (probs[i] > 0.0f && logits[i] > kMasked) cand.push_back({i, probs[i]});
+  if (cand.empty()) return;
+  std::stable_sort(cand.begin(), cand.end(),
+                   [](const std::pair<int64_t, float>& a, const std::pair<int64_t, float>& b) {
+                     return a.second > b.second;
+                   });
+  float cumulative = 0.0f;
+  size_t cutoff = cand.size();
+  for (size_t r = 0; r < cand.size(); ++r) {
+    cumulative += cand[r].second;
+    if (cumulative >= p) {
+      cutoff = r + 1;
+      break;
+    }
+  }
+  for (size_t r = cutoff; r < cand.size(); ++r) logits[cand[r].first] = kMasked;
+}
+
+// Sampler::sample for DefaultSampler (sampling.rs:266-293) with the draw's
+// uniform given.  `logits` is modified in place, as the reference's &mut row.
+// Returns the token (-1 for an empty row); *margin = the distance from r to
+// the nearest cumulative boundary of the final distribution (0 for greedy).
+ORACLE_API int64_t oracle_sample(float* logits, int64_t len, const uint32_t* prev, int64_t nprev,
+                                 float temperature, int64_t top_k, float top_p, float penalty,
+                                 float r, float* margin) {
+  if (margin) *margin = 0.0f;
+  if (len <= 0) return -1;
+  oracle_repetition_penalty(logits, len, prev, nprev, penalty);
+  if (temperature == 0.0f) return oracle_argmax(logits, len);
+  oracle_temperature(logits, len, temperature);
+  oracle_top_k(logits, len, top_k);
+  oracle_top_p(logits, len, top_p);
+  std::vector<float> probs(len);
+  oracle_sampling_softmax(logits, len, probs.data());
+  // sample_from (sampling.rs:208-223)
+  float cumulative = 0.0f, lo = 0.0f;
+  for (int64_t i = 0; i < len; ++i) {
+    lo = cumulative;
+    cumulative += probs[i];
+    if (r < cumulative) {
+      if (margin) *margin = std::min(r - lo, cumulative - r);
+      return i;
+    }
+  }
+  int64_t last = -1;
+  for (int64_t i = len - 1; i >= 0; --i)
+    if (probs[i] > 0.0f) {
+      last = i;
+      break;
+    }
+  if (margin) *margin = r - cumulative;
+  return last >= 0 ? last : len - 1;
 }
 
 // orion-cuda/src/lib.rs:206-224 `Tolerance::matches` and :269-317 `validate`:

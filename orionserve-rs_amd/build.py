@@ -21,6 +21,7 @@ SOURCES = [
     "elementwise.hip",
     "runtime.cpp",
     "checkpoint.cpp",
+    "sampling.hip",
 ]
 
 CFLAGS = [

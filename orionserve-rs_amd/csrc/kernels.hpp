@@ -166,6 +166,22 @@ hipError_t launch_gemm(hipStream_t st, const float* x, const uint16_t* w, const 
                        int64_t M, int64_t N, int64_t K, Epilogue ep, float* out,
                        const GemmScratch* scratch = nullptr, const GemmFuse* fuse = nullptr);
 
+// ---- sampling (runtime/src/sampling.rs DefaultSampler) ----------------------
+// Per-row SamplingParams fields the sampler reads (orion-core/src/sampling.rs).
+struct SampleParams {
+  float temperature;
+  int32_t top_k;
+  float top_p;
+  float repetition_penalty;
+};
+constexpr int64_t kSampleMaxVocab = 262144;
+// logits [rows, vocab] are filtered in place; probs_ws holds rows * vocab
+// floats; out gets one token per row.
+hipError_t launch_sample(hipStream_t st, float* logits, int64_t rows, int64_t vocab,
+                         const SampleParams* params, const int64_t* prev_off,
+                         const uint32_t* prev_tok, const float* uniform, float* probs_ws,
+                         int32_t* out);
+
 // ---- elementwise / normalisation -------------------------------------------
 hipError_t launch_embed(hipStream_t st, const uint32_t* tokens, int64_t n, const uint16_t* table,
                         int64_t hidden, float* out);

@@ -146,6 +146,7 @@ struct orion_hip_device {
   // every call on this device's stream.
   DevBuf gemm_ws, gemm_cnt;
   DevBuf prefill_order;  // op-level prefill work list
+  DevBuf sample_io, sample_ws;  // sampler inputs/outputs and probabilities
   // Per-kernel timing (orion_hip_kernel_timing): event pairs per kernel
   // index, resolved when read.
   bool ktiming = false;
@@ -219,6 +220,7 @@ struct orion_hip_model {
   float* rope_sin = nullptr;
   void* arena = nullptr;
   size_t arena_bytes = 0;
+  int64_t last_rows = 0;  // rows of `logits` the last forward produced
 
   // activations / batch buffers (grown on demand)
   DevBuf hidden, xn, qkv, qrot, attn, act, logits, argmax, ws, sumsq;
@@ -304,6 +306,8 @@ ORION_EXPORT void orion_hip_device_close(orion_hip_device* dev) {
   dev->gemm_ws.release();
   dev->gemm_cnt.release();
   dev->prefill_order.release();
+  dev->sample_io.release();
+  dev->sample_ws.release();
   (void)hipStreamDestroy(dev->stream);
   delete dev;
 }
@@ -829,6 +833,106 @@ ORION_EXPORT int orion_hip_model_load_checkpoint(orion_hip_model* model,
   return ORION_HIP_OK;
 }
 
+// ---------------------------------------------------------------------------
+// Sampling
+// ---------------------------------------------------------------------------
+
+namespace {
+
+// SamplingParams::validate (orion-core/src/sampling.rs:84-106), the fields the
+// sampler reads.
+int check_sampling(const orion_hip_sampling_params& p, int64_t row, const char* st) {
+  if (!std::isfinite(p.temperature) || p.temperature < 0.0f)
+    return internal(st, "row %lld: temperature must be a finite value >= 0.0, got %g",
+                    (long long)row, (double)p.temperature);
+  if (!std::isfinite(p.top_p) || p.top_p <= 0.0f || p.top_p > 1.0f)
+    return internal(st, "row %lld: top_p must be in (0.0, 1.0], got %g", (long long)row,
+                    (double)p.top_p);
+  if (!std::isfinite(p.repetition_penalty) || p.repetition_penalty <= 0.0f)
+    return internal(st, "row %lld: repetition_penalty must be a finite value > 0.0, got %g",
+                    (long long)row, (double)p.repetition_penalty);
+  if (p.top_k < 0) return internal(st, "row %lld: top_k must be >= 0", (long long)row);
+  return ORION_HIP_OK;
+}
+
+int sample_on(orion_hip_device* dev, float* d_logits, int64_t rows, int64_t vocab,
+              const orion_hip_sampling_params* params, const int64_t* prev_off,
+              const uint32_t* prev_tok, const float* uniform, int32_t* tokens, const char* st) {
+  if (rows < 0) return internal(st, "rows must be >= 0");
+  if (rows == 0) return ORION_HIP_OK;
+  if (!d_logits || !params || !prev_off || !uniform || !tokens)
+    return internal(st, "null argument");
+  if (vocab <= 0) return internal(st, "sampler received an empty logits row");
+  if (vocab > kSampleMaxVocab)
+    return set_err(ORION_HIP_ERR_BACKEND, st, "vocab %lld exceeds the device sampler's %lld",
+                   (long long)vocab, (long long)kSampleMaxVocab);
+  for (int64_t r = 0; r < rows; ++r) {
+    if (int rc = check_sampling(params[r], r, st)) return rc;
+    if (!(uniform[r] >= 0.0f && uniform[r] < 1.0f))
+      return internal(st, "row %lld: the uniform draw must be in [0, 1)", (long long)r);
+    if (prev_off[r + 1] < prev_off[r]) return internal(st, "prev_offsets must not decrease");
+  }
+  if (prev_off[0] != 0) return internal(st, "prev_offsets[0] must be 0");
+  const int64_t nprev = prev_off[rows];
+  if (nprev > 0 && !prev_tok) return internal(st, "null prev_tokens");
+  // One staging copy: params | offsets | tokens | uniforms | outputs.
+  const size_t o_par = 0;
+  const size_t o_off = (o_par + rows * sizeof(SampleParams) + 7) & ~(size_t)7;
+  const size_t o_tok = o_off + (rows + 1) * 8;
+  const size_t o_uni = (o_tok + nprev * 4 + 3) & ~(size_t)3;
+  const size_t o_out = o_uni + rows * 4;
+  const size_t total = o_out + rows * 4;
+  std::vector<char> host(total);
+  for (int64_t r = 0; r < rows; ++r) {
+    const SampleParams sp{params[r].temperature, params[r].top_k, params[r].top_p,
+                          params[r].repetition_penalty};
+    std::memcpy(host.data() + o_par + r * sizeof(SampleParams), &sp, sizeof(sp));
+  }
+  std::memcpy(host.data() + o_off, prev_off, (rows + 1) * 8);
+  if (nprev) std::memcpy(host.data() + o_tok, prev_tok, nprev * 4);
+  std::memcpy(host.data() + o_uni, uniform, rows * 4);
+  HIP_TRY(st, hipSetDevice(dev->ordinal));
+  HIP_TRY(st, dev->sample_io.reserve(total));
+  HIP_TRY(st, dev->sample_ws.reserve((size_t)rows * vocab * 4));
+  hipStream_t stream = dev->stream;
+  char* d = static_cast<char*>(dev->sample_io.ptr);
+  HIP_TRY(st, hipMemcpyAsync(d, host.data(), o_out, hipMemcpyHostToDevice, stream));
+  HIP_TRY(st, launch_sample(stream, d_logits, rows, vocab,
+                            reinterpret_cast<const SampleParams*>(d + o_par),
+                            reinterpret_cast<const int64_t*>(d + o_off),
+                            reinterpret_cast<const uint32_t*>(d + o_tok),
+                            reinterpret_cast<const float*>(d + o_uni),
+                            dev->sample_ws.as<float>(), reinterpret_cast<int32_t*>(d + o_out)));
+  HIP_TRY(st, hipMemcpyAsync(tokens, d + o_out, rows * 4, hipMemcpyDeviceToHost, stream));
+  HIP_TRY(st, hipStreamSynchronize(stream));
+  for (int64_t r = 0; r < rows; ++r)  // a greedy row with no number above -inf
+    if (tokens[r] < 0) return internal(st, "row %lld: argmax over empty logits", (long long)r);
+  return ORION_HIP_OK;
+}
+
+}  // namespace
+
+ORION_EXPORT int orion_hip_sample(orion_hip_device* dev, float* d_logits, int64_t rows,
+                                  int64_t vocab, const orion_hip_sampling_params* params,
+                                  const int64_t* prev_offsets, const uint32_t* prev_tokens,
+                                  const float* h_uniform, int32_t* h_tokens) {
+  if (!dev) return internal("sample", "null device");
+  return sample_on(dev, d_logits, rows, vocab, params, prev_offsets, prev_tokens, h_uniform,
+                   h_tokens, "sample");
+}
+
+ORION_EXPORT int orion_hip_model_sample(orion_hip_model* model,
+                                        const orion_hip_sampling_params* params,
+                                        const int64_t* prev_offsets, const uint32_t* prev_tokens,
+                                        const float* h_uniform, int32_t* h_tokens) {
+  const char* st = "model_sample";
+  if (!model) return internal(st, "null model");
+  if (model->last_rows <= 0) return internal(st, "no forward has produced logits yet");
+  return sample_on(model->dev, model->logits.as<float>(), model->last_rows,
+                   model->desc.vocab_size, params, prev_offsets, prev_tokens, h_uniform,
+                   h_tokens, st);
+}
+
 ORION_EXPORT int orion_hip_model_download_weight(orion_hip_model* model, int which, int layer,
                                                  float* host, size_t count) {
   const char* st = "download_weight";
@@ -1288,6 +1392,7 @@ ORION_EXPORT int orion_hip_model_forward(orion_hip_model* m, const orion_hip_bat
   const uint16_t* head = m->w_lm ? m->w_lm : m->w_embed;
   float* logits = m->logits.as<float>();
   HIP_TRY(st, gemm_on(m->dev, xn, head, nullptr, S, V, H, Epilogue::kStore, logits));
+  m->last_rows = S;
   if (argmax_out) {
     HIP_TRY(st, launch_argmax(stream, logits, S, V, m->argmax.as<int64_t>()));
     HIP_TRY(st, hipMemcpyAsync(argmax_out, m->argmax.ptr, S * 8, hipMemcpyDeviceToHost, stream));

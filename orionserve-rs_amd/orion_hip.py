@@ -44,7 +44,7 @@ EXPORTED = [
     "orion_hip_model_init_synthetic", "orion_hip_synthetic_value",
     "orion_hip_checkpoint_open", "orion_hip_checkpoint_close", "orion_hip_checkpoint_num_tensors",
     "orion_hip_checkpoint_tensor_info", "orion_hip_checkpoint_read_f32",
-    "orion_hip_model_load_checkpoint",
+    "orion_hip_model_load_checkpoint", "orion_hip_sample", "orion_hip_model_sample",
     "orion_hip_model_download_weight", "orion_hip_model_forward", "orion_hip_model_kv_read",
     "orion_hip_model_kv_write", "orion_hip_model_kv_arena", "orion_hip_model_kv_layout", "orion_hip_decode_plan_create",
     "orion_hip_decode_plan_destroy", "orion_hip_decode_plan_info", "orion_hip_paged_attention_decode",
@@ -68,6 +68,17 @@ class BackendError(EngineError):
         super().__init__(f"backend `hip` failed during {stage}: {reason}")
         self.stage = stage
         self.reason = reason
+
+
+class SamplingParams(C.Structure):
+    """orion_core::SamplingParams (orion-core/src/sampling.rs:22-70), the fields
+    the sampler reads; defaults as SamplingParams::default (:55-70)."""
+
+    _fields_ = [("temperature", C.c_float), ("top_k", C.c_int32), ("top_p", C.c_float),
+                ("repetition_penalty", C.c_float)]
+
+    def __init__(self, temperature=1.0, top_k=0, top_p=1.0, repetition_penalty=1.0):
+        super().__init__(temperature, top_k, top_p, repetition_penalty)
 
 
 class ModelDesc(C.Structure):
@@ -148,6 +159,8 @@ def load_library(path: str = LIB_PATH) -> C.CDLL:
                                              C.c_int),
         "orion_hip_checkpoint_read_f32": ([vp, C.c_char_p, vp, sz], C.c_int),
         "orion_hip_model_load_checkpoint": ([vp, vp], C.c_int),
+        "orion_hip_sample": ([vp, vp, i64, i64, P(SamplingParams), vp, vp, vp, vp], C.c_int),
+        "orion_hip_model_sample": ([vp, P(SamplingParams), vp, vp, vp, vp], C.c_int),
         "orion_hip_model_download_weight": ([vp, C.c_int, C.c_int, vp, sz], C.c_int),
         "orion_hip_model_forward": ([vp, P(BatchDesc), vp, vp], C.c_int),
         "orion_hip_model_kv_read": ([vp, i64, u32, i64, i64, C.c_int, vp], C.c_int),
@@ -589,6 +602,15 @@ class HipTransformerModel:
         return ForwardOutput(logits if logits is not None else np.zeros((S, 0), np.float32), V,
                              list(batch.sequence_ids), am)
 
+    def sample(self, params, previous, uniforms) -> List[int]:
+        """Samples one token per sequence of the last forward from its logits,
+        which stay on the device (runtime/src/sampling.rs DefaultSampler)."""
+        par, offs, toks, uni, out = _sampling_args(params, previous, uniforms)
+        _check(self._backend.lib.orion_hip_model_sample(self.handle, par, offs.ctypes.data,
+                                                        toks.ctypes.data, uni.ctypes.data,
+                                                        out.ctypes.data))
+        return out[:len(params)].tolist()
+
     def kv_read(self, layer: int, block: int, slot: int, head: int, is_value: bool) -> np.ndarray:
         out = np.empty(self.meta.head_dim, dtype=np.float32)
         _check(self._backend.lib.orion_hip_model_kv_read(self.handle, layer, block, slot, head,
@@ -615,6 +637,29 @@ class HipTransformerModel:
         if self.handle:
             self._backend.lib.orion_hip_model_destroy(self.handle)
             self.handle = None
+
+
+def _sampling_args(params, previous, uniforms):
+    rows = len(params)
+    if len(previous) != rows or len(uniforms) != rows:
+        raise ValueError("one params, previous-token list and uniform per row")
+    par = (SamplingParams * max(rows, 1))(*params)
+    offs = np.zeros(rows + 1, np.int64)
+    offs[1:] = np.cumsum([len(p) for p in previous])
+    toks = (np.concatenate([np.asarray(p, np.uint32) for p in previous])
+            if rows and offs[-1] else np.zeros(1, np.uint32))
+    uni = np.ascontiguousarray(uniforms, dtype=np.float32)
+    out = np.empty(max(rows, 1), np.int32)
+    return par, offs, toks, uni, out
+
+
+def sample(be: HipBackend, logits_ptr: int, rows: int, vocab: int, params, previous, uniforms):
+    """Sampler::sample on the device for each row of device logits (filtered in
+    place); `uniforms` are the draws' r values.  Returns the tokens."""
+    par, offs, toks, uni, out = _sampling_args(params, previous, uniforms)
+    _check(be.lib.orion_hip_sample(be.handle, logits_ptr, rows, vocab, par, offs.ctypes.data,
+                                   toks.ctypes.data, uni.ctypes.data, out.ctypes.data))
+    return out[:rows].tolist()
 
 
 def synthetic_value(seed: int, which: int, layer: int, index: int, std: float = 0.02) -> float:
