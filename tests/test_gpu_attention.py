@@ -82,6 +82,22 @@ def test_ragged_positions_and_shared_sequences(backend):
     assert np.abs(got - want).max() <= 1e-4
 
 
+def test_consecutive_calls_of_different_sizes(backend):
+    # The split kernel's last arriving split merges the others, counted on
+    # per-(row, KV head) counters that every launch must leave at zero: calls
+    # with many rows, then few, then many again (and one plan replayed) must
+    # each match the oracle, and replays must repeat the same bits.
+    ctxs = [3000, 70, 1500, 900, 2048, 5, 700, 1300] * 4
+    big = PagedCase(41, ctxs, 32, 8, 128, 16, dtype="bf16")
+    small = PagedCase(42, [4000, 33], 32, 8, 128, 16, dtype="bf16")
+    outs = []
+    for case in (big, small, big, big):
+        got = run_decode(backend, case)
+        assert np.abs(got - case.oracle()).max() <= 1e-4
+        outs.append(got)
+    assert np.array_equal(outs[0], outs[2]) and np.array_equal(outs[2], outs[3])
+
+
 def test_single_position_returns_value_exactly(backend):
     # attention.rs:375-403 at a supported head_dim: one position -> softmax 1.0 -> V.
     case = PagedCase(3, [1, 1, 1], 8, 2, 64, 16, dtype="f32")
