@@ -146,7 +146,8 @@ struct GemmScratch {
 //    per-row f64 sum-of-squares slots [row][norm_slots] a previous GEMM wrote
 //    (summed in slot order) -- the same per-element roundings as rmsnorm;
 //  - sumsq_out (kAccumulate): after out += x W^T, the GEMM writes the f64 sum
-//    of squares of each updated row in gemm_sumsq_slots(N) slots per row;
+//    of squares of each updated row in gemm_sumsq_slots(N) slots per row
+//    (slot j covers columns 64j .. 64j+63);
 //  - defer (kStore): the K-slice partials are left unreduced for the consumer
 //    (launch_rope_and_cache) instead of a reduce launch.
 struct GemmFuse {
@@ -157,7 +158,7 @@ struct GemmFuse {
   double* sumsq_out = nullptr;
   GemmPartials* defer = nullptr;
 };
-bool gemm_splitk_fusable(int64_t M, int64_t K);
+bool gemm_splitk_fusable(int64_t M, int64_t N, int64_t K);
 int gemm_sumsq_slots(int64_t N);
 
 // Scratch a launch_gemm of this shape needs (0 / 0: none).

@@ -1220,8 +1220,9 @@ ORION_EXPORT int orion_hip_model_forward(orion_hip_model* m, const orion_hip_bat
     const char* v = getenv("ORION_GEMM_FUSE");
     return !(v && v[0] == '0');
   }();
-  const bool fused = allow_fuse && gemm_splitk_fusable(n, H) && gemm_splitk_fusable(n, m->qd) &&
-                     gemm_splitk_fusable(n, F);
+  const bool fused = allow_fuse && gemm_splitk_fusable(n, m->qkvd, H) &&
+                     gemm_splitk_fusable(n, H, m->qd) && gemm_splitk_fusable(n, 2 * F, H) &&
+                     gemm_splitk_fusable(n, H, F);
   const int nslots = gemm_sumsq_slots(H);
   if (fused) HIP_TRY(st, m->sumsq.reserve(n * nslots * 8));
   // Attention routing, shared by every layer.  A sequence whose rows are a
