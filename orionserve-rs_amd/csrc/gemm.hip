@@ -713,9 +713,11 @@ namespace {
 // reduces (fused) or a second kernel does.  Chosen per shape from M = 32
 // measurements on the config-4 projections (us per call, weights streamed):
 //   N <= 4096, K <= 4096 (QKV, O)  NT 1, KS 8, fused   O 11.2 -> 10.1
-//   N <= 16384 (gate/up)           NT 2, KS 8, fused   19.3 -> 18.1
+//     partials left to the consumer (QKV into RoPE): NT 2, KS 8; narrower
+//     tiles only repeat the norm and activation staging (7.1 -> 9.9 in the
+//     decode step)
+//   N > 4096 (gate/up, LM head)    NT 2, KS 8, fused   19.3 -> 18.1, 41.4 -> 39.4
 //   K > 4096 (down)                NT 2, KS 16         17.9 -> 15.4
-//   N > 16384 (LM head)            NT 4, KS 8          41.4 -> 37.5
 // Few column tiles want narrow tiles (more workgroups); long K wants long
 // slices (fewer partials); the fused reduction pays while one workgroup's
 // share of the partials is small.  ORION_GEMV_NT / ORION_GEMV_KS /
@@ -731,7 +733,7 @@ struct GemvShape {
   bool fused;  // the last K slice reduces (when the scratch brings counters)
   size_t ws_bytes;
 };
-GemvShape gemv_shape(int64_t M, int64_t N, int64_t K) {
+GemvShape gemv_shape(int64_t M, int64_t N, int64_t K, bool deferred = false) {
   static const int knob_nt = gemv_knob("ORION_GEMV_NT", 1, 2, 4);
   static const int knob_ks = gemv_knob("ORION_GEMV_KS", 4, 8, 16);
   static const bool knob_unfused = [] {
@@ -742,10 +744,10 @@ GemvShape gemv_shape(int64_t M, int64_t N, int64_t K) {
   g.mt = (int)((M + 15) / 16);
   if (K > 4096) {
     g.nt = 2, g.ks = 16, g.fused = false;
-  } else if (N > 16384) {
-    g.nt = 4, g.ks = 8, g.fused = false;
   } else if (N > 4096) {
     g.nt = 2, g.ks = 8, g.fused = true;
+  } else if (deferred) {
+    g.nt = 2, g.ks = 8, g.fused = false;
   } else {
     g.nt = 1, g.ks = 8, g.fused = true;
   }
@@ -817,8 +819,8 @@ void gemm_scratch_need(int64_t M, int64_t N, int64_t K, size_t* ws_bytes, int64_
     *counters = 0;
     return;
   }
-  const GemvShape g = gemv_shape(M, N, K);
-  *ws_bytes = g.ws_bytes;
+  const GemvShape g = gemv_shape(M, N, K), gd = gemv_shape(M, N, K, true);
+  *ws_bytes = std::max(g.ws_bytes, gd.ws_bytes);
   *counters = g.kslices > 1 ? g.n_tiles : 0;
 }
 
@@ -842,14 +844,15 @@ hipError_t launch_gemm(hipStream_t st, const float* x, const uint16_t* w, const 
   // Decode-shaped M: split-K weight streaming (needs the scratch when K spans
   // several slices).
   if (M <= 64 && N <= INT32_MAX && K <= INT32_MAX) {
-    const GemvShape g = gemv_shape(M, N, K);
+    // A consumer that takes the unreduced partials gets them (no reduce
+    // launch); only for the store epilogue.
+    const bool wants_defer = f.defer && ep == Epilogue::kStore && !f.sumsq_out;
+    const GemvShape g = gemv_shape(M, N, K, wants_defer);
     const bool fits = g.kslices == 1 || (scratch && scratch->ws_bytes >= g.ws_bytes);
     if (needs_splitk && !fits) return hipErrorInvalidValue;
     if (fits && g.kslices <= 65535) {
       const int m = (int)M, n = (int)N, k = (int)K, e = (int)ep;
-      // A consumer that takes the unreduced partials gets them (no reduce
-      // launch); only for the store / accumulate epilogues.
-      const bool deferred = f.defer && g.kslices > 1 && ep == Epilogue::kStore && !f.sumsq_out;
+      const bool deferred = wants_defer && g.kslices > 1;
       if (deferred) {
         f.defer->ws = scratch->ws;
         f.defer->kslices = g.kslices;
