@@ -368,7 +368,12 @@ __global__ void __launch_bounds__(256)
   static_assert(MT * KSTEPS * 64 % 256 == 0, "fragments must split evenly over the workgroup");
   // Every load below is unconditional (clamped address, value selected
   // afterwards), so the waits can count them in issue order.
-  float4 xa[FR][2], wa[FR][2];
+  // Fragment j of a thread is f = wave + 4j, so fragments j and j + KSTEPS/4
+  // cover the same k (next row tile): the norm weight is loaded for the first
+  // KSTEPS/4 only.
+  static_assert(KSTEPS % 4 == 0, "fragments of one k repeat every KSTEPS/4");
+  constexpr int FW = KSTEPS / 4;
+  float4 xa[FR][2], wa[FW][2];
   const float* nwp = nsq ? nw : x;
 #pragma unroll
   for (int j = 0; j < FR; ++j) {
@@ -380,9 +385,11 @@ __global__ void __launch_bounds__(256)
     const float* xp = x + (int64_t)min(row, M - 1) * K + kk;
     xa[j][0] = *reinterpret_cast<const float4*>(xp);
     xa[j][1] = *reinterpret_cast<const float4*>(xp + 4);
-    const float* wp = nwp + (nsq ? kk : 0);
-    wa[j][0] = *reinterpret_cast<const float4*>(wp);
-    wa[j][1] = *reinterpret_cast<const float4*>(wp + 4);
+    if (j < FW) {
+      const float* wp = nwp + (nsq ? kk : 0);
+      wa[j][0] = *reinterpret_cast<const float4*>(wp);
+      wa[j][1] = *reinterpret_cast<const float4*>(wp + 4);
+    }
   }
   // Fused RMSNorm: the row's f64 sum-of-squares slots, TPR threads per row,
   // each summing up to kSlotsPerThread consecutive slots (larger rows take
@@ -461,8 +468,9 @@ __global__ void __launch_bounds__(256)
     for (int e = 0; e < 8; ++e) a[e] = live ? a[e] : 0.f;
     if (nsq) {
       const float sc = row < M ? nscale[row] : 0.f;
-      const float wv[8] = {wa[j][0].x, wa[j][0].y, wa[j][0].z, wa[j][0].w,
-                           wa[j][1].x, wa[j][1].y, wa[j][1].z, wa[j][1].w};
+      const float4* wj = wa[j % FW];
+      const float wv[8] = {wj[0].x, wj[0].y, wj[0].z, wj[0].w,
+                           wj[1].x, wj[1].y, wj[1].z, wj[1].w};
 #pragma unroll
       for (int e = 0; e < 8; ++e) a[e] = a[e] * sc * wv[e];
     }
@@ -575,7 +583,7 @@ __global__ void __launch_bounds__(256)
   // Slices are summed in order, CH at a time with all their loads in flight
   // (loads past the last slice fall outside the buffer and read zeros, and
   // adding +0 leaves every sum unchanged).
-  constexpr int CH = 8;
+  constexpr int CH = 4;
   v4f sum[PASSES];
 #pragma unroll
   for (int p = 0; p < PASSES; ++p) sum[p] = v4f{0.f, 0.f, 0.f, 0.f};
