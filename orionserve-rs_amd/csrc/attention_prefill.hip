@@ -288,11 +288,8 @@ __global__ void __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu
     }
 
     // S^T[rt][kt]: raw scores of keys t*64 + kt*16 + 4*grp + i, query l16.
+    // (the first k-step starts from a zero C operand: no zeroing moves)
     f32x4 s[kNR][4];
-#pragma unroll
-    for (int rt = 0; rt < kNR; ++rt)
-#pragma unroll
-      for (int kt = 0; kt < 4; ++kt) s[rt][kt] = f32x4{0.f, 0.f, 0.f, 0.f};
     // K fragments one k-step ahead of the MFMAs that consume them.
     u32x4 kf[2][4];
     auto read_k = [&](int c, u32x4 (&dst)[4]) {
@@ -310,7 +307,8 @@ __global__ void __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu
         const bf16x8 ka = __builtin_bit_cast(bf16x8, kf[c & 1][kt]);
 #pragma unroll
         for (int rt = 0; rt < kNR; ++rt) {
-          s[rt][kt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ka, qhi[rt][c], s[rt][kt], 0, 0, 0);
+          s[rt][kt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+              ka, qhi[rt][c], c == 0 ? f32x4{0.f, 0.f, 0.f, 0.f} : s[rt][kt], 0, 0, 0);
           if constexpr (HILO)
             s[rt][kt] =
                 __builtin_amdgcn_mfma_f32_16x16x32_bf16(ka, qlo[rt][c], s[rt][kt], 0, 0, 0);
@@ -332,11 +330,12 @@ __global__ void __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu
           for (int i = 0; i < 4; ++i)
             if (t * kBN + kt * 16 + 4 * grp + i > qpos[rt]) s[rt][kt][i] = -INFINITY;
       }
-      float mx = -INFINITY;
+      // three-input maxes (v_max3_f32): 8 per 16 scores
+      float mx = fmaxf(fmaxf(s[rt][0][0], s[rt][0][1]), s[rt][0][2]);
+      mx = fmaxf(fmaxf(mx, s[rt][0][3]), s[rt][1][0]);
 #pragma unroll
-      for (int kt = 0; kt < 4; ++kt)
-        mx = fmaxf(fmaxf(mx, fmaxf(s[rt][kt][0], s[rt][kt][1])),
-                   fmaxf(s[rt][kt][2], s[rt][kt][3]));
+      for (int e = 5; e < 16; e += 2)
+        mx = fmaxf(fmaxf(mx, s[rt][e >> 2][e & 3]), s[rt][(e + 1) >> 2][(e + 1) & 3]);
       if (__builtin_amdgcn_ballot_w64(mx > m[rt] + lazy_raw) != 0) {
         mx = fmaxf(mx, __shfl_xor(mx, 16));
         mx = fmaxf(mx, __shfl_xor(mx, 32));
