@@ -344,7 +344,8 @@ __global__ void __launch_bounds__(256)
                      const float* __restrict__ bias, int M, int N, int K, int ep,
                      float* __restrict__ out, float* __restrict__ partial,
                      const double* __restrict__ nsq, int nslots, const float* __restrict__ nw,
-                     float neps, unsigned* __restrict__ tile_cnt, double* __restrict__ sumsq_out) {
+                     float neps, unsigned* __restrict__ tile_cnt, int wpacked,
+                     double* __restrict__ sumsq_out) {
   constexpr int BN = 64 * NT;
   __shared__ __attribute__((aligned(16))) uint4 xs[2][MT * KSTEPS * 64];  // [hi|lo][frag][lane]
   __shared__ float nscale[MT * 16];
@@ -415,17 +416,31 @@ __global__ void __launch_bounds__(256)
 
   // 2. weight loads (clamped column and k-step: unconditional loads)
   //    in k-step order, so the MFMAs of step s wait only for its loads
+  //    Row-major W: lane (l16, grp) reads W[col][k .. k+8) of its column.
+  //    Packed W (wpacked, launch_gemv_pack): the workgroup's whole share is
+  //    one contiguous chunk, in dispatch order, and a wave load one
+  //    contiguous KiB.
   bf16x8 bw[KSTEPS][NT];
   const uint16_t* wrow[NT];
+  int wstep;
+  if (wpacked) {
 #pragma unroll
-  for (int nt = 0; nt < NT; ++nt)
-    wrow[nt] = w + (int64_t)min(n0 + (wave * NT + nt) * 16 + l16, N - 1) * K + k0 + grp * 8;
+    for (int nt = 0; nt < NT; ++nt)
+      wrow[nt] = w + (((int64_t)blockIdx.y * gridDim.x + blockIdx.x) * (4 * NT) + wave * NT + nt) *
+                         (KSTEPS * 512) + lane * 8;
+    wstep = 512;
+  } else {
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt)
+      wrow[nt] = w + (int64_t)min(n0 + (wave * NT + nt) * 16 + l16, N - 1) * K + k0 + grp * 8;
+    wstep = 32;
+  }
 #pragma unroll
   for (int s2 = 0; s2 < KSTEPS; ++s2)
 #pragma unroll
     for (int nt = 0; nt < NT; ++nt)
       bw[s2][nt] = __builtin_bit_cast(
-          bf16x8, *reinterpret_cast<const uint4*>(wrow[nt] + min(s2, nsteps - 1) * 32));
+          bf16x8, *reinterpret_cast<const uint4*>(wrow[nt] + min(s2, nsteps - 1) * wstep));
   // nothing that waits for a load may be scheduled above this point
   __builtin_amdgcn_sched_barrier(0);
 
@@ -584,6 +599,25 @@ __global__ void __launch_bounds__(256)
   // (loads past the last slice fall outside the buffer and read zeros, and
   // adding +0 leaves every sum unchanged).
   constexpr int CH = 4;
+  // What each output element combines with (the residual for accumulate,
+  // the bias for store), loaded ahead of the slice sums so the epilogue
+  // below waits for no further load.
+  float pre[PASSES][4];
+#pragma unroll
+  for (int p = 0; p < PASSES; ++p) {
+    const int e0 = (p * 256 + tid) * 4;
+    const int row = e0 / BN, col = n0 + e0 - row * BN;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const bool ok = row < M && col + j < N;
+      float v = 0.f;
+      if (ok && ep == (int)Epilogue::kAccumulate)
+        v = out[(int64_t)row * N + col + j];
+      else if (ok && bias && ep == (int)Epilogue::kStore)
+        v = bias[col + j];
+      pre[p][j] = v;
+    }
+  }
   v4f sum[PASSES];
 #pragma unroll
   for (int p = 0; p < PASSES; ++p) sum[p] = v4f{0.f, 0.f, 0.f, 0.f};
@@ -627,12 +661,11 @@ __global__ void __launch_bounds__(256)
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         if (col + j < N) {
-          float* op = out + (int64_t)row * N + col + j;
           if (ep == (int)Epilogue::kAccumulate)
-            nv[j] = *op + vv[j];
+            nv[j] = pre[p][j] + vv[j];
           else
-            nv[j] = bias ? vv[j] + bias[col + j] : vv[j];
-          *op = nv[j];
+            nv[j] = bias ? vv[j] + pre[p][j] : vv[j];
+          out[(int64_t)row * N + col + j] = nv[j];
         }
       }
       if (sumsq_out) {
@@ -776,10 +809,11 @@ void launch_gemv_t(const GemvShape& g, hipStream_t st, const float* x, const uin
   const bool fused = g.fused && g.kslices > 1 && reduce && sc && sc->counters &&
                      sc->num_counters >= g.n_tiles;
   hipLaunchKernelGGL((gemm_gemv_kernel<MT, NT, KS>),
-                     dim3((unsigned)g.n_tiles, (unsigned)g.kslices), dim3(256), 0, st, x, w, bias,
+                     dim3((unsigned)g.n_tiles, (unsigned)g.kslices), dim3(256), 0, st, x,
+                     f.w_packed ? f.w_packed : w, bias,
                      M, N, K, ep, out, sc ? sc->ws : nullptr, f.norm_sumsq, f.norm_slots,
                      f.norm_weight, f.norm_eps, fused ? sc->counters : nullptr,
-                     fused ? f.sumsq_out : nullptr);
+                     f.w_packed ? 1 : 0, fused ? f.sumsq_out : nullptr);
   if (g.kslices > 1 && reduce && !fused) {
     const int64_t threads = (int64_t)g.n_tiles * M * 64 * NT;
     hipLaunchKernelGGL((gemm_gemv_reduce_kernel<MT, NT>),
@@ -810,6 +844,48 @@ void launch_gemv(const GemvShape& g, hipStream_t st, const float* x, const uint1
     launch_gemv_nt<MT, 2>(g, st, x, w, bias, M, N, K, ep, out, sc, f, reduce);
 }
 }  // namespace
+
+// One thread per 16-byte unit of the packed layout: unit u = (chunk, step,
+// lane) with chunk = ((slice * n_tiles + tile) * 4 + wave) * NT + nt, i.e.
+// the order in which gemm_gemv_kernel's workgroups (x = column tile, y = K
+// slice), waves, column tiles, k-steps and lanes read it.  Columns past N and
+// k past K are zero.
+__global__ void __launch_bounds__(256)
+    gemv_pack_kernel(const uint16_t* __restrict__ w, int N, int K, int nt, int ks, int n_tiles,
+                     int64_t units, uint4* __restrict__ out) {
+  const int64_t u = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (u >= units) return;
+  const int lane = (int)(u & 63);
+  const int64_t q = u >> 6;
+  const int s = (int)(q % ks);
+  const int64_t chunk = q / ks;
+  const int nti = (int)(chunk % nt);
+  const int wave = (int)((chunk / nt) & 3);
+  const int64_t wg = chunk / (4 * nt);
+  const int bx = (int)(wg % n_tiles), by = (int)(wg / n_tiles);
+  const int col = bx * 64 * nt + (wave * nt + nti) * 16 + (lane & 15);
+  const int k = by * ks * 32 + s * 32 + (lane >> 4) * 8;
+  uint4 v = uint4{0u, 0u, 0u, 0u};
+  if (col < N && k < K) v = *reinterpret_cast<const uint4*>(w + (int64_t)col * K + k);
+  out[u] = v;
+}
+
+size_t gemv_packed_bytes(int64_t N, int64_t K, bool deferred) {
+  if (K % 32 != 0 || K <= 0 || N <= 0) return 0;
+  const GemvShape g = gemv_shape(1, N, K, deferred);
+  return (size_t)g.n_tiles * g.kslices * 4 * g.nt * g.ks * 1024;
+}
+
+hipError_t launch_gemv_pack(hipStream_t st, const uint16_t* w, int64_t N, int64_t K,
+                            bool deferred, uint16_t* out) {
+  if (K % 32 != 0 || K <= 0 || N <= 0 || N > INT32_MAX || K > INT32_MAX)
+    return hipErrorInvalidValue;
+  const GemvShape g = gemv_shape(1, N, K, deferred);
+  const int64_t units = (int64_t)gemv_packed_bytes(N, K, deferred) / 16;
+  hipLaunchKernelGGL(gemv_pack_kernel, dim3((unsigned)((units + 255) / 256)), dim3(256), 0, st, w,
+                     (int)N, (int)K, g.nt, g.ks, g.n_tiles, units, reinterpret_cast<uint4*>(out));
+  return hipGetLastError();
+}
 
 bool gemm_splitk_fusable(int64_t M, int64_t N, int64_t K) {
   if (M < 1 || M > 64 || K % 32 != 0 || K > INT32_MAX || N < 1 || N > INT32_MAX) return false;

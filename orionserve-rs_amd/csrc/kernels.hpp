@@ -157,7 +157,18 @@ struct GemmFuse {
   float norm_eps = 0.f;
   double* sumsq_out = nullptr;
   GemmPartials* defer = nullptr;
+  // The same weights in the decode kernel's packed order (launch_gemv_pack,
+  // same shape and `defer` choice); read instead of w when the decode-shaped
+  // split-K kernel runs.
+  const uint16_t* w_packed = nullptr;
 };
+// Bytes of W [N, K] in the decode kernel's packed order (0: K not a multiple
+// of 32), and the kernel that writes it from row-major W.  `deferred` must be
+// what the consuming launch_gemm calls will have (GemmFuse::defer set, store
+// epilogue, no sums of squares).
+size_t gemv_packed_bytes(int64_t N, int64_t K, bool deferred);
+hipError_t launch_gemv_pack(hipStream_t st, const uint16_t* w, int64_t N, int64_t K,
+                            bool deferred, uint16_t* out);
 bool gemm_splitk_fusable(int64_t M, int64_t N, int64_t K);
 int gemm_sumsq_slots(int64_t N);
 

@@ -203,6 +203,12 @@ struct LayerDev {
   uint16_t* w_o = nullptr;    // [hidden, Hq*d]
   uint16_t* w_gu = nullptr;   // [2*ffn, hidden], gate/up rows interleaved by 8
   uint16_t* w_down = nullptr; // [hidden, ffn]
+  // The same four matrices in the decode GEMM's packed order (launch_gemv_pack),
+  // made on the first decode-shaped forward after a weight write.
+  uint16_t* p_qkv = nullptr;
+  uint16_t* p_o = nullptr;
+  uint16_t* p_gu = nullptr;
+  uint16_t* p_down = nullptr;
 };
 
 struct orion_hip_model {
@@ -215,6 +221,8 @@ struct orion_hip_model {
   uint16_t* w_embed = nullptr;
   uint16_t* w_lm = nullptr;  // null when tied
   float* final_norm = nullptr;
+  uint16_t* p_head = nullptr;  // LM head (or tied embedding) in packed order
+  bool packs_valid = false;    // packed copies match the row-major weights
   std::vector<LayerDev> layers;
   float* rope_cos = nullptr;
   float* rope_sin = nullptr;
@@ -636,6 +644,7 @@ ORION_EXPORT int orion_hip_model_upload_weight(orion_hip_model* model, int which
   const char* st = "upload_weight";
   WeightSlot s;
   if (int rc = weight_slot(model, which, layer, &s)) return rc;
+  model->packs_valid = false;
   if ((int64_t)count != s.rows * s.cols)
     return internal(st, "weight %d has %zu elements, expected %lld", which, count,
                     (long long)(s.rows * s.cols));
@@ -978,6 +987,7 @@ static int init_one(orion_hip_model* m, int which, int layer, uint64_t seed, flo
   const char* st = "init_synthetic";
   WeightSlot s;
   if (int rc = weight_slot(m, which, layer, &s)) return rc;
+  m->packs_valid = false;
   hipStream_t stream = m->dev->stream;
   const float mul = std_ / kIrwinHallSd;
   const uint64_t key = synthetic_key(seed, which, which >= ORION_W_INPUT_NORM ? layer : -1);
@@ -1189,6 +1199,37 @@ int validate_batch(orion_hip_model* m, const orion_hip_batch* b, HostBatch* hb) 
 
 }  // namespace
 
+// Writes the packed copies of every layer matrix and the LM head
+// (allocated on first use), in the geometry each forward GEMM call uses: the
+// QKV GEMM leaves its partials to RoPE (deferred), the others reduce.  A
+// matrix whose K is not a multiple of 32 keeps no copy.
+static hipError_t make_packs(orion_hip_model* m) {
+  const auto& d = m->desc;
+  const int64_t H = d.hidden_size, F = d.intermediate_size, V = d.vocab_size;
+  hipStream_t stream = m->dev->stream;
+  auto one = [&](uint16_t** dst, const uint16_t* w, int64_t N, int64_t K,
+                 bool deferred) -> hipError_t {
+    const size_t bytes = gemv_packed_bytes(N, K, deferred);
+    if (!bytes) return hipSuccess;
+    if (!*dst) {
+      hipError_t e = m->alloc(dst, bytes / 2);
+      if (e != hipSuccess) return e;
+    }
+    return launch_gemv_pack(stream, w, N, K, deferred, *dst);
+  };
+  for (LayerDev& L : m->layers) {
+    hipError_t e = one(&L.p_qkv, L.w_qkv, m->qkvd, H, true);
+    if (e == hipSuccess) e = one(&L.p_o, L.w_o, H, m->qd, false);
+    if (e == hipSuccess) e = one(&L.p_gu, L.w_gu, 2 * F, H, false);
+    if (e == hipSuccess) e = one(&L.p_down, L.w_down, H, F, false);
+    if (e != hipSuccess) return e;
+  }
+  hipError_t e = one(&m->p_head, m->w_lm ? m->w_lm : m->w_embed, V, H, false);
+  if (e != hipSuccess) return e;
+  m->packs_valid = true;
+  return hipSuccess;
+}
+
 ORION_EXPORT int orion_hip_model_forward(orion_hip_model* m, const orion_hip_batch* b,
                                          float* logits_out, int64_t* argmax_out) {
   const char* st = "forward";
@@ -1225,6 +1266,15 @@ ORION_EXPORT int orion_hip_model_forward(orion_hip_model* m, const orion_hip_bat
                      gemm_splitk_fusable(n, H, F);
   const int nslots = gemm_sumsq_slots(H);
   if (fused) HIP_TRY(st, m->sumsq.reserve(n * nslots * 8));
+  // Decode-shaped GEMMs (<= 64 rows) read the packed weight copies, made on
+  // the first such forward after a weight write.  ORION_GEMV_PACK=0 keeps
+  // them on the row-major matrices (A/B knob).
+  static const bool allow_pack = [] {
+    const char* v = getenv("ORION_GEMV_PACK");
+    return !(v && v[0] == '0');
+  }();
+  const bool pack_layers = allow_pack && n <= 64, pack_head = allow_pack && S <= 64;
+  if ((pack_layers || pack_head) && !m->packs_valid) HIP_TRY(st, make_packs(m));
   // Attention routing, shared by every layer.  A sequence whose rows are a
   // chunk of consecutive positions with at least half a prefill tile of
   // (row, query head) pairs goes to the MFMA prefill kernel (bf16 arena);
@@ -1366,6 +1416,7 @@ ORION_EXPORT int orion_hip_model_forward(orion_hip_model* m, const orion_hip_bat
       qkv_x = xn;
     }
     qkv_f.defer = &part;
+    if (pack_layers) qkv_f.w_packed = L.p_qkv;
     HIP_TRY(st, gemm_on(m->dev, qkv_x, L.w_qkv, L.b_qkv, n, m->qkvd, H, Epilogue::kStore, qkv,
                         &qkv_f));
     HIP_TRY(st, launch_rope_and_cache(stream, m->kv, m->arena, l, n, Hq, qkv, m->qkvd, qrot,
@@ -1377,22 +1428,29 @@ ORION_EXPORT int orion_hip_model_forward(orion_hip_model* m, const orion_hip_bat
       HIP_TRY(st, launch_paged_prefill(stream, m->kv, m->arena, l, qrot, Hq, d_pforder,
                                        (int64_t)pf_order.size(), d_pfstart, d_pfcount, d_pfpos,
                                        d_pfoff, d_btids, /*hilo=*/true, attn));
+    GemmFuse o_f = accumulate;
+    if (pack_layers) o_f.w_packed = L.p_o;
     HIP_TRY(st, gemm_on(m->dev, attn, L.w_o, nullptr, n, H, m->qd, Epilogue::kAccumulate,
-                        hidden, &accumulate));
-    const GemmFuse gu_f = norm_in(L.post_norm);
+                        hidden, &o_f));
+    GemmFuse gu_f = norm_in(L.post_norm);
+    if (pack_layers) gu_f.w_packed = L.p_gu;
     if (!fused)
       HIP_TRY(st, launch_rmsnorm(stream, hidden, nullptr, L.post_norm, n, H, d.rms_norm_eps, xn));
     HIP_TRY(st, gemm_on(m->dev, fused ? hidden : xn, L.w_gu, nullptr, n, 2 * F, H,
                         Epilogue::kSwiGLU, act, &gu_f));
+    GemmFuse down_f = accumulate;
+    if (pack_layers) down_f.w_packed = L.p_down;
     HIP_TRY(st, gemm_on(m->dev, act, L.w_down, nullptr, n, H, F, Epilogue::kAccumulate, hidden,
-                        &accumulate));
+                        &down_f));
   }
   // Final norm on the last row of each sequence only (norm is row-wise, so
   // this equals norming all rows and then gathering), then the LM head.
   HIP_TRY(st, launch_rmsnorm(stream, hidden, d_last, m->final_norm, S, H, d.rms_norm_eps, xn));
   const uint16_t* head = m->w_lm ? m->w_lm : m->w_embed;
   float* logits = m->logits.as<float>();
-  HIP_TRY(st, gemm_on(m->dev, xn, head, nullptr, S, V, H, Epilogue::kStore, logits));
+  GemmFuse head_f;
+  if (pack_head) head_f.w_packed = m->p_head;
+  HIP_TRY(st, gemm_on(m->dev, xn, head, nullptr, S, V, H, Epilogue::kStore, logits, &head_f));
   m->last_rows = S;
   if (argmax_out) {
     HIP_TRY(st, launch_argmax(stream, logits, S, V, m->argmax.as<int64_t>()));
