@@ -124,9 +124,19 @@ __device__ inline float partial_sum(const GemmPartials& p, int64_t row, int64_t 
   const int64_t tile = col / p.bn, c = col - tile * p.bn;
   const float* e = p.ws + (tile * p.tile_rows + row) * p.bn + c;
   const int64_t stride = (int64_t)p.n_tiles * p.tile_rows * p.bn;
+  // Slices are loaded 8 at a time with every load of a group in flight, then
+  // added in slice order (a slice past the end adds +0, which leaves the sum
+  // unchanged).
+  const float bias = p.bias ? p.bias[col] : 0.f;
   float v = 0.f;
-  for (int ks = 0; ks < p.kslices; ++ks) v += e[ks * stride];
-  return p.bias ? v + p.bias[col] : v;
+  for (int ks0 = 0; ks0 < p.kslices; ks0 += 8) {
+    float t[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) t[j] = ks0 + j < p.kslices ? e[(ks0 + j) * stride] : 0.f;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) v += t[j];
+  }
+  return p.bias ? v + bias : v;
 }
 #endif
 
