@@ -697,10 +697,25 @@ __global__ void __launch_bounds__(256)
   const int tile = (int)(idx / per_tile);
   const int rem = (int)(idx - tile * per_tile);
   const int row = rem / BN, c = rem - row * BN;
-  float v = 0.f;
-  for (int ks = 0; ks < kslices; ++ks)
-    v += partial[((int64_t)ks * n_tiles + tile) * tile_elems + row * BN + c];
   const int col = tile * BN + c;
+  // The residual (accumulate) or bias (store) first, then the slices 8 at a
+  // time with every load of a group in flight, added in slice order (a slice
+  // past the end adds +0, which leaves the sum unchanged).
+  float pre = 0.f;
+  if (col < N && ep == (int)Epilogue::kAccumulate)
+    pre = out[(int64_t)row * N + col];
+  else if (col < N && bias && ep == (int)Epilogue::kStore)
+    pre = bias[col];
+  const float* pp = partial + (int64_t)tile * tile_elems + row * BN + c;
+  const int64_t slice_stride = (int64_t)n_tiles * tile_elems;
+  float v = 0.f;
+  for (int ks0 = 0; ks0 < kslices; ks0 += 8) {
+    float t[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) t[j] = ks0 + j < kslices ? pp[(ks0 + j) * slice_stride] : 0.f;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) v += t[j];
+  }
   if (ep == (int)Epilogue::kSwiGLU) {
     const float u = __shfl_xor(v, 8);
     if ((c & 15) < 8 && col < N)
@@ -708,12 +723,11 @@ __global__ void __launch_bounds__(256)
   } else {
     float nv = 0.f;
     if (col < N) {
-      float* op = out + (int64_t)row * N + col;
       if (ep == (int)Epilogue::kAccumulate)
-        nv = *op + v;
+        nv = pre + v;
       else
-        nv = bias ? v + bias[col] : v;
-      *op = nv;
+        nv = bias ? v + pre : v;
+      out[(int64_t)row * N + col] = nv;
     }
     // Sum of squares of the updated row, one f64 slot per (row, 64 columns):
     // a wave covers 64 consecutive columns of one row.
