@@ -772,7 +772,8 @@ namespace {
 //     tiles only repeat the norm and activation staging (7.1 -> 9.9 in the
 //     decode step)
 //   N > 4096 (gate/up, LM head)    NT 2, KS 8, fused   19.3 -> 18.1, 41.4 -> 39.4
-//   K > 4096 (down)                NT 2, KS 16         17.9 -> 15.4
+//   K > 4096 (down)                NT 1, KS 8, separate reduce (704 workgroups at 3
+//     per CU; NT 2, KS 16 had 176 at one per CU: decode step 1.690 -> 1.676 ms)
 // Few column tiles want narrow tiles (more workgroups); long K wants long
 // slices (fewer partials); the fused reduction pays while one workgroup's
 // share of the partials is small.  ORION_GEMV_NT / ORION_GEMV_KS /
@@ -798,7 +799,7 @@ GemvShape gemv_shape(int64_t M, int64_t N, int64_t K, bool deferred = false) {
   GemvShape g;
   g.mt = (int)((M + 15) / 16);
   if (K > 4096) {
-    g.nt = 2, g.ks = 16, g.fused = false;
+    g.nt = 1, g.ks = 8, g.fused = false;
   } else if (N > 4096) {
     g.nt = 2, g.ks = 8, g.fused = true;
   } else if (deferred) {
