@@ -344,8 +344,7 @@ __global__ void __launch_bounds__(256)
                      const float* __restrict__ bias, int M, int N, int K, int ep,
                      float* __restrict__ out, float* __restrict__ partial,
                      const double* __restrict__ nsq, int nslots, const float* __restrict__ nw,
-                     float neps, unsigned* __restrict__ tile_cnt, int wpacked,
-                     double* __restrict__ sumsq_out) {
+                     float neps, int wpacked) {
   constexpr int BN = 64 * NT;
   __shared__ __attribute__((aligned(16))) uint4 xs[2][MT * KSTEPS * 64];  // [hi|lo][frag][lane]
   __shared__ float nscale[MT * 16];
@@ -547,138 +546,17 @@ __global__ void __launch_bounds__(256)
     return;
   }
   // Partial tile of this K slice: partial[slice][tile][row][BN], rows < 16*MT.
+  // gemm_gemv_reduce_kernel (or the consumer of deferred partials) sums the
+  // slices in order; the kernel boundary orders the two.
   const int64_t tile_elems = (int64_t)MT * 16 * BN;
   float* mine = partial + ((int64_t)blockIdx.y * gridDim.x + blockIdx.x) * tile_elems;
-  if (!tile_cnt) {
-    // gemm_gemv_reduce_kernel sums the slices in order (the kernel boundary
-    // orders the two).
-#pragma unroll
-    for (int mt = 0; mt < MT; ++mt)
-#pragma unroll
-      for (int nt = 0; nt < NT; ++nt)
-#pragma unroll
-        for (int i = 0; i < 4; ++i)
-          mine[(mt * 16 + 4 * grp + i) * BN + (wave * NT + nt) * 16 + l16] = acc[mt][nt][i];
-    return;
-  }
-  // Fused reduction: the last K slice of this column tile to finish sums all
-  // slices in slice order and applies the epilogue.  Partials are stored and
-  // loaded agent-coherently (sc1: past the per-XCD L2s), so once every
-  // thread's stores have completed (vmcnt 0, then the barrier) the arrival
-  // count orders them before the last workgroup's loads.
 #pragma unroll
   for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
     for (int nt = 0; nt < NT; ++nt)
 #pragma unroll
       for (int i = 0; i < 4; ++i)
-        __hip_atomic_store(mine + (mt * 16 + 4 * grp + i) * BN + (wave * NT + nt) * 16 + l16,
-                           acc[mt][nt][i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-  __shared__ unsigned arrived;
-  __syncthreads();
-  if (tid == 0)
-    arrived = __hip_atomic_fetch_add(tile_cnt + blockIdx.x, 1u, __ATOMIC_RELAXED,
-                                     __HIP_MEMORY_SCOPE_AGENT);
-  __syncthreads();
-  if (arrived != (unsigned)(kslices - 1)) return;
-  if (tid == 0)  // re-armed for the next launch
-    __hip_atomic_store(tile_cnt + blockIdx.x, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  // Thread t sums 4 consecutive columns of one row per pass: a 16-column
-  // group is 4 lanes (SwiGLU partners are 2 lanes apart) and a 64-column
-  // sum-of-squares slot is 16 lanes.
-  const float* tile0 = partial + (int64_t)blockIdx.x * tile_elems;
-  const int64_t slice_stride = (int64_t)gridDim.x * tile_elems;
-  const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
-      (void*)tile0, 0, (int)(((int64_t)(kslices - 1) * slice_stride + tile_elems) * 4),
-      0x00020000);
-  constexpr int PASSES = MT * 16 * BN / 4 / 256;
-  static_assert(MT * 16 * BN % 1024 == 0, "tile must split into whole passes");
-  typedef float v4f __attribute__((ext_vector_type(4)));
-  // Slices are summed in order, CH at a time with all their loads in flight
-  // (loads past the last slice fall outside the buffer and read zeros, and
-  // adding +0 leaves every sum unchanged).
-  constexpr int CH = 4;
-  // What each output element combines with (the residual for accumulate,
-  // the bias for store), loaded ahead of the slice sums so the epilogue
-  // below waits for no further load.
-  float pre[PASSES][4];
-#pragma unroll
-  for (int p = 0; p < PASSES; ++p) {
-    const int e0 = (p * 256 + tid) * 4;
-    const int row = e0 / BN, col = n0 + e0 - row * BN;
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const bool ok = row < M && col + j < N;
-      float v = 0.f;
-      if (ok && ep == (int)Epilogue::kAccumulate)
-        v = out[(int64_t)row * N + col + j];
-      else if (ok && bias && ep == (int)Epilogue::kStore)
-        v = bias[col + j];
-      pre[p][j] = v;
-    }
-  }
-  v4f sum[PASSES];
-#pragma unroll
-  for (int p = 0; p < PASSES; ++p) sum[p] = v4f{0.f, 0.f, 0.f, 0.f};
-  for (int ks0 = 0; ks0 < kslices; ks0 += CH) {
-    v4f t[PASSES][CH];
-#pragma unroll
-    for (int p = 0; p < PASSES; ++p)
-#pragma unroll
-      for (int j = 0; j < CH; ++j)
-        t[p][j] = __builtin_amdgcn_raw_buffer_load_b128(
-            rs, (int)(((int64_t)(ks0 + j) * slice_stride + (p * 256 + tid) * 4) * 4), 0, 16);
-#pragma unroll
-    for (int p = 0; p < PASSES; ++p)
-#pragma unroll
-      for (int j = 0; j < CH; ++j) sum[p] += t[p][j];
-  }
-#pragma unroll
-  for (int p = 0; p < PASSES; ++p) {
-    const int e0 = (p * 256 + tid) * 4;  // element index within the tile
-    const int row = e0 / BN, c = e0 - row * BN;
-    if (row >= M) break;  // rows past M: whole 16-lane groups exit together
-    const v4f v = sum[p];
-    const int col = n0 + c;
-    if (ep == (int)Epilogue::kSwiGLU) {
-      // gate columns 0-7 of a 16-column group pair with up columns 8-15
-      v4f u;
-      u.x = __shfl_xor(v.x, 2);
-      u.y = __shfl_xor(v.y, 2);
-      u.z = __shfl_xor(v.z, 2);
-      u.w = __shfl_xor(v.w, 2);
-      if ((c & 15) < 8 && col < N) {
-        float* op = out + (int64_t)row * (N >> 1) + ((col & ~15) >> 1) + (c & 7);
-        op[0] = v.x / (1.0f + __expf(-v.x)) * u.x;
-        op[1] = v.y / (1.0f + __expf(-v.y)) * u.y;
-        op[2] = v.z / (1.0f + __expf(-v.z)) * u.z;
-        op[3] = v.w / (1.0f + __expf(-v.w)) * u.w;
-      }
-    } else {
-      float nv[4] = {0.f, 0.f, 0.f, 0.f};
-      const float vv[4] = {v.x, v.y, v.z, v.w};
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        if (col + j < N) {
-          if (ep == (int)Epilogue::kAccumulate)
-            nv[j] = pre[p][j] + vv[j];
-          else
-            nv[j] = bias ? vv[j] + pre[p][j] : vv[j];
-          out[(int64_t)row * N + col + j] = nv[j];
-        }
-      }
-      if (sumsq_out) {
-        // one f64 slot per (row, 64 columns): 16 lanes, fixed-order tree
-        double q = (double)nv[0] * nv[0] + (double)nv[1] * nv[1] + (double)nv[2] * nv[2] +
-                   (double)nv[3] * nv[3];
-#pragma unroll
-        for (int o = 1; o < 16; o <<= 1) q += __shfl_xor(q, o);
-        const int slot = col >> 6, nslots = (N + 63) >> 6;
-        if ((lane & 15) == 0 && slot < nslots) sumsq_out[(int64_t)row * nslots + slot] = q;
-      }
-    }
-  }
+        mine[(mt * 16 + 4 * grp + i) * BN + (wave * NT + nt) * 16 + l16] = acc[mt][nt][i];
 }
 
 // Sums the K-slice partials of gemm_gemv_kernel in slice order and applies
@@ -763,22 +641,20 @@ static void launch_skinny(int KW, dim3 grid, hipStream_t st, const float* x, con
 }
 
 namespace {
-// Split-K decode GEMM geometry: NT x 64 columns per workgroup (BN), KS
-// k-steps of 32 per K slice, and whether the last K slice of each column tile
-// reduces (fused) or a second kernel does.  Chosen per shape from M = 32
-// measurements on the config-4 projections (us per call, weights streamed):
-//   N <= 4096, K <= 4096 (QKV, O)  NT 1, KS 8, fused   O 11.2 -> 10.1
+// Split-K decode GEMM geometry: NT x 64 columns per workgroup (BN) and KS
+// k-steps of 32 per K slice; the slices are summed by gemm_gemv_reduce_kernel
+// (or by the consumer of deferred partials).  Chosen per shape from M = 32
+// measurements on the config-4 projections:
+//   N <= 4096, K <= 4096 (QKV, O)  NT 1, KS 8 (O: 32 x 8 workgroups)
 //     partials left to the consumer (QKV into RoPE): NT 2, KS 8; narrower
-//     tiles only repeat the norm and activation staging (7.1 -> 9.9 in the
+//     tiles only repeat the norm and activation staging (7.1 -> 9.9 us in the
 //     decode step)
-//   N > 4096 (gate/up, LM head)    NT 2, KS 8, fused   19.3 -> 18.1, 41.4 -> 39.4
-//   K > 4096 (down)                NT 1, KS 8, separate reduce (704 workgroups at 3
-//     per CU; NT 2, KS 16 had 176 at one per CU: decode step 1.690 -> 1.676 ms)
-// Few column tiles want narrow tiles (more workgroups); long K wants long
-// slices (fewer partials); the fused reduction pays while one workgroup's
-// share of the partials is small.  ORION_GEMV_NT / ORION_GEMV_KS /
-// ORION_GEMV_FUSED_REDUCE=0 override every shape (measurement knobs; NT in
-// {1, 2, 4}, KS in {4, 8, 16}).
+//   N > 4096 (gate/up, LM head)    NT 2, KS 8
+//   K > 4096 (down)                NT 1, KS 8 (704 workgroups at 3 per CU;
+//     NT 2, KS 16 had 176 at one per CU: decode step 1.690 -> 1.676 ms)
+// Few column tiles want narrow tiles (more workgroups).  ORION_GEMV_NT /
+// ORION_GEMV_KS override every shape (measurement knobs; NT in {1, 2, 4}, KS
+// in {4, 8, 16}).
 int gemv_knob(const char* name, int a, int b, int c) {
   const char* e = getenv(name);
   const int v = e ? atoi(e) : 0;
@@ -786,30 +662,24 @@ int gemv_knob(const char* name, int a, int b, int c) {
 }
 struct GemvShape {
   int mt, nt, ks, n_tiles, kslices;
-  bool fused;  // the last K slice reduces (when the scratch brings counters)
   size_t ws_bytes;
 };
 GemvShape gemv_shape(int64_t M, int64_t N, int64_t K, bool deferred = false) {
   static const int knob_nt = gemv_knob("ORION_GEMV_NT", 1, 2, 4);
   static const int knob_ks = gemv_knob("ORION_GEMV_KS", 4, 8, 16);
-  static const bool knob_unfused = [] {
-    const char* e = getenv("ORION_GEMV_FUSED_REDUCE");
-    return e && e[0] == '0';
-  }();
   GemvShape g;
   g.mt = (int)((M + 15) / 16);
   if (K > 4096) {
-    g.nt = 1, g.ks = 8, g.fused = false;
+    g.nt = 1, g.ks = 8;
   } else if (N > 4096) {
-    g.nt = 2, g.ks = 8, g.fused = true;
+    g.nt = 2, g.ks = 8;
   } else if (deferred) {
-    g.nt = 2, g.ks = 8, g.fused = false;
+    g.nt = 2, g.ks = 8;
   } else {
-    g.nt = 1, g.ks = 8, g.fused = true;
+    g.nt = 1, g.ks = 8;
   }
   if (knob_nt) g.nt = knob_nt;
   if (knob_ks) g.ks = knob_ks;
-  if (knob_unfused) g.fused = false;
   g.n_tiles = (int)((N + 64 * g.nt - 1) / (64 * g.nt));
   g.kslices = (int)((K + g.ks * 32 - 1) / (g.ks * 32));
   g.ws_bytes = g.kslices > 1 ? (size_t)g.kslices * g.n_tiles * g.mt * 16 * 64 * g.nt * 4 : 0;
@@ -819,17 +689,12 @@ template <int MT, int NT, int KS>
 void launch_gemv_t(const GemvShape& g, hipStream_t st, const float* x, const uint16_t* w,
                    const float* bias, int M, int N, int K, int ep, float* out,
                    const GemmScratch* sc, const GemmFuse& f, bool reduce) {
-  // The last K slice of each column tile reduces (no second launch) when the
-  // scratch brings counters.
-  const bool fused = g.fused && g.kslices > 1 && reduce && sc && sc->counters &&
-                     sc->num_counters >= g.n_tiles;
   hipLaunchKernelGGL((gemm_gemv_kernel<MT, NT, KS>),
                      dim3((unsigned)g.n_tiles, (unsigned)g.kslices), dim3(256), 0, st, x,
                      f.w_packed ? f.w_packed : w, bias,
                      M, N, K, ep, out, sc ? sc->ws : nullptr, f.norm_sumsq, f.norm_slots,
-                     f.norm_weight, f.norm_eps, fused ? sc->counters : nullptr,
-                     f.w_packed ? 1 : 0, fused ? f.sumsq_out : nullptr);
-  if (g.kslices > 1 && reduce && !fused) {
+                     f.norm_weight, f.norm_eps, f.w_packed ? 1 : 0);
+  if (g.kslices > 1 && reduce) {
     const int64_t threads = (int64_t)g.n_tiles * M * 64 * NT;
     hipLaunchKernelGGL((gemm_gemv_reduce_kernel<MT, NT>),
                        dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, st, sc->ws,
@@ -912,15 +777,13 @@ int gemm_sumsq_slots(int64_t N) {
   return (int)((N + 63) / 64);
 }
 
-void gemm_scratch_need(int64_t M, int64_t N, int64_t K, size_t* ws_bytes, int64_t* counters) {
+void gemm_scratch_need(int64_t M, int64_t N, int64_t K, size_t* ws_bytes) {
   if (M < 1 || M > 64 || K % 32 != 0) {
     *ws_bytes = 0;
-    *counters = 0;
     return;
   }
   const GemvShape g = gemv_shape(M, N, K), gd = gemv_shape(M, N, K, true);
   *ws_bytes = std::max(g.ws_bytes, gd.ws_bytes);
-  *counters = g.kslices > 1 ? g.n_tiles : 0;
 }
 
 hipError_t launch_gemm(hipStream_t st, const float* x, const uint16_t* w, const float* bias,

@@ -140,13 +140,10 @@ __device__ inline float partial_sum(const GemmPartials& p, int64_t row, int64_t 
 }
 #endif
 
-// Scratch for split-K decode GEMMs: partial tiles and per-column-tile
-// arrival counters (zero between calls; the kernel re-arms them).
+// Scratch for split-K decode GEMMs: the K-slice partial tiles.
 struct GemmScratch {
   float* ws = nullptr;
   size_t ws_bytes = 0;
-  unsigned int* counters = nullptr;
-  int64_t num_counters = 0;
 };
 // Fusions a decode-shaped split-K GEMM (gemm_splitk_fusable) performs with
 // its neighbours, so the RMSNorm and residual-add launches between the layer's
@@ -183,7 +180,7 @@ bool gemm_splitk_fusable(int64_t M, int64_t N, int64_t K);
 int gemm_sumsq_slots(int64_t N);
 
 // Scratch a launch_gemm of this shape needs (0 / 0: none).
-void gemm_scratch_need(int64_t M, int64_t N, int64_t K, size_t* ws_bytes, int64_t* counters);
+void gemm_scratch_need(int64_t M, int64_t N, int64_t K, size_t* ws_bytes);
 hipError_t launch_gemm(hipStream_t st, const float* x, const uint16_t* w, const float* bias,
                        int64_t M, int64_t N, int64_t K, Epilogue ep, float* out,
                        const GemmScratch* scratch = nullptr, const GemmFuse* fuse = nullptr);

@@ -142,9 +142,9 @@ struct orion_hip_device {
   hipEvent_t ev_start = nullptr, ev_stop = nullptr;
   std::string name;
   int64_t wave_slots = 2048;  // resident decode waves: CUs x 4 SIMDs x 2
-  // Split-K GEMM scratch (partials + zeroed arrival counters), shared by
-  // every call on this device's stream.
-  DevBuf gemm_ws, gemm_cnt;
+  // Split-K GEMM scratch (partial tiles), shared by every call on this
+  // device's stream.
+  DevBuf gemm_ws;
   DevBuf prefill_order;  // op-level prefill work list
   DevBuf sample_io, sample_ws;  // sampler inputs/outputs and probabilities
   // Per-kernel timing (orion_hip_kernel_timing): event pairs per kernel
@@ -312,7 +312,6 @@ ORION_EXPORT void orion_hip_device_close(orion_hip_device* dev) {
   dev->recycle_events();
   for (hipEvent_t e : dev->event_pool) (void)hipEventDestroy(e);
   dev->gemm_ws.release();
-  dev->gemm_cnt.release();
   dev->prefill_order.release();
   dev->sample_io.release();
   dev->sample_ws.release();
@@ -437,27 +436,17 @@ static hipError_t timed_launch(orion_hip_device* dev, int k, F&& launch) {
   return hipSuccess;
 }
 
-// The split-K GEMM scratch for a call of this shape, grown on demand (new
-// counter memory is zeroed; the kernels leave counters at zero).
+// The split-K GEMM scratch for a call of this shape, grown on demand.
 static hipError_t gemm_scratch(orion_hip_device* dev, int64_t M, int64_t N, int64_t K,
                                GemmScratch* sc) {
   size_t ws = 0;
-  int64_t cnt = 0;
-  gemm_scratch_need(M, N, K, &ws, &cnt);
+  gemm_scratch_need(M, N, K, &ws);
   if (ws > dev->gemm_ws.bytes) {
     hipError_t e = dev->gemm_ws.reserve(ws);
     if (e != hipSuccess) return e;
   }
-  if ((size_t)cnt * 4 > dev->gemm_cnt.bytes) {
-    hipError_t e = dev->gemm_cnt.reserve((size_t)cnt * 4);
-    if (e != hipSuccess) return e;
-    e = hipMemsetAsync(dev->gemm_cnt.ptr, 0, dev->gemm_cnt.bytes, dev->stream);
-    if (e != hipSuccess) return e;
-  }
   sc->ws = dev->gemm_ws.as<float>();
   sc->ws_bytes = dev->gemm_ws.bytes;
-  sc->counters = dev->gemm_cnt.as<unsigned int>();
-  sc->num_counters = (int64_t)(dev->gemm_cnt.bytes / 4);
   return hipSuccess;
 }
 
