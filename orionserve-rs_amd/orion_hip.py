@@ -9,6 +9,7 @@ missing: there is no CPU fallback here.
 """
 from __future__ import annotations
 
+import array
 import ctypes as C
 import os
 from dataclasses import dataclass, field
@@ -380,16 +381,23 @@ class ForwardBatch:
                                 f"{len(self.tokens)} tokens")
 
     def to_csr(self):
-        """Flattened arrays in the layout of orion_hip_batch."""
-        tokens = np.asarray(self.tokens, dtype=np.uint32)
-        positions = np.asarray(self.positions, dtype=np.uint32)
-        counts = np.asarray(self.slot_token_counts, dtype=np.int64)
-        ctx = np.asarray(self.context_lens, dtype=np.int64)
-        offs = np.zeros(len(self.block_tables) + 1, dtype=np.int64)
-        offs[1:] = np.cumsum([len(t) for t in self.block_tables]) if self.block_tables else []
-        ids = (np.concatenate([np.asarray(t, dtype=np.uint32) for t in self.block_tables])
-               if self.block_tables and offs[-1] > 0 else np.zeros(1, dtype=np.uint32))
-        return tokens, positions, counts, ctx, offs, ids
+        """Flattened arrays in the layout of orion_hip_batch.  Built with
+        array.array (straight from Python ints; an out-of-range value raises
+        OverflowError as numpy's conversion does), which keeps the per-step
+        host cost of a 32-sequence decode batch in the tens of microseconds."""
+        def arr(code, values):
+            return np.frombuffer(array.array(code, values), dtype=np.dtype(code))
+        tokens = arr("I", self.tokens)
+        positions = arr("I", self.positions)
+        counts = arr("q", self.slot_token_counts)
+        ctx = arr("q", self.context_lens)
+        flat = array.array("I")
+        offs = array.array("q", [0])
+        for t in self.block_tables:
+            flat.extend(t)
+            offs.append(len(flat))
+        ids = np.frombuffer(flat, dtype=np.uint32) if len(flat) else np.zeros(1, dtype=np.uint32)
+        return tokens, positions, counts, ctx, np.frombuffer(offs, dtype=np.int64), ids
 
 
 @dataclass
