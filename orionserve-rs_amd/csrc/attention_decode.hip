@@ -29,6 +29,7 @@
 #include <algorithm>
 #include <cstdlib>
 #include <functional>
+#include <type_traits>
 #include <vector>
 
 namespace orion {
@@ -501,7 +502,9 @@ __device__ __forceinline__ void decode_wave_mfma2(
   }
 }
 
-template <int D, int G, bool STREAM, bool BIG_BLOCKS>
+// KV: 0 cached K/V loads, 1 streaming, 2 per item (streaming unless the item
+// reads a shared block, DecodeWork::shared).
+template <int D, int G, int KV, bool BIG_BLOCKS>
 __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3)))
     paged_decode_mfma2_kernel(const uint16_t* __restrict__ kv_layer, uint32_t blk_stride,
                               uint32_t v_off, uint32_t slot_stride,
@@ -521,11 +524,20 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3)))
   if (w >= num_work) return;
   const DecodeWork wk = work[w];
   const int row = wk.item / num_kv_heads, kvh = wk.item - row * num_kv_heads;
-  decode_wave_mfma2<D, G, STREAM, BIG_BLOCKS>(kv_layer, blk_stride, v_off, slot_stride, head_stride,
-                                          bs_log2,
-                                          num_q_heads, q, bt_ids + wk.tbl_off, wk.blk0, max_splits,
-                                          scale, out, ws_o, ws_ml, lds_v[wv], lds_q[wv], lds_k[wv], row, kvh,
-                                          wk.start, wk.end, wk.start / chunk, wk.nsplit);
+  auto run = [&](auto stream_tag) {
+    decode_wave_mfma2<D, G, decltype(stream_tag)::value, BIG_BLOCKS>(
+        kv_layer, blk_stride, v_off, slot_stride, head_stride, bs_log2, num_q_heads, q,
+        bt_ids + wk.tbl_off, wk.blk0, max_splits, scale, out, ws_o, ws_ml, lds_v[wv], lds_q[wv],
+        lds_k[wv], row, kvh, wk.start, wk.end, wk.start / chunk, wk.nsplit);
+  };
+  if constexpr (KV == 2) {
+    if (__builtin_amdgcn_readfirstlane(wk.shared))
+      run(std::false_type{});
+    else
+      run(std::true_type{});
+  } else {
+    run(std::integral_constant<bool, KV == 1>{});
+  }
 }
 
 // Merges the per-split states of rows whose context spans several splits.
@@ -697,8 +709,10 @@ void build_decode_plan(const uint32_t* positions, const int32_t* row_seq,
   for (const auto& t : tails) push(t.second, (lens[t.second] / C) * C);
   // Shared blocks: a block id attended by two planned rows (two rows of one
   // sequence share their prefix blocks too).  One pass over the attended
-  // ids with a bitmap that is cleared again afterwards.
-  static thread_local std::vector<uint64_t> seen;
+  // ids with two bitmaps (seen, seen again) that are cleared afterwards;
+  // then each work item is flagged when its token range reads a shared
+  // block.
+  static thread_local std::vector<uint64_t> seen, again;
   bool shared = false;
   auto attended = [&](auto&& f) {
     for (int64_t r = 0; r < rows; ++r) {
@@ -710,13 +724,30 @@ void build_decode_plan(const uint32_t* positions, const int32_t* row_seq,
   };
   attended([&](uint32_t id) {
     const size_t w = id >> 6;
-    if (w >= seen.size()) seen.resize(w + 1, 0);
+    if (w >= seen.size()) seen.resize(w + 1, 0), again.resize(w + 1, 0);
     const uint64_t bit = 1ull << (id & 63);
-    shared |= (seen[w] & bit) != 0;
+    if (seen[w] & bit) {
+      again[w] |= bit;
+      shared = true;
+    }
     seen[w] |= bit;
   });
-  attended([&](uint32_t id) { seen[id >> 6] = 0; });
+  int64_t shared_items = 0;
+  if (shared) {
+    for (DecodeWork& wk : plan->work) {
+      const int nb = ((wk.end - 1) >> bs_log2) - (wk.start >> bs_log2) + 1;
+      bool s = false;
+      for (int j = 0; j < nb && !s; ++j) {
+        const uint32_t id = bt_ids[wk.tbl_off + j];
+        s = (again[id >> 6] >> (id & 63)) & 1;
+      }
+      wk.shared = s ? 1 : 0;
+      shared_items += s;
+    }
+  }
+  attended([&](uint32_t id) { seen[id >> 6] = 0, again[id >> 6] = 0; });
   plan->stream_kv = !shared;
+  plan->mixed_kv = shared && shared_items < (int64_t)plan->work.size();
 }
 
 size_t decode_workspace_bytes(int64_t rows, int64_t hq, int64_t D, int64_t max_splits) {
@@ -752,7 +783,7 @@ static hipError_t launch_valu(int G, dim3 grid, hipStream_t st, const T* kv, con
   return hipGetLastError();
 }
 
-template <int D, bool STREAM, bool BIG>
+template <int D, int KV, bool BIG>
 static hipError_t launch_mfma2(int G, dim3 grid, hipStream_t st, const uint16_t* kv,
                                const ArenaStrides& a, int bsl, int hkv, int hq,
                                const DecodeWork* work, int nwork, const float* q,
@@ -761,7 +792,7 @@ static hipError_t launch_mfma2(int G, dim3 grid, hipStream_t st, const uint16_t*
                                float* wo, float* wml) {
 #define ORION_MFMA2_CASE(GG)                                                                   \
   case GG:                                                                                     \
-    hipLaunchKernelGGL((paged_decode_mfma2_kernel<D, GG, STREAM, BIG>), grid, dim3(256), 0, st, \
+    hipLaunchKernelGGL((paged_decode_mfma2_kernel<D, GG, KV, BIG>), grid, dim3(256), 0, st,     \
                        kv,                                                                     \
                        (uint32_t)a.blk, (uint32_t)a.v_off, (uint32_t)a.slot, (uint32_t)a.head, \
                        bsl, hkv, hq, work, nwork, q, pos, rs, bo, bi, C, ms, scale, out, wo,   \
@@ -831,13 +862,16 @@ hipError_t launch_paged_decode(hipStream_t st, const KvGeom& kv, const void* are
   launch_mfma2<DD, SS, BB>(G, grid, st, base, a, bs_log2, (int)hkv, (int)hq, plan.work,          \
                        plan.num_work, q, positions, row_seq, bt_off, bt_ids, C, ms, scale, out, \
                        ws_o, ws_ml)
-    const bool sk = plan.stream_kv;
+    // per-item load flavour only with whole-block steps (blocks of >= 16 slots)
+    const int kvm = plan.stream_kv ? 1 : (plan.mixed_kv && big) ? 2 : 0;
     if (D == 128)
-      e = big ? (sk ? ORION_MFMA2(128, true, true) : ORION_MFMA2(128, false, true))
-              : (sk ? ORION_MFMA2(128, true, false) : ORION_MFMA2(128, false, false));
+      e = big ? (kvm == 1 ? ORION_MFMA2(128, 1, true)
+                 : kvm == 2 ? ORION_MFMA2(128, 2, true) : ORION_MFMA2(128, 0, true))
+              : (kvm == 1 ? ORION_MFMA2(128, 1, false) : ORION_MFMA2(128, 0, false));
     else if (D == 64)
-      e = big ? (sk ? ORION_MFMA2(64, true, true) : ORION_MFMA2(64, false, true))
-              : (sk ? ORION_MFMA2(64, true, false) : ORION_MFMA2(64, false, false));
+      e = big ? (kvm == 1 ? ORION_MFMA2(64, 1, true)
+                 : kvm == 2 ? ORION_MFMA2(64, 2, true) : ORION_MFMA2(64, 0, true))
+              : (kvm == 1 ? ORION_MFMA2(64, 1, false) : ORION_MFMA2(64, 0, false));
     else
       return hipErrorInvalidValue;
 #undef ORION_MFMA2

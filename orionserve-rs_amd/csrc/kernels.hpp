@@ -46,7 +46,8 @@ inline ArenaStrides arena_strides(const KvGeom& kv) {
 // block_table_ids[tbl_off]; blk0 is its first entry, so the first step's loads
 // can be issued before the slice arrives.
 struct DecodeWork {
-  int32_t item, start, end, nsplit, tbl_off, blk0, pad0, pad1;
+  // shared: the item reads a block that another planned row also reads
+  int32_t item, start, end, nsplit, tbl_off, blk0, shared, pad1;
 };
 // Decode work plan: items in longest-first order; built on the host from the
 // query positions and block tables, shared by every layer of a forward.
@@ -58,6 +59,9 @@ struct DecodePlanHost {
   // No block is attended by two planned rows: K/V are then read once and
   // streamed past the caches; shared (prefix) blocks keep cached loads.
   bool stream_kv = true;
+  // Some blocks are shared but some work items read none of them: those
+  // items stream, the others keep cached loads (DecodeWork::shared).
+  bool mixed_kv = false;
 };
 struct DecodePlanDev {
   const DecodeWork* work = nullptr;
@@ -69,6 +73,7 @@ struct DecodePlanDev {
   const int32_t* rows = nullptr;  // rows to merge (nullptr: every row)
   int num_rows = 0;
   bool stream_kv = true;  // DecodePlanHost::stream_kv
+  bool mixed_kv = false;  // DecodePlanHost::mixed_kv
 };
 void build_decode_plan(const uint32_t* positions, const int32_t* row_seq,
                        const int64_t* bt_offsets, const uint32_t* bt_ids, int64_t rows,

@@ -191,6 +191,7 @@ struct orion_hip_decode_plan {
     d.ws = ws.as<float>();
     d.ws_bytes = ws.bytes;
     d.stream_kv = host.stream_kv;
+    d.mixed_kv = host.mixed_kv;
     return d;
   }
 };
@@ -1361,6 +1362,7 @@ ORION_EXPORT int orion_hip_model_forward(orion_hip_model* m, const orion_hip_bat
   dplan.ws = m->ws.as<float>();
   dplan.ws_bytes = m->ws.bytes;
   dplan.stream_kv = plan.stream_kv;
+  dplan.mixed_kv = plan.mixed_kv;
   if (npf) {
     dplan.rows = reinterpret_cast<const int32_t*>(dp + o_drows);
     dplan.num_rows = (int)plan.rows.size();
