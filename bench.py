@@ -188,6 +188,11 @@ def decode_e2e(steps=64, seqs=32, seed=20261204, cpu=True):
         step()
     be.synchronize()
     n_steps = steps - 2
+    # KV bytes the timed steps read (every attended position, all layers, K
+    # and V) and write (one new position per sequence and step)
+    kv_pos_bytes = cfg["L"] * 2 * cfg["hkv"] * cfg["d"] * 2
+    kv_read = sum(sum(c + k + 1 for c in ctx) for k in range(n_steps)) * kv_pos_bytes
+    kv_write = n_steps * seqs * kv_pos_bytes
     t0 = time.perf_counter()
     for _ in range(n_steps):
         step()
@@ -204,6 +209,10 @@ def decode_e2e(steps=64, seqs=32, seed=20261204, cpu=True):
         "weight_bytes_per_step": int((22 * (2048 * (2048 + 512) + 2048 * 2048 + 3 * 2048 * 5632)
                                       + 32000 * 2048) * 2),
     }
+    # HBM roofline of the step: weights + KV read + KV write per step at 8 TB/s
+    res["hbm_bytes_per_step"] = int(res["weight_bytes_per_step"] + (kv_read + kv_write) / n_steps)
+    res["frac_of_hbm_roofline"] = round(
+        res["hbm_bytes_per_step"] / (res["decode_ms_per_step"] * 1e-3) / HBM_PEAK_GBS / 1e9, 4)
     model.close()
     be.close()
     if cpu:
