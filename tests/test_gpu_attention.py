@@ -83,8 +83,7 @@ def test_ragged_positions_and_shared_sequences(backend):
 
 
 def test_consecutive_calls_of_different_sizes(backend):
-    # The split kernel's last arriving split merges the others, counted on
-    # per-(row, KV head) counters that every launch must leave at zero: calls
+    # Split-K partials live in per-device scratch reused by every call: calls
     # with many rows, then few, then many again (and one plan replayed) must
     # each match the oracle, and replays must repeat the same bits.
     ctxs = [3000, 70, 1500, 900, 2048, 5, 700, 1300] * 4
