@@ -373,3 +373,33 @@ def test_tinyllama_shape_greedy_tokens_match_oracle(backend):
     assert mismatches <= 1
     om.close()
     gm.close()
+
+
+@pytest.mark.parametrize("H,F,hq,hkv,d,V", [(160, 224, 2, 1, 64, 1000), (96, 352, 4, 2, 64, 517)])
+def test_odd_shapes_decode_through_packed_weights(backend, H, F, hq, hkv, d, V):
+    # Decode-shaped forwards read the packed weight copies: K that does not
+    # fill a whole K slice (160, 224, 96, 352 over slices of 256) and N that
+    # does not fill a column tile (vocab 1000 and 517 over 128-column tiles)
+    # take the packer's zero padding and the kernel's partial last slice.
+    rng = np.random.default_rng(H + F)
+    spec = Spec(2, H, hq, hkv, d, F, V, max_pos=512, bias=True, tied=False,
+                num_blocks=48, block_size=16)
+    W = random_weights(spec, rng, std=0.05)
+    gm = gpu_model(backend, spec, W, oh.F32)
+    om = oracle_model(spec, W)
+    lens = [9, 30, 17]
+    tables = [list(range(16 * s, 16 * s + 16)) for s in range(3)]
+    toks = rng.integers(0, V, sum(lens))
+    pos = np.concatenate([np.arange(n) for n in lens])
+    print(f"[odd shapes] H={H} F={F} V={V}", flush=True)
+    g = gm.forward(batch(toks, pos, lens, tables)).logits
+    o = om.forward(toks, pos, lens, lens, tables)
+    assert rel_err(g, o) <= 1e-4, rel_err(g, o)
+    for step in range(3):
+        nxt = [orc.argmax(r) for r in o]
+        cur = [n + step for n in lens]
+        g = gm.forward(batch(nxt, cur, [1] * 3, tables, [c + 1 for c in cur])).logits
+        o = om.forward(nxt, cur, [1] * 3, [c + 1 for c in cur], tables)
+        assert rel_err(g, o) <= 1e-4, (step, rel_err(g, o))
+    om.close()
+    gm.close()
