@@ -1436,12 +1436,19 @@ ORION_EXPORT int orion_hip_model_forward(orion_hip_model* m, const orion_hip_bat
   }
   // Final norm on the last row of each sequence only (norm is row-wise, so
   // this equals norming all rows and then gathering), then the LM head.
-  HIP_TRY(st, launch_rmsnorm(stream, hidden, d_last, m->final_norm, S, H, d.rms_norm_eps, xn));
+  // When every row is its sequence's last row (a decode batch) and the layer
+  // GEMMs left the row sums of squares, the LM head applies the norm while
+  // staging its input, as the layer GEMMs do.
+  bool head_norm = fused && S == n && gemm_splitk_fusable(S, V, H);
+  for (int64_t i = 0; head_norm && i < S; ++i) head_norm = hb.last_rows[i] == (int32_t)i;
+  GemmFuse head_f = head_norm ? norm_in(m->final_norm) : GemmFuse{};
+  if (!head_norm)
+    HIP_TRY(st, launch_rmsnorm(stream, hidden, d_last, m->final_norm, S, H, d.rms_norm_eps, xn));
   const uint16_t* head = m->w_lm ? m->w_lm : m->w_embed;
   float* logits = m->logits.as<float>();
-  GemmFuse head_f;
   if (pack_head) head_f.w_packed = m->p_head;
-  HIP_TRY(st, gemm_on(m->dev, xn, head, nullptr, S, V, H, Epilogue::kStore, logits, &head_f));
+  HIP_TRY(st, gemm_on(m->dev, head_norm ? hidden : xn, head, nullptr, S, V, H, Epilogue::kStore,
+                      logits, &head_f));
   m->last_rows = S;
   if (argmax_out) {
     HIP_TRY(st, launch_argmax(stream, logits, S, V, m->argmax.as<int64_t>()));
