@@ -72,18 +72,21 @@ def prefill_cfg3(be, steps=20, warmup=3, head_major=False):
         be.kernel_timing(True)
         for _ in range(steps):
             call()
-        tot, cnt = be.kernel_timing_read(be.K_PREFILL)
+        samples = be.kernel_timing_samples(be.K_PREFILL)
         be.kernel_timing(False)
-        ms = tot / cnt
+        ms = float(np.median(samples))
         tf = flops / (ms * 1e-3) / 1e12
         key = "hilo" if hilo else "bf16"
-        res[key] = {"ms": round(ms, 4), "tflops": round(tf, 1),
+        res[key] = {"ms": round(ms, 4), "ms_mean": round(float(samples.mean()), 4),
+                    "launches": int(len(samples)), "tflops": round(tf, 1),
                     "frac_of_bf16_peak": round(tf / BF16_PEAK_TFLOPS, 4)}
-        if not hilo:
-            got = dout.download(np.float32, (n, case.hq * case.d))
-            rows = np.array([0, 511, 512 * 3 + 100, n - 1])
-            res[key]["max_abs_err_vs_oracle"] = float(
-                np.abs(got[rows] - case.oracle_rows(rows)).max())
+        # spot check of the timed output: the first and last row of every
+        # chunk (all 32 heads); the full-size parity test checks ~200 rows
+        got = dout.download(np.float32, (n, case.hq * case.d))
+        rows = np.array(sorted({r for c in range(case.S) for r in (512 * c, 512 * c + 511)}))
+        res[key]["max_abs_err_vs_oracle"] = float(
+            np.abs(got[rows] - case.oracle_rows(rows)).max())
+        res[key]["rows_checked"] = f"{len(rows)} of {n}"
     res["operands"] = ("bf16: Q and softmax weights rounded to bf16 (MFMA rate); hilo: each as "
                        "a hi+lo bf16 pair (2x MFMA work)")
     for b in bufs:
@@ -99,62 +102,69 @@ def algorithmic_bytes(case):
     return kv + q + out + tables
 
 
-def cpu_baseline(case, seconds_budget=30.0):
+def host_threads():
+    """(threads used, nproc): nproc = CPUs this process may run on; the oracle
+    uses at most 16 (the GPU box's CPU share for one GPU)."""
+    try:
+        nproc = len(os.sched_getaffinity(0))
+    except AttributeError:
+        nproc = os.cpu_count() or 1
+    return min(16, nproc), nproc
+
+
+def timed_median(fn, reps, budget_s):
+    """Median wall time of `fn` over `reps` calls (fewer if `budget_s` runs out)."""
+    times = []
+    t_end = time.perf_counter() + budget_s
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        fn()
+        times.append(time.perf_counter() - t0)
+        if time.perf_counter() > t_end:
+            break
+    return float(np.median(times)), len(times)
+
+
+def cpu_baseline(case):
     """The oracle (C++ restatement of the reference CPU attention) on the same
-    workload, all host threads (OpenMP over independent (row, head) pairs)."""
+    workload: all allowed host threads (OpenMP over independent (row, head)
+    pairs), and one thread (the reference's own execution model)."""
     import oracle as orc
 
-    threads = min(16, os.cpu_count() or 1)
+    threads, nproc = host_threads()
     orc.set_num_threads(threads)
     case.oracle()  # warm caches / page in
-    t0 = time.perf_counter()
-    reps = 0
-    while True:
-        case.oracle()
-        reps += 1
-        if time.perf_counter() - t0 > min(seconds_budget, 5.0) or reps >= 3:
-            break
-    dt = (time.perf_counter() - t0) / reps
-    # The reference's own execution model: one thread, one step.
+    dt, reps = timed_median(case.oracle, 20, 10.0)
     orc.set_num_threads(1)
-    t1 = time.perf_counter()
-    case.oracle()
-    dt1 = time.perf_counter() - t1
+    dt1, reps1 = timed_median(case.oracle, 20, 12.0)
     orc.set_num_threads(threads)
     return {
         "value": algorithmic_bytes(case) / dt / 1e9,
         "unit": "GB/s",
         "cores": threads,
+        "nproc": nproc,
         "kind": "port",
-        "sample": f"full config-2 step ({case.S} rows, sum ctx {int(case.ctxs.sum())}), "
-                  f"{reps} reps, {dt * 1e3:.1f} ms/step, f32 arena holding the same bf16 values",
+        "sample": f"full config-2 step ({case.S} rows, sum ctx {int(case.ctxs.sum())}), median "
+                  f"of {reps} steps, {dt * 1e3:.1f} ms/step, f32 arena holding the same bf16 "
+                  f"values",
         "single_thread": {"value": algorithmic_bytes(case) / dt1 / 1e9, "unit": "GB/s",
-                          "cores": 1, "sample": f"one full step, {dt1:.2f} s"},
+                          "cores": 1, "sample": f"median of {reps1} full steps, {dt1:.3f} s"},
     }
-
-
-TINYLLAMA = dict(L=22, H=2048, hq=32, hkv=4, d=64, F=5632, V=32000, eps=1e-5, theta=10000.0,
-                 max_pos=2048)
 
 
 def decode_e2e(steps=64, seqs=32, seed=20261204, cpu=True):
     """full decode step of a random-init TinyLlama-1.1B-shape
     model (bf16 weights N(0, 0.02), bf16 KV cache), 32 sequences with prompt
     lengths U[16, 1024] (random token ids), prefilled in one forward, then
-    `steps` greedy decode steps (device argmax).  Returns a dict of results."""
+    `steps` greedy decode steps (device argmax).  The greedy tokens are
+    compared with the CPU oracle's greedy decode of the same batch
+    (tests/golden/cfg4_greedy.npz).  Returns a dict of results."""
     import orion_hip as oh
+    from cfg4_case import TINYLLAMA, cfg4_case
 
     cfg = TINYLLAMA
-    rng = np.random.default_rng(seed)
-    lens = rng.integers(16, 1025, size=seqs)
-    bs = 16
-    need = [-(-int(n + steps) // bs) for n in lens]
-    num_blocks = int(sum(need) * 1.1) + 8
-    perm = rng.permutation(num_blocks)
-    tables, cur = [], 0
-    for nb in need:
-        tables.append(perm[cur:cur + nb].tolist())
-        cur += nb
+    case = cfg4_case(seed, seqs, steps)
+    lens, tables, num_blocks, bs = case.lens, case.tables, case.num_blocks, 16
     meta = oh.ModelMetadata(hidden_size=cfg["H"], num_layers=cfg["L"],
                             num_attention_heads=cfg["hq"], num_kv_heads=cfg["hkv"],
                             head_dim=cfg["d"], vocab_size=cfg["V"], intermediate_size=cfg["F"],
@@ -163,8 +173,7 @@ def decode_e2e(steps=64, seqs=32, seed=20261204, cpu=True):
     be = oh.HipBackend(0)
     model = oh.HipTransformerModel(meta, num_blocks, bs, be, oh.BF16)
     model.init_synthetic(seed, 0.02)
-    prompts = [rng.integers(0, cfg["V"], size=int(n)).tolist() for n in lens]
-    toks = [t for p in prompts for t in p]
+    toks = [t for p in case.prompts for t in p]
     pos = [i for n in lens for i in range(int(n))]
     t0 = time.perf_counter()
     out = model.forward(oh.ForwardBatch(toks, pos, list(range(seqs)), [int(n) for n in lens],
@@ -174,6 +183,7 @@ def decode_e2e(steps=64, seqs=32, seed=20261204, cpu=True):
     prefill_s = time.perf_counter() - t0
     last = out.argmax.tolist()
     ctx = [int(n) for n in lens]
+    generated = [last]
 
     def step():
         nonlocal last
@@ -181,6 +191,7 @@ def decode_e2e(steps=64, seqs=32, seed=20261204, cpu=True):
                             tables, False)
         o = model.forward(b, want_logits=False, want_argmax=True)
         last = o.argmax.tolist()
+        generated.append(last)
         for i in range(seqs):
             ctx[i] += 1
 
@@ -193,14 +204,23 @@ def decode_e2e(steps=64, seqs=32, seed=20261204, cpu=True):
     kv_pos_bytes = cfg["L"] * 2 * cfg["hkv"] * cfg["d"] * 2
     kv_read = sum(sum(c + k + 1 for c in ctx) for k in range(n_steps)) * kv_pos_bytes
     kv_write = n_steps * seqs * kv_pos_bytes
+    # every step ends in a device-to-host copy of its tokens (a full sync), so
+    # each step is timed on its own; tokens/s uses the median step
+    per_step = []
     t0 = time.perf_counter()
     for _ in range(n_steps):
+        t1 = time.perf_counter()
         step()
+        per_step.append(time.perf_counter() - t1)
     be.synchronize()
     dt = time.perf_counter() - t0
+    med = float(np.median(per_step))
     res = {
-        "decode_tokens_per_s": round(seqs * n_steps / dt, 1),
-        "decode_ms_per_step": round(dt / n_steps * 1e3, 4),
+        "decode_tokens_per_s": round(seqs / med, 1),
+        "decode_ms_per_step": round(med * 1e3, 4),
+        "step_ms_mean": round(dt / n_steps * 1e3, 4),
+        "step_ms_min_max": [round(min(per_step) * 1e3, 4), round(max(per_step) * 1e3, 4)],
+        "timed_steps": n_steps,
         "prefill_tokens": int(sum(lens)),
         "prefill_s": round(prefill_s, 3),
         "workload": "TinyLlama-1.1B shape (22L, hidden 2048, 32q/4kv, d 64, ffn 5632, vocab "
@@ -213,12 +233,37 @@ def decode_e2e(steps=64, seqs=32, seed=20261204, cpu=True):
     res["hbm_bytes_per_step"] = int(res["weight_bytes_per_step"] + (kv_read + kv_write) / n_steps)
     res["frac_of_hbm_roofline"] = round(
         res["hbm_bytes_per_step"] / (res["decode_ms_per_step"] * 1e-3) / HBM_PEAK_GBS / 1e9, 4)
+    res["greedy_vs_oracle"] = greedy_vs_golden(generated, steps, seqs)
     model.close()
     be.close()
     if cpu:
         res["cpu_baseline"] = cpu_decode_step(cfg, lens, tables, num_blocks, seqs)
         res["speedup_vs_cpu"] = round(res["decode_tokens_per_s"] / res["cpu_baseline"]["value"], 1)
     return res
+
+
+def greedy_vs_golden(generated, steps, seqs):
+    """The bench's free-running greedy tokens against the CPU oracle's greedy
+    decode of the same batch with the same KV dtype
+    (tests/golden/cfg4_greedy_bf16kv.npz: K/V rounded to bf16 when written):
+    per sequence, the tokens that agree up to the first difference (after
+    one, the two sequences continue from different inputs)."""
+    path = os.path.join(ROOT, "tests", "golden", "cfg4_greedy_bf16kv.npz")
+    if not os.path.exists(path):
+        return None
+    gold = np.load(path)["tokens"]
+    got = np.asarray(generated, np.int64)
+    if got.shape != gold.shape:
+        return {"error": f"shape {got.shape} against golden {gold.shape}"}
+    agree = got == gold
+    prefix = [int(np.argmin(agree[:, s])) if not agree[:, s].all() else steps + 1
+              for s in range(seqs)]
+    return {"tokens_compared": int(gold.size), "tokens_matched": int(sum(prefix)),
+            "sequences_identical": int(sum(p == steps + 1 for p in prefix)),
+            "first_difference_steps": [p for p in prefix if p <= steps],
+            "note": "bf16 KV on both sides (the oracle rounds each K/V element to bf16 "
+                    "when written); matched = tokens up to each sequence's first "
+                    "difference"}
 
 
 def gemm_shapes(reps=5):
@@ -421,7 +466,7 @@ def cpu_decode_step(cfg, lens, tables, num_blocks, seqs):
     whatever it holds (timing does not depend on it)."""
     import oracle as orc
 
-    threads = min(16, os.cpu_count() or 1)
+    threads, nproc = host_threads()
     orc.set_num_threads(threads)
     m = orc.OracleTransformer(cfg["L"], cfg["H"], cfg["hq"], cfg["hkv"], cfg["d"], cfg["F"],
                               cfg["V"], cfg["max_pos"], cfg["eps"], cfg["theta"], False, False,
@@ -440,22 +485,20 @@ def cpu_decode_step(cfg, lens, tables, num_blocks, seqs):
             m.set_weight(wid, l, c(n))
     pos = [int(n) for n in lens]
     step = lambda: m.forward([1] * seqs, pos, [1] * seqs, [p + 1 for p in pos], tables)
-    t0 = time.perf_counter()
-    step()
-    dt = time.perf_counter() - t0
-    # The reference's own execution model (single-threaded): a bounded sample,
-    # one decode step at one thread.
+    step()  # warm-up (page in the weights)
+    dt, reps = timed_median(step, 20, 12.0)
+    # The reference's own execution model (single-threaded): a bounded sample.
     orc.set_num_threads(1)
-    t1 = time.perf_counter()
-    step()
-    dt1 = time.perf_counter() - t1
+    dt1, reps1 = timed_median(step, 5, 12.0)
     orc.set_num_threads(threads)
     m.close()
-    return {"value": round(seqs / dt, 3), "unit": "tokens/s", "cores": threads, "kind": "port",
-            "sample": f"one decode step of the same model shape and batch ({seqs} rows), "
-                      f"{dt:.2f} s/step, constant weights, OpenMP over independent outputs",
+    return {"value": round(seqs / dt, 3), "unit": "tokens/s", "cores": threads, "nproc": nproc,
+            "kind": "port",
+            "sample": f"decode steps of the same model shape and batch ({seqs} rows, same "
+                      f"positions each time), median of {reps}, {dt:.3f} s/step, constant "
+                      f"weights, OpenMP over independent outputs",
             "single_thread": {"value": round(seqs / dt1, 3), "unit": "tokens/s", "cores": 1,
-                              "sample": f"one decode step, {dt1:.2f} s"}}
+                              "sample": f"median of {reps1} decode steps, {dt1:.2f} s"}}
 
 
 def main():
@@ -514,13 +557,24 @@ def main():
     # The dominant kernel alone (split-K pass; the merge kernel is separate),
     # HIP events on the library's stream around each launch.
     be.kernel_timing(True)
-    for _ in range(a.steps):
+    for _ in range(max(a.steps, 20)):
         step()
     split_ms, split_n = be.kernel_timing_read(be.K_DECODE_SPLIT)
     merge_ms, merge_n = be.kernel_timing_read(be.K_DECODE_MERGE)
+    split_samples = be.kernel_timing_samples(be.K_DECODE_SPLIT)
+    merge_samples = be.kernel_timing_samples(be.K_DECODE_MERGE)
     be.kernel_timing(False)
     split_avg = split_ms / max(split_n, 1)
     merge_avg = merge_ms / max(merge_n, 1)
+    # Whole steps one at a time (events around each), for the median.
+    step_samples = []
+    for _ in range(max(a.steps, 20)):
+        be.timer_start()
+        step()
+        step_samples.append(be.timer_stop())
+    be.synchronize()
+    step_med = float(np.median(step_samples))
+    split_med = float(np.median(split_samples)) if len(split_samples) else split_avg
 
     # correctness spot-check of the measured output (cheap: 4 rows)
     got = dout.download(np.float32, (case.S, case.hq * case.d))
@@ -565,8 +619,14 @@ def main():
             "frac": round(kern_gbs / HBM_PEAK_GBS, 4),
             "traffic": measured_traffic(),
             "kernel_ms": round(split_avg, 5),
+            "kernel_ms_median": round(split_med, 5),
+            "kernel_launches_timed": int(split_n),
             "merge_kernel_ms": round(merge_avg, 5),
+            "merge_kernel_ms_median": round(float(np.median(merge_samples)), 5)
+            if len(merge_samples) else None,
         },
+        "step_ms_median": round(step_med, 5),
+        "value_at_step_median": round(nbytes / (step_med * 1e-3) / 1e9, 1),
         "max_abs_err_vs_oracle": max_err,
     }
     if not a.no_cpu:

@@ -109,6 +109,11 @@ int orion_hip_timer_stop(orion_hip_device* dev, float* ms);
 int orion_hip_kernel_timing(orion_hip_device* dev, int enable);
 int orion_hip_kernel_timing_read(orion_hip_device* dev, int kernel, double* total_ms,
                                  int64_t* calls);
+/* The same events one launch at a time: up to `capacity` per-launch durations
+ * (ms, in launch order) into ms_out, and the number of recorded launches in
+ * *calls (for medians). */
+int orion_hip_kernel_timing_samples(orion_hip_device* dev, int kernel, float* ms_out,
+                                    int64_t capacity, int64_t* calls);
 
 /* ---------------------------------------------------------------------------
  * LanguageModel (traits.rs:297-309) over TransformerModel

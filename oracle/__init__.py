@@ -98,6 +98,8 @@ def lib() -> C.CDLL:
         "oracle_model_kv": ([vp, C.POINTER(i64)], C.POINTER(C.c_float)),
         "oracle_model_set_weight": ([vp, C.c_int, C.c_int, vp, i64], C.c_int),
         "oracle_model_forward": ([vp, i64, i64, vp, vp, vp, vp, vp, vp, vp], C.c_int),
+        "oracle_model_set_kv_bf16": ([vp, C.c_int], None),
+        "oracle_synthetic_fill": ([C.c_uint64, C.c_int, C.c_int, f32, i64, vp], None),
     }
     for name, (args, res) in sig.items():
         fn = getattr(L, name)
@@ -114,6 +116,14 @@ def _check(rc: int) -> None:
 
 def _f32(a) -> np.ndarray:
     return np.ascontiguousarray(a, dtype=np.float32)
+
+
+def synthetic_weight(seed: int, which: int, layer: int, count: int, std: float = 0.02):
+    """The HIP library's synthetic weight values (a test input generator restated in
+    the oracle, not a reference function): f32, bf16-exact, logical row-major order."""
+    out = np.empty(count, np.float32)
+    lib().oracle_synthetic_fill(seed, which, layer, std, count, out.ctypes.data)
+    return out
 
 
 def set_num_threads(n: int) -> None:
@@ -328,17 +338,20 @@ def validate(expected, actual, tol: Tolerance):
 
 
 class OracleTransformer:
-    """TransformerModel (transformer.rs:137-443) with an f32 KV arena."""
+    """TransformerModel (transformer.rs:137-443) with an f32 KV arena (the
+    reference's), or with every K/V element rounded to bf16 when written
+    (kv_bf16=True: the KV dtype of BASELINE's bf16 configurations)."""
 
     def __init__(self, num_layers, hidden, num_q_heads, num_kv_heads, head_dim, ffn, vocab,
                  max_positions, rms_norm_eps, rope_theta, has_qkv_bias, tied_lm_head, num_blocks,
-                 block_size):
+                 block_size, kv_bf16=False):
         self.desc = OracleModelDesc(num_layers, hidden, num_q_heads, num_kv_heads, head_dim, ffn,
                                     vocab, max_positions, rms_norm_eps, rope_theta,
                                     int(has_qkv_bias), int(tied_lm_head), num_blocks, block_size)
         self.h = lib().oracle_model_create(C.byref(self.desc))
         if not self.h:
             raise OracleError(lib().oracle_last_error().decode())
+        lib().oracle_model_set_kv_bf16(self.h, int(kv_bf16))
 
     def set_weight(self, which, layer, data) -> None:
         d = _f32(data).ravel()

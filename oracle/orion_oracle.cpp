@@ -79,8 +79,13 @@ ORACLE_API void oracle_set_num_threads(int n) {
 
 // tensor.rs:96-130 `linear`: out[i][j] = (sum_k x[i][k]*W[j][k]) + (b[j] or 0.0),
 // sequential f32 accumulation starting from 0.0, W is [out_features, in_features].
-// Four rows are computed together purely for instruction-level parallelism;
-// each accumulator still sees the reference's exact operation sequence.
+// Rows are computed in blocks of 16, each block against 2 weight rows at a
+// time, with the 16 row accumulators held in 4-wide vector registers: this is
+// only data parallelism across independent outputs.  Each accumulator still
+// sees the reference's exact operation sequence (acc = acc + x*w, rounded
+// after the multiply and after the add, k ascending, starting from 0.0).
+typedef float orc_v4 __attribute__((vector_size(16)));
+
 ORACLE_API int oracle_linear(const float* x, int64_t n, int64_t k, const float* w,
                              int64_t out_features, int64_t in_features,
                              const float* bias, int64_t bias_len, float* out) {
@@ -90,36 +95,53 @@ ORACLE_API int oracle_linear(const float* x, int64_t n, int64_t k, const float* 
   if (bias && bias_len != out_features)
     return fail("bias has " + std::to_string(bias_len) + " elements, expected " +
                 std::to_string(out_features));
-  const int64_t n4 = (n + 3) / 4;
+  constexpr int64_t R = 16;
+  const int64_t nb = (n + R - 1) / R;
+  // x transposed per 16-row block, [block][t][16], zero rows past n
+  std::vector<orc_v4> xt((size_t)nb * k * (R / 4));
+#pragma omp parallel for schedule(static)
+  for (int64_t b = 0; b < nb; ++b) {
+    float* dst = reinterpret_cast<float*>(xt.data() + (size_t)b * k * (R / 4));
+    for (int64_t r = 0; r < R; ++r) {
+      const int64_t i = b * R + r;
+      for (int64_t t = 0; t < k; ++t) dst[t * R + r] = i < n ? x[i * k + t] : 0.0f;
+    }
+  }
+  const int64_t jb = (out_features + 1) / 2;
 #pragma omp parallel for collapse(2) schedule(static)
-  for (int64_t ib = 0; ib < n4; ++ib) {
-    for (int64_t j = 0; j < out_features; ++j) {
-      const float* wr = w + j * in_features;
-      const int64_t i0 = ib * 4;
-      const int64_t cnt = (n - i0) < 4 ? (n - i0) : 4;
-      float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-      if (cnt == 4) {
-        const float* x0 = x + (i0 + 0) * k;
-        const float* x1 = x + (i0 + 1) * k;
-        const float* x2 = x + (i0 + 2) * k;
-        const float* x3 = x + (i0 + 3) * k;
-        for (int64_t t = 0; t < k; ++t) {
-          const float b = wr[t];
-          acc[0] += x0[t] * b;
-          acc[1] += x1[t] * b;
-          acc[2] += x2[t] * b;
-          acc[3] += x3[t] * b;
-        }
-      } else {
-        for (int64_t r = 0; r < cnt; ++r) {
-          const float* xr = x + (i0 + r) * k;
-          float a = 0.0f;
-          for (int64_t t = 0; t < k; ++t) a += xr[t] * wr[t];
-          acc[r] = a;
-        }
+  for (int64_t b = 0; b < nb; ++b) {
+    for (int64_t jj = 0; jj < jb; ++jj) {
+      const int64_t j0 = jj * 2;
+      const bool two = j0 + 1 < out_features;
+      const float* w0 = w + j0 * in_features;
+      const float* w1 = two ? w0 + in_features : w0;
+      const orc_v4* xb = xt.data() + (size_t)b * k * (R / 4);
+      orc_v4 a0 = {0, 0, 0, 0}, a1 = a0, a2 = a0, a3 = a0;
+      orc_v4 c0 = a0, c1 = a0, c2 = a0, c3 = a0;
+      for (int64_t t = 0; t < k; ++t) {
+        const orc_v4* xv = xb + t * 4;
+        const float s0 = w0[t], s1 = w1[t];
+        const orc_v4 v0 = {s0, s0, s0, s0}, v1 = {s1, s1, s1, s1};
+        a0 = a0 + xv[0] * v0;
+        a1 = a1 + xv[1] * v0;
+        a2 = a2 + xv[2] * v0;
+        a3 = a3 + xv[3] * v0;
+        c0 = c0 + xv[0] * v1;
+        c1 = c1 + xv[1] * v1;
+        c2 = c2 + xv[2] * v1;
+        c3 = c3 + xv[3] * v1;
       }
-      const float bj = bias ? bias[j] : 0.0f;
-      for (int64_t r = 0; r < cnt; ++r) out[(i0 + r) * out_features + j] = acc[r] + bj;
+      float ra[R], rc[R];
+      __builtin_memcpy(ra, &a0, 16); __builtin_memcpy(ra + 4, &a1, 16);
+      __builtin_memcpy(ra + 8, &a2, 16); __builtin_memcpy(ra + 12, &a3, 16);
+      __builtin_memcpy(rc, &c0, 16); __builtin_memcpy(rc + 4, &c1, 16);
+      __builtin_memcpy(rc + 8, &c2, 16); __builtin_memcpy(rc + 12, &c3, 16);
+      for (int64_t r = 0; r < R; ++r) {
+        const int64_t i = b * R + r;
+        if (i >= n) break;
+        out[i * out_features + j0] = ra[r] + (bias ? bias[j0] : 0.0f);
+        if (two) out[i * out_features + j0 + 1] = rc[r] + (bias ? bias[j0 + 1] : 0.0f);
+      }
     }
   }
   return 0;
@@ -634,6 +656,9 @@ struct OracleModel {
   std::vector<float> rope_cos, rope_sin;
   std::vector<float> kv;
   KvDims dims;
+  // Store K/V rounded to bf16 (nearest even), the KV dtype of BASELINE's
+  // bf16 configurations; the reference's own KvStore is f32 (false).
+  bool kv_bf16 = false;
 };
 
 ORACLE_API void* oracle_model_create(const OracleModelDesc* d) {
@@ -661,6 +686,14 @@ ORACLE_API void* oracle_model_create(const OracleModelDesc* d) {
 }
 
 ORACLE_API void oracle_model_destroy(void* p) { delete static_cast<OracleModel*>(p); }
+
+static float bf16_round_f32(float f);
+
+// The arena's element type: 0 = f32 (KvStore, attention.rs:34-62), 1 = bf16
+// values (each K/V element rounded to bf16, nearest even, when written).
+ORACLE_API void oracle_model_set_kv_bf16(void* p, int on) {
+  static_cast<OracleModel*>(p)->kv_bf16 = on != 0;
+}
 
 ORACLE_API float* oracle_model_kv(void* p, int64_t* len) {
   auto* m = static_cast<OracleModel*>(p);
@@ -749,6 +782,10 @@ static int oracle_layer_forward(OracleModel* m, int64_t layer, std::vector<float
       if (oracle_apply_rope(k.data() + row * kvd + h * hd, hd, c, s, half)) return 1;
   }
   // :283-297 write every row's K and V before any attention
+  if (m->kv_bf16) {
+    for (float& x : k) x = bf16_round_f32(x);
+    for (float& x : v) x = bf16_round_f32(x);
+  }
   for (int64_t row = 0; row < n; ++row) {
     for (int64_t h = 0; h < hkv; ++h) {
       if (oracle_kv_write(m->kv.data(), d.num_layers, d.num_blocks, d.block_size, hkv, hd, layer,
@@ -843,4 +880,60 @@ ORACLE_API int oracle_model_forward(void* p, int64_t n, int64_t S, const uint32_
   const std::vector<float>& head =
       (d.tied_lm_head || m->lm_head.empty()) ? m->embed : m->lm_head;
   return oracle_linear(tail.data(), S, H, head.data(), d.vocab, H, nullptr, 0, logits);
+}
+
+// ---------------------------------------------------------------------------
+// Synthetic weights (test input generator, not a reference function)
+// ---------------------------------------------------------------------------
+
+// The HIP library's counter-based synthetic weights (orion_hip_synthetic_value
+// / orion_hip_model_init_synthetic), restated so the oracle can hold the same
+// model the bench runs without a GPU: splitmix64 of a per-tensor key plus the
+// element index, the sum of the hash's four 16-bit fields (Irwin-Hall, mean
+// 131070, sd 65536/sqrt(3)) centred and scaled by std / sd in f32, rounded to
+// bf16 (nearest even) and widened back.  Norm weights are ones.  Checked
+// element-wise against the library's host entry point and a numpy restatement
+// (tests/test_cfg4_golden.py).
+namespace {
+uint64_t syn_mix(uint64_t x) {
+  x += 0x9E3779B97F4A7C15ull;
+  x = (x ^ (x >> 30)) * 0xBF58476D1CE4E5B9ull;
+  x = (x ^ (x >> 27)) * 0x94D049BB133111EBull;
+  return x ^ (x >> 31);
+}
+}  // namespace
+
+// f32 -> bf16 (nearest even; NaN stays NaN) -> f32.
+static float bf16_round_f32(float f) {
+  uint32_t u;
+  std::memcpy(&u, &f, 4);
+  if ((u & 0x7f800000u) == 0x7f800000u && (u & 0x007fffffu)) {
+    u = ((u >> 16) | 0x40u) << 16;
+  } else {
+    u += 0x7fffu + ((u >> 16) & 1u);
+    u &= 0xffff0000u;
+  }
+  float r;
+  std::memcpy(&r, &u, 4);
+  return r;
+}
+
+ORACLE_API void oracle_synthetic_fill(uint64_t seed, int which, int layer, float std_,
+                                      int64_t count, float* out) {
+  const bool is_norm = which == 1 || which == 3 || which == 11;  // final, input, post norm
+  if (is_norm) {
+    for (int64_t i = 0; i < count; ++i) out[i] = 1.0f;
+    return;
+  }
+  const int lay = which >= 3 ? layer : -1;
+  const uint64_t key =
+      syn_mix(seed ^ ((uint64_t)(which + 1) << 48) ^ ((uint64_t)(lay + 1) << 24));
+  const float mul = std_ / 37837.2265625f;
+#pragma omp parallel for schedule(static)
+  for (int64_t i = 0; i < count; ++i) {
+    const uint64_t h = syn_mix(key + (uint64_t)i);
+    const int32_t s = (int32_t)(h & 0xffff) + (int32_t)((h >> 16) & 0xffff) +
+                      (int32_t)((h >> 32) & 0xffff) + (int32_t)(h >> 48);
+    out[i] = bf16_round_f32((float)(s - 131070) * mul);
+  }
 }

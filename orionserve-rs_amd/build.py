@@ -56,11 +56,33 @@ def build(jobs=None):
     jobs = jobs or min(len(SOURCES), os.cpu_count() or 4)
     with ThreadPoolExecutor(max_workers=jobs) as ex:
         objs = list(ex.map(_compile, SOURCES))
-    cmd = [HIPCC, "--offload-arch=gfx950", "-shared", "-fPIC", "-o", LIB] + objs
+    # link beside the library, then rename over it: a process that still
+    # maps the previous build keeps its (unlinked) copy intact
+    tmp = LIB + ".tmp"
+    cmd = [HIPCC, "--offload-arch=gfx950", "-shared", "-fPIC", "-o", tmp] + objs
     p = subprocess.run(cmd, capture_output=True, text=True)
     if p.returncode != 0:
         raise RuntimeError(f"link failed:\n{p.stderr}")
+    os.replace(tmp, LIB)
+    build_abi_check()
     return LIB
+
+
+ROOT = os.path.dirname(HERE)
+ABI_CHECK_SRC = os.path.join(ROOT, "tests", "abi", "abi_check.cpp")
+ABI_CHECK = os.path.join(ROOT, "tests", "abi", "abi_check")
+
+
+def build_abi_check():
+    """The C++ program that calls the C-ABI as a foreign caller would
+    (tests/abi/abi_check.cpp): host code only, linked against the library."""
+    tmp = ABI_CHECK + ".tmp"
+    cmd = ["g++", "-std=c++17", "-O1", "-Wall", "-Wextra", ABI_CHECK_SRC, "-o", tmp,
+           "-L" + HERE, "-lorion_hip", "-Wl,-rpath,$ORIGIN/../../orionserve-rs_amd"]
+    p = subprocess.run(cmd, capture_output=True, text=True)
+    if p.returncode != 0:
+        raise RuntimeError(f"abi_check build failed:\n{p.stderr}")
+    os.replace(tmp, ABI_CHECK)
 
 
 if __name__ == "__main__":

@@ -618,6 +618,155 @@ __global__ void __launch_bounds__(256)
 }
 
 // ---------------------------------------------------------------------------
+// Any head_dim and GQA group (the shapes the kernels above do not cover)
+// ---------------------------------------------------------------------------
+
+// paged_attention (attention.rs:219-295) accepts any even head_dim and any
+// grouping of query heads over KV heads.  This wave covers what the MFMA and
+// per-dtype VALU waves do not: head_dim even and at most 256, any group size.
+// One wave per work item (row, KV head, chunk).  Lane l holds dimensions
+// {2l, 2l+1} and {128+2l, 128+2l+1} of every vector; a 16-token step loads
+// the 16 keys, reduces each score over the wave, and updates the online
+// softmax (max, sum, output) of one query head.  The G query heads of the
+// item run one after another over the same chunk, so heads after the first
+// re-read its K/V from the caches.  Partial results use the same split
+// layout as the other waves.
+template <typename T>
+__device__ inline float2 load_pair(const T* p, bool valid);
+template <>
+__device__ inline float2 load_pair<float>(const float* p, bool valid) {
+  return valid ? *reinterpret_cast<const float2*>(p) : make_float2(0.f, 0.f);
+}
+template <>
+__device__ inline float2 load_pair<uint16_t>(const uint16_t* p, bool valid) {
+  const uint32_t v = valid ? *reinterpret_cast<const uint32_t*>(p) : 0u;
+  return make_float2(bf16lo(v), bf16hi(v));
+}
+
+template <typename T>
+__global__ void __launch_bounds__(256)
+    paged_decode_any_kernel(const T* __restrict__ kv_layer, int64_t blk_stride, int64_t v_off,
+                            int64_t slot_stride, int64_t head_stride, int bs_log2,
+                            int num_kv_heads, int num_q_heads, int D,
+                            const DecodeWork* __restrict__ work, int num_work,
+                            const float* __restrict__ q, const uint32_t* __restrict__ bt_ids,
+                            int chunk, int max_splits, float scale, float* __restrict__ out,
+                            float* __restrict__ ws_o, float* __restrict__ ws_ml) {
+  const int w = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (w >= num_work) return;
+  const DecodeWork wk = work[w];
+  const int row = wk.item / num_kv_heads, kvh = wk.item - row * num_kv_heads;
+  const int G = num_q_heads / num_kv_heads;
+  const int lane = threadIdx.x & 63;
+  const int d0 = 2 * lane, d1 = 128 + 2 * lane;
+  const bool has0 = d0 < D, has1 = d1 < D;
+  const int start = wk.start, end = wk.end;
+  const int split = start / chunk;
+  const int bs_mask = (1 << bs_log2) - 1;
+  const int first_blk = start >> bs_log2;
+  const int nblk = ((end - 1) >> bs_log2) - first_blk + 1;
+  const uint32_t* tbl = bt_ids + wk.tbl_off;
+  const int my_blk = lane < nblk ? (int)tbl[lane] : 0;
+  const T* kbase = kv_layer + (int64_t)kvh * head_stride;
+  for (int g = 0; g < G; ++g) {
+    const int64_t head = (int64_t)row * num_q_heads + (int64_t)kvh * G + g;
+    const float* qp = q + head * D;
+    const float2 q0 = has0 ? *reinterpret_cast<const float2*>(qp + d0) : make_float2(0.f, 0.f);
+    const float2 q1 = has1 ? *reinterpret_cast<const float2*>(qp + d1) : make_float2(0.f, 0.f);
+    float m = -INFINITY, l = 0.f;
+    float o[4] = {0.f, 0.f, 0.f, 0.f};
+    for (int base = start; base < end; base += 16) {
+      float s[16];
+      int64_t off[16];
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int j = base + r;
+        const bool valid = j < end;
+        const int blk = __shfl(my_blk, valid ? (j >> bs_log2) - first_blk : 0);
+        off[r] = (int64_t)blk * blk_stride + (int64_t)(j & bs_mask) * slot_stride;
+        const float2 k0 = load_pair<T>(kbase + off[r] + d0, valid && has0);
+        const float2 k1 = load_pair<T>(kbase + off[r] + d1, valid && has1);
+        const float part = q0.x * k0.x + q0.y * k0.y + q1.x * k1.x + q1.y * k1.y;
+        const float dot = wave_sum(part);
+        s[r] = valid ? dot * scale : -INFINITY;
+      }
+      float mx = -INFINITY;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s[r]);
+      const float m_new = fmaxf(m, mx);
+      const float alpha = __expf(m - m_new);
+      float psum = 0.f;
+      float acc[4] = {o[0] * alpha, o[1] * alpha, o[2] * alpha, o[3] * alpha};
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const bool valid = base + r < end;
+        const float p = valid ? __expf(s[r] - m_new) : 0.f;
+        psum += p;
+        const float2 v0 = load_pair<T>(kbase + off[r] + v_off + d0, valid && has0);
+        const float2 v1 = load_pair<T>(kbase + off[r] + v_off + d1, valid && has1);
+        acc[0] += p * v0.x;
+        acc[1] += p * v0.y;
+        acc[2] += p * v1.x;
+        acc[3] += p * v1.y;
+      }
+      l = l * alpha + psum;
+      m = m_new;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) o[e] = acc[e];
+    }
+    if (wk.nsplit == 1) {
+      const float inv = 1.f / l;
+      float* op = out + head * D;
+      if (has0) *reinterpret_cast<float2*>(op + d0) = make_float2(o[0] * inv, o[1] * inv);
+      if (has1) *reinterpret_cast<float2*>(op + d1) = make_float2(o[2] * inv, o[3] * inv);
+    } else {
+      const int64_t slot = head * max_splits + split;
+      float* op = ws_o + slot * D;
+      if (has0) *reinterpret_cast<float2*>(op + d0) = make_float2(o[0], o[1]);
+      if (has1) *reinterpret_cast<float2*>(op + d1) = make_float2(o[2], o[3]);
+      if (lane == 0) *reinterpret_cast<float2*>(ws_ml + slot * 2) = make_float2(m, l);
+    }
+  }
+}
+
+// Merges the split partials for any head_dim (even, <= 256): one wave per
+// (row, query head), splits in order, lane l holding dimensions l + 64 i.
+__global__ void __launch_bounds__(256)
+    paged_decode_combine_any_kernel(int num_rows, int num_q_heads, int D,
+                                    const uint32_t* __restrict__ positions,
+                                    const int32_t* __restrict__ row_list, int partition,
+                                    int max_splits, const float* __restrict__ ws_o,
+                                    const float* __restrict__ ws_ml, float* __restrict__ out) {
+  const int lane = threadIdx.x & 63;
+  const int64_t slot = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (slot >= (int64_t)num_rows * num_q_heads) return;
+  const int li = (int)(slot / num_q_heads);
+  const int row = row_list ? row_list[li] : li;
+  const int64_t item = (int64_t)row * num_q_heads + (slot - (int64_t)li * num_q_heads);
+  const int len = (int)positions[row] + 1;
+  const int nsplit = (len + partition - 1) / partition;
+  if (nsplit <= 1) return;
+  const float* ml = ws_ml + item * max_splits * 2;
+  const float* ob = ws_o + item * max_splits * D;
+  float mx = -INFINITY;
+  for (int s = lane; s < nsplit; s += 64) mx = fmaxf(mx, ml[2 * s]);
+  mx = wave_max(mx);
+  float ls = 0.f;
+  for (int s = lane; s < nsplit; s += 64) ls += __expf(ml[2 * s] - mx) * ml[2 * s + 1];
+  const float inv = 1.f / wave_sum(ls);
+  float acc[4] = {0.f, 0.f, 0.f, 0.f};
+  for (int s = 0; s < nsplit; ++s) {
+    const float wj = __expf(ml[2 * s] - mx);
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      if (lane + 64 * i < D) acc[i] += wj * ob[(int64_t)s * D + lane + 64 * i];
+  }
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+    if (lane + 64 * i < D) out[item * D + lane + 64 * i] = acc[i] * inv;
+}
+
+// ---------------------------------------------------------------------------
 // Host side: decode plans and launch
 // ---------------------------------------------------------------------------
 
@@ -821,7 +970,10 @@ static hipError_t launch_combine(hipStream_t st, int64_t D, int64_t rows, int64_
   const int64_t nr = plan.rows ? plan.num_rows : rows;
   if (nr == 0) return hipSuccess;
   dim3 cgrid((unsigned)((nr * hq + 3) / 4));
-  if (D == 128)
+  if (D != 64 && D != 128)
+    hipLaunchKernelGGL(paged_decode_combine_any_kernel, cgrid, dim3(256), 0, st, (int)nr,
+                       (int)hq, (int)D, positions, plan.rows, C, ms, ws_o, ws_ml, out);
+  else if (D == 128)
     hipLaunchKernelGGL(paged_decode_combine_kernel<128>, cgrid, dim3(256), 0, st, (int)nr,
                        (int)hq, positions, plan.rows, C, ms, ws_o, ws_ml, out);
   else
@@ -854,7 +1006,20 @@ hipError_t launch_paged_decode(hipStream_t st, const KvGeom& kv, const void* are
   const float scale = 1.0f / sqrtf((float)D);
   const dim3 grid((unsigned)((plan.num_work + 3) / 4));
   hipError_t e;
-  if (kv.dtype_bf16) {
+  if ((D != 64 && D != 128) || G > 8) {
+    if (D > 256 || (D & 1)) return hipErrorInvalidValue;
+    if (kv.dtype_bf16)
+      hipLaunchKernelGGL(paged_decode_any_kernel<uint16_t>, grid, dim3(256), 0, st,
+                         static_cast<const uint16_t*>(arena) + layer * a.layer, a.blk, a.v_off,
+                         a.slot, a.head, bs_log2, (int)hkv, (int)hq, (int)D, plan.work,
+                         plan.num_work, q, bt_ids, C, ms, scale, out, ws_o, ws_ml);
+    else
+      hipLaunchKernelGGL(paged_decode_any_kernel<float>, grid, dim3(256), 0, st,
+                         static_cast<const float*>(arena) + layer * a.layer, a.blk, a.v_off,
+                         a.slot, a.head, bs_log2, (int)hkv, (int)hq, (int)D, plan.work,
+                         plan.num_work, q, bt_ids, C, ms, scale, out, ws_o, ws_ml);
+    e = hipGetLastError();
+  } else if (kv.dtype_bf16) {
     if (a.layer > (int64_t)UINT32_MAX) return hipErrorInvalidValue;
     const uint16_t* base = static_cast<const uint16_t*>(arena) + layer * a.layer;
     const bool big = kv.block_size >= 16;

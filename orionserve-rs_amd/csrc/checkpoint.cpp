@@ -276,7 +276,9 @@ std::string parse_header(const char* base, size_t size,
         }
         if (offs[0] < 0 || offs[1] < offs[0] || (uint64_t)offs[1] > data_size)
           return "tensor `" + key + "` data_offsets fall outside the file";
-        if ((uint64_t)(offs[1] - offs[0]) != (uint64_t)count * elem)
+        // count * elem computed only once it cannot wrap (count <= data_size)
+        if ((uint64_t)count > data_size / elem ||
+            (uint64_t)(offs[1] - offs[0]) != (uint64_t)count * elem)
           return "tensor `" + key + "` data_offsets do not match its shape and dtype";
         t.data = data + offs[0];
         t.bytes = (size_t)(offs[1] - offs[0]);

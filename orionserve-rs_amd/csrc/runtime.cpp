@@ -418,6 +418,21 @@ ORION_EXPORT int orion_hip_kernel_timing_read(orion_hip_device* dev, int kernel,
   return ORION_HIP_OK;
 }
 
+ORION_EXPORT int orion_hip_kernel_timing_samples(orion_hip_device* dev, int kernel, float* ms_out,
+                                                 int64_t capacity, int64_t* calls) {
+  const char* st = "kernel_timing";
+  if (kernel < 0 || kernel > 2) return internal(st, "kernel index %d is not 0, 1 or 2", kernel);
+  int64_t i = 0;
+  for (auto& p : dev->kevents[kernel]) {
+    if (i >= capacity) break;
+    HIP_TRY(st, hipEventSynchronize(p.second));
+    HIP_TRY(st, hipEventElapsedTime(&ms_out[i], p.first, p.second));
+    ++i;
+  }
+  *calls = (int64_t)dev->kevents[kernel].size();
+  return ORION_HIP_OK;
+}
+
 // Records a (start, stop) event pair for kernel index k around `launch` when
 // per-kernel timing is on.
 template <typename F>
@@ -475,11 +490,12 @@ static int check_desc(const orion_hip_model_desc* d) {
                     d->num_attention_heads, d->num_kv_heads);
   if (d->block_size < 4 || d->block_size > 256 || (d->block_size & (d->block_size - 1)))
     return internal(st, "block_size must be a power of two in [4, 256], got %d", d->block_size);
-  if (d->head_dim != 64 && d->head_dim != 128)
-    return set_err(ORION_HIP_ERR_BACKEND, st, "head_dim %d unsupported (64 or 128)", d->head_dim);
-  if (d->num_attention_heads / d->num_kv_heads > 8)
-    return set_err(ORION_HIP_ERR_BACKEND, st, "GQA group %d unsupported (at most 8)",
-                   d->num_attention_heads / d->num_kv_heads);
+  // RoPE rotates halves (tensor.rs:283-298), so head_dim is even; the
+  // attention kernels cover every even head_dim up to 256 and any grouping
+  // (MFMA for 64 and 128 with groups up to 8, a general wave otherwise).
+  if (d->head_dim % 2 || d->head_dim > 256)
+    return set_err(ORION_HIP_ERR_BACKEND, st, "head_dim %d unsupported (even, at most 256)",
+                   d->head_dim);
   if (d->hidden_size % 32 || d->intermediate_size % 32 ||
       (d->num_attention_heads * d->head_dim) % 32)
     return set_err(ORION_HIP_ERR_BACKEND, st,
@@ -1246,11 +1262,10 @@ ORION_EXPORT int orion_hip_model_forward(orion_hip_model* m, const orion_hip_bat
   // Decode-shaped batches run the layer with the split-K GEMM fusions: each
   // residual-add GEMM also writes the per-row sums of squares, the next GEMM
   // applies the RMSNorm to its input, and the QKV partials go straight into
-  // RoPE + cache write.  ORION_GEMM_FUSE=0 runs the separate launches.
-  static const bool allow_fuse = [] {
-    const char* v = getenv("ORION_GEMM_FUSE");
-    return !(v && v[0] == '0');
-  }();
+  // RoPE + cache write.  ORION_GEMM_FUSE=0 runs the separate launches (read
+  // per call, so a test can run one batch both ways in one process).
+  const char* fuse_env = getenv("ORION_GEMM_FUSE");
+  const bool allow_fuse = !(fuse_env && fuse_env[0] == '0');
   const bool fused = allow_fuse && gemm_splitk_fusable(n, m->qkvd, H) &&
                      gemm_splitk_fusable(n, H, m->qd) && gemm_splitk_fusable(n, 2 * F, H) &&
                      gemm_splitk_fusable(n, H, F);
@@ -1278,7 +1293,7 @@ ORION_EXPORT int orion_hip_model_forward(orion_hip_model* m, const orion_hip_bat
   // call; lets tests compare the two routes on one batch).
   const char* route = getenv("ORION_PREFILL_ROUTE");
   const bool route_pf = !(route && route[0] == '0');
-  if (route_pf && m->kv.dtype_bf16 && (d.head_dim == 64 || d.head_dim == 128)) {
+  if (route_pf && m->kv.dtype_bf16 && (d.head_dim == 64 || d.head_dim == 128) && G <= 8) {
     int64_t r0 = 0;
     for (int64_t s = 0; s < S; ++s) {
       const int64_t c = b->slot_token_counts[s];
@@ -1469,8 +1484,8 @@ static int kv_geom_from(const orion_hip_kv_layout* kv, KvGeom* g, const char* st
     return set_err(ORION_HIP_ERR_BACKEND, st, "kv dtype must be F32 or BF16");
   if (kv->block_size < 1 || (kv->block_size & (kv->block_size - 1)) || kv->block_size > 256)
     return internal(st, "block_size must be a power of two <= 256");
-  if (kv->head_dim != 64 && kv->head_dim != 128)
-    return set_err(ORION_HIP_ERR_BACKEND, st, "head_dim %lld unsupported (64 or 128)",
+  if (kv->head_dim <= 0 || kv->head_dim % 2 || kv->head_dim > 256)
+    return set_err(ORION_HIP_ERR_BACKEND, st, "head_dim %lld unsupported (even, at most 256)",
                    (long long)kv->head_dim);
   *g = KvGeom{kv->num_layers, kv->num_blocks, kv->block_size, kv->num_kv_heads, kv->head_dim,
               kv->dtype == ORION_DTYPE_BF16, kv->head_major != 0};
@@ -1544,8 +1559,6 @@ ORION_EXPORT int orion_hip_paged_attention_decode(
   if (g.num_kv_heads <= 0 || num_q_heads % g.num_kv_heads)
     return internal(st, "%lld query heads cannot be grouped over %lld kv heads",
                     (long long)num_q_heads, (long long)g.num_kv_heads);
-  if (num_q_heads / g.num_kv_heads > 8)
-    return set_err(ORION_HIP_ERR_BACKEND, st, "GQA group above 8 unsupported");
   if (layer < 0 || layer >= g.num_layers)
     return internal(st, "layer %lld out of range (have %lld)", (long long)layer,
                     (long long)g.num_layers);
@@ -1586,6 +1599,15 @@ ORION_EXPORT int orion_hip_paged_attention_prefill(
   if (int rc = kv_geom_from(kv, &g, st)) return rc;
   if (g.num_kv_heads <= 0 || num_q_heads % g.num_kv_heads)
     return internal(st, "query heads cannot be grouped over kv heads");
+  if (g.head_dim != 64 && g.head_dim != 128)
+    return set_err(ORION_HIP_ERR_BACKEND, st,
+                   "prefill attention covers head_dim 64 and 128 (got %lld); other shapes take "
+                   "the decode entry point row by row", (long long)g.head_dim);
+  if (num_q_heads / g.num_kv_heads > 8)
+    return set_err(ORION_HIP_ERR_BACKEND, st,
+                   "prefill attention covers groups of up to 8 query heads per kv head (got "
+                   "%lld); larger groups take the decode entry point",
+                   (long long)(num_q_heads / g.num_kv_heads));
   HIP_TRY(st, hipSetDevice(dev->ordinal));
   (void)max_rows;
   (void)max_position;
@@ -1644,10 +1666,9 @@ ORION_EXPORT int orion_hip_rmsnorm(orion_hip_device* dev, const float* d_x, cons
   return ORION_HIP_OK;
 }
 
-ORION_EXPORT int orion_hip_gemm(orion_hip_device* dev, const float* d_x, const uint16_t* d_w,
-                                const float* d_bias, int64_t M, int64_t N, int64_t K,
-                                int epilogue, float* d_out) {
-  const char* st = "gemm";
+// Argument checks shared by orion_hip_gemm and orion_hip_gemm_noalloc.
+static int gemm_args(const char* st, const float* d_bias, int64_t N, int64_t K, int epilogue,
+                     Epilogue* ep) {
   if (K % 32 != 0 || K <= 0)
     return set_err(ORION_HIP_ERR_BACKEND, st, "K must be a positive multiple of 32, got %lld",
                    (long long)K);
@@ -1658,10 +1679,19 @@ ORION_EXPORT int orion_hip_gemm(orion_hip_device* dev, const float* d_x, const u
   if (epilogue == ORION_GEMM_SWIGLU && N % 16 != 0)
     return internal(st, "SwiGLU needs N (gate/up rows) to be a multiple of 16, got %lld",
                     (long long)N);
+  *ep = epilogue == ORION_GEMM_ACCUMULATE ? Epilogue::kAccumulate
+        : epilogue == ORION_GEMM_SWIGLU   ? Epilogue::kSwiGLU
+                                          : Epilogue::kStore;
+  return ORION_HIP_OK;
+}
+
+ORION_EXPORT int orion_hip_gemm(orion_hip_device* dev, const float* d_x, const uint16_t* d_w,
+                                const float* d_bias, int64_t M, int64_t N, int64_t K,
+                                int epilogue, float* d_out) {
+  const char* st = "gemm";
+  Epilogue ep;
+  if (int rc = gemm_args(st, d_bias, N, K, epilogue, &ep)) return rc;
   HIP_TRY(st, hipSetDevice(dev->ordinal));
-  const Epilogue ep = epilogue == ORION_GEMM_ACCUMULATE ? Epilogue::kAccumulate
-                      : epilogue == ORION_GEMM_SWIGLU   ? Epilogue::kSwiGLU
-                                                        : Epilogue::kStore;
   HIP_TRY(st, gemm_on(dev, d_x, d_w, d_bias, M, N, K, ep, d_out));
   return ORION_HIP_OK;
 }

@@ -41,6 +41,7 @@ EXPORTED = [
     "orion_hip_alloc", "orion_hip_free", "orion_hip_memcpy_h2d", "orion_hip_memcpy_d2h",
     "orion_hip_memcpy_d2d", "orion_hip_memset", "orion_hip_timer_start", "orion_hip_timer_stop",
     "orion_hip_kernel_timing", "orion_hip_kernel_timing_read",
+    "orion_hip_kernel_timing_samples",
     "orion_hip_model_create", "orion_hip_model_destroy", "orion_hip_model_upload_weight",
     "orion_hip_model_init_synthetic", "orion_hip_synthetic_value",
     "orion_hip_checkpoint_open", "orion_hip_checkpoint_close", "orion_hip_checkpoint_num_tensors",
@@ -148,6 +149,7 @@ def load_library(path: str = LIB_PATH) -> C.CDLL:
         "orion_hip_timer_stop": ([vp, P(f32)], C.c_int),
         "orion_hip_kernel_timing": ([vp, C.c_int], C.c_int),
         "orion_hip_kernel_timing_read": ([vp, C.c_int, P(C.c_double), P(i64)], C.c_int),
+        "orion_hip_kernel_timing_samples": ([vp, C.c_int, vp, i64, P(i64)], C.c_int),
         "orion_hip_model_create": ([vp, P(ModelDesc), P(vp)], C.c_int),
         "orion_hip_model_destroy": ([vp], None),
         "orion_hip_model_upload_weight": ([vp, C.c_int, C.c_int, vp, C.c_int, sz], C.c_int),
@@ -321,6 +323,16 @@ class HipBackend:
         _check(self.lib.orion_hip_kernel_timing_read(self.handle, kernel, C.byref(ms),
                                                      C.byref(n)))
         return ms.value, n.value
+
+    def kernel_timing_samples(self, kernel: int) -> np.ndarray:
+        """Per-launch milliseconds recorded for `kernel` since enabling, in launch order."""
+        n = C.c_int64()
+        _check(self.lib.orion_hip_kernel_timing_samples(self.handle, kernel, None, 0,
+                                                        C.byref(n)))
+        out = np.zeros(n.value, np.float32)
+        _check(self.lib.orion_hip_kernel_timing_samples(self.handle, kernel, _ptr(out), n.value,
+                                                        C.byref(n)))
+        return out
 
     def close(self) -> None:
         if self.handle:

@@ -7,10 +7,13 @@ class PagedCase:
     """Sequences with context lengths `ctxs`, block tables drawn from a
     seeded permutation of a pool of `num_blocks`, and one query row per
     sequence at position ctx - 1 (decode).  K/V pool entries are N(0, 1)
-    (also the never-referenced blocks), stored in `dtype` ('f32' | 'bf16')."""
+    (also the never-referenced blocks), stored in `dtype` ('f32' | 'bf16').
+    With `rope_theta`, every cached K vector and every query is rotated by
+    RoPE at its position first (rotate-half, the reference's f32 table and
+    formula, tensor.rs:228-298), as the model does before caching."""
 
     def __init__(self, seed, ctxs, hq, hkv, d, block_size, num_blocks=None, dtype="f32",
-                 pool_factor=1.25, disjoint=True, head_major=False):
+                 pool_factor=1.25, disjoint=True, head_major=False, rope_theta=None):
         rng = np.random.default_rng(seed)
         self.ctxs = np.asarray(ctxs, dtype=np.int64)
         self.S = len(ctxs)
@@ -34,12 +37,23 @@ class PagedCase:
         self.bt_ids = np.concatenate(tables) if total else np.zeros(1, np.uint32)
         n_el = self.num_blocks * 2 * block_size * hkv * d
         arena = rng.standard_normal(n_el, dtype=np.float32)
+        self.q = rng.standard_normal((self.S, hq * d), dtype=np.float32)
+        self.positions = (self.ctxs - 1).astype(np.uint32)
+        self.rope_theta = rope_theta
+        if rope_theta is not None and total:
+            import oracle as orc
+            table = orc.RopeTable(d, int(self.ctxs.max()), rope_theta)
+            k = arena.reshape(self.num_blocks, 2, block_size, hkv, d)
+            for t, c in zip(tables, self.ctxs):
+                p = np.arange(int(c))
+                blk, slot = t[p // block_size], p % block_size
+                k[blk, 0, slot] = rope_rotate(k[blk, 0, slot], table.cos[p], table.sin[p])
+            self.q = rope_rotate(self.q.reshape(self.S, hq, d), table.cos[self.positions],
+                                 table.sin[self.positions]).reshape(self.S, hq * d)
         if dtype == "bf16":
             from model_fixtures import bf16_round
             arena = bf16_round(arena)
         self.arena_f32 = arena  # exact values the device holds, widened to f32
-        self.q = rng.standard_normal((self.S, hq * d), dtype=np.float32)
-        self.positions = (self.ctxs - 1).astype(np.uint32)
         self.row_seq = np.arange(self.S, dtype=np.int32)
 
     def dims(self):
@@ -76,6 +90,16 @@ class PagedCase:
             self.row_seq if row_seq is None else row_seq, self.bt_offsets, self.bt_ids)
 
 
+def rope_rotate(x, cos, sin):
+    """apply_rope (tensor.rs:283-298) on [n, heads, d] vectors at n positions:
+    (x_i, x_{i+d/2}) -> (x_i c - x_{i+d/2} s, x_i s + x_{i+d/2} c) in f32;
+    cos/sin are [n, d/2] rows of the reference's RopeTable."""
+    half = x.shape[-1] // 2
+    c, s = cos[:, None, :].astype(np.float32), sin[:, None, :].astype(np.float32)
+    x0, x1 = x[..., :half], x[..., half:]
+    return np.concatenate([x0 * c - x1 * s, x0 * s + x1 * c], axis=-1).astype(np.float32)
+
+
 def cfg1(seed=20261201):
     """4 seqs, ctx U[1,512], bs 16, 8q/2kv, d 64, f32, 256-block pool."""
     rng = np.random.default_rng(seed)
@@ -85,11 +109,12 @@ def cfg1(seed=20261201):
 
 def cfg2(seed=20261202, num_seqs=64, head_major=False):
     """64 seqs, ctx U[128,4096], bs 16, 32q/8kv, d 128, bf16 KV,
-    pool 1.25x the blocks needed, scattered tables."""
+    pool 1.25x the blocks needed, scattered tables; Q and cached K rotated by
+    RoPE (theta 500000) at their positions before caching."""
     rng = np.random.default_rng(seed)
     ctxs = rng.integers(128, 4097, size=num_seqs)
     return PagedCase(seed + 1, ctxs, 32, 8, 128, 16, dtype="bf16", pool_factor=1.25,
-                     head_major=head_major)
+                     head_major=head_major, rope_theta=500000.0)
 
 
 class PrefillCase(PagedCase):

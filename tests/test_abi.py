@@ -3,6 +3,7 @@ declares (no GPU needed: no compute call is made)."""
 import os
 import re
 import subprocess
+import ctypes as C
 
 import numpy as np
 
@@ -60,3 +61,25 @@ def test_bf16_helpers_round_to_nearest_even():
     # 1 + 2^-8 is a tie -> even (1.0); 1 + 3*2^-8 is a tie -> 1 + 2^-6
     assert back[0] == 1.0 and back[1] == 1.0 and back[2] == np.float32(1.015625)
     assert back[3] == -2.5 and np.isinf(back[5])
+
+
+ABI_CHECK = os.path.join(ROOT, "tests", "abi", "abi_check")
+
+
+def test_c_struct_layouts_match_the_ctypes_binding():
+    # tests/abi/abi_check.cpp static_asserts the header's layouts against the
+    # #[repr(C)] structs of the Rust bindings; here the same layouts are
+    # compared with the ctypes binding's structures.
+    import json
+
+    out = subprocess.run([ABI_CHECK, "layout"], capture_output=True, text=True, check=True)
+    lay = json.loads(out.stdout)
+    for cname, py in [("orion_hip_model_desc", orion_hip.ModelDesc),
+                      ("orion_hip_batch", orion_hip.BatchDesc),
+                      ("orion_hip_sampling_params", orion_hip.SamplingParams),
+                      ("orion_hip_kv_layout", orion_hip.KvLayout)]:
+        assert lay[cname]["size"] == C.sizeof(py), cname
+        fields = [f[0] for f in py._fields_]
+        assert list(lay[cname]["offsets"]) == fields, cname
+        for f in fields:
+            assert lay[cname]["offsets"][f] == getattr(py, f).offset, (cname, f)

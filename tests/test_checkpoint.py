@@ -118,7 +118,7 @@ def _raw_file(path, header_obj, data=b"", header_bytes=None):
 
 
 @pytest.mark.parametrize("case", ["truncated", "bad_json", "outside", "size", "overlap",
-                                  "short_len", "no_offsets", "trailing"])
+                                  "short_len", "no_offsets", "trailing", "wrap"])
 def test_malformed_files_are_refused(tmp_path, case):
     p = str(tmp_path / "m.safetensors")
     z = b"\0" * 16
@@ -141,6 +141,10 @@ def test_malformed_files_are_refused(tmp_path, case):
         _raw_file(p, {"a": {"dtype": "F32", "shape": [2]}}, z)
     elif case == "trailing":
         _raw_file(p, None, z, header_bytes=b'{} {}')
+    elif case == "wrap":
+        # 2^62 f32 elements: count * 4 wraps to 0 in 64 bits, matching the
+        # empty data_offsets unless the size check refuses it first
+        _raw_file(p, {"a": {"dtype": "F32", "shape": [1 << 62], "data_offsets": [0, 0]}}, z)
     with pytest.raises(hc.Malformed):
         oh.Checkpoint(str(tmp_path))
 

@@ -67,6 +67,24 @@ def test_shapes_groups_and_block_sizes(backend, hq, hkv, d, bs, dtype, head_majo
     assert mm == 0, (ma, mr, wi)
 
 
+@pytest.mark.parametrize("hq,hkv,d,bs,dtype", [
+    # head_dim other than 64/128 (the reference accepts any even head_dim,
+    # attention.rs:244-249) and groups above 8 (any divisible grouping):
+    # the general decode wave and merge
+    (8, 1, 80, 16, "bf16"), (16, 1, 96, 16, "f32"), (32, 2, 256, 16, "bf16"),
+    (32, 1, 64, 16, "bf16"), (24, 2, 128, 8, "f32"), (4, 2, 2, 16, "f32"),
+    (6, 3, 160, 32, "bf16"), (12, 1, 48, 4, "bf16"),
+])
+def test_any_head_dim_and_group(backend, hq, hkv, d, bs, dtype):
+    ctxs = [1, 2, 17, 64, 65, 300, 513, 1000, 2049]
+    case = PagedCase(hq * 100 + d + bs, ctxs, hq, hkv, d, bs, dtype=dtype)
+    got = run_decode(backend, case)
+    want = case.oracle()
+    tol = orc.Tolerance.F32 if dtype == "f32" else orc.Tolerance(1e-4, 1e-4)
+    mm, ma, mr, wi = orc.validate(want, got, tol)
+    assert mm == 0, (ma, mr, wi)
+
+
 def test_ragged_positions_and_shared_sequences(backend):
     # Several query rows per sequence at arbitrary positions (what a chunked
     # prefill batch looks like to the decode kernel) and sequences sharing

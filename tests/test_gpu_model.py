@@ -357,6 +357,9 @@ def test_tinyllama_shape_greedy_tokens_match_oracle(backend):
     for step in range(steps):
         err = float(np.abs(g - o).max())
         assert err <= 1e-2 * max(float(np.abs(o).max()), 1.0), (step, err)
+        # f32 KV: the decode steps run the fused norm / head-norm path, and
+        # must stay at the f32-arena bound the unfused odd-shape tests meet
+        assert rel_err(g, o) <= 1e-4, (step, rel_err(g, o))
         og = [orc.argmax(r) for r in o]
         gg = [int(np.argmax(r)) for r in g]
         for s in range(S):
@@ -403,3 +406,100 @@ def test_odd_shapes_decode_through_packed_weights(backend, H, F, hq, hkv, d, V):
         assert rel_err(g, o) <= 1e-4, (step, rel_err(g, o))
     om.close()
     gm.close()
+
+
+@pytest.mark.parametrize("H,F,hq,hkv,d,V,S,tied,bias", [
+    # hidden > 256 and not a multiple of 256 (partial last K slice in the
+    # norm and sums-of-squares code), vocab not a multiple of 128 (partial
+    # column tile), tied head (the LM head's packed copy comes from the
+    # embedding) with QKV bias (deferred QKV partials + bias in RoPE)
+    (576, 800, 9, 3, 64, 1000, 5, True, True),
+    # hidden 2304 with 40 rows: more sum-of-squares slots per row than the
+    # early norm path holds, so the GEMMs take the late norm loop
+    (2304, 1024, 18, 6, 128, 517, 40, False, False),
+])
+def test_fused_decode_layer_matches_oracle_and_unfused(backend, monkeypatch, H, F, hq, hkv, d, V,
+                                                       S, tied, bias):
+    # Decode batches (one row per sequence, every GEMM split over K) run the
+    # fused layer: RMSNorm applied inside the GEMMs from the residual reduces'
+    # row sums of squares, QKV partials summed by RoPE + cache, and the final
+    # norm inside the LM head.  Checked against the oracle at the f32-KV
+    # bound, and against the same batch with ORION_GEMM_FUSE=0 (separate
+    # norm and reduce launches) at f32 rounding.
+    rng = np.random.default_rng(H + S)
+    spec = Spec(2, H, hq, hkv, d, F, V, max_pos=512, bias=bias, tied=tied,
+                num_blocks=8 * S, block_size=16)
+    W = random_weights(spec, rng, std=0.05)
+    gm = gpu_model(backend, spec, W, oh.F32)
+    om = oracle_model(spec, W)
+    lens = [int(x) for x in rng.integers(3, 40, S)]
+    tables = [list(range(8 * s, 8 * s + 8)) for s in range(S)]
+    toks = rng.integers(0, V, sum(lens))
+    pos = np.concatenate([np.arange(n) for n in lens])
+    print(f"[fused decode] H={H} F={F} V={V} S={S} tied={tied} bias={bias}", flush=True)
+    g = gm.forward(batch(toks, pos, lens, tables)).logits
+    o = om.forward(toks, pos, lens, lens, tables)
+    assert rel_err(g, o) <= 1e-4, rel_err(g, o)
+    for step in range(3):
+        nxt = [orc.argmax(r) for r in o]
+        cur = [n + step for n in lens]
+        b = batch(nxt, cur, [1] * S, tables, [c + 1 for c in cur])
+        g = gm.forward(b).logits
+        o = om.forward(nxt, cur, [1] * S, [c + 1 for c in cur], tables)
+        assert rel_err(g, o) <= 1e-4, (step, rel_err(g, o))
+        # the same batch again without the fusions: rewrites identical K/V
+        monkeypatch.setenv("ORION_GEMM_FUSE", "0")
+        u = gm.forward(b).logits
+        monkeypatch.delenv("ORION_GEMM_FUSE")
+        assert rel_err(g, u) <= 1e-5, (step, rel_err(g, u))
+    om.close()
+    gm.close()
+
+
+@pytest.mark.parametrize("H,hq,hkv,d,kv", [(320, 4, 2, 80, oh.F32), (320, 4, 2, 80, oh.BF16),
+                                           (256, 16, 1, 48, oh.F32), (384, 24, 2, 96, oh.BF16)])
+def test_any_head_dim_and_group_forward(backend, H, hq, hkv, d, kv):
+    # head_dim 80 / 48 / 96 and groups of 2, 16 and 12 query heads per KV
+    # head: RoPE + cache write, the general decode wave for every row and the
+    # general merge, through prefill and decode forwards.  A bf16 arena is
+    # compared with the oracle rounding K/V to bf16 when written.
+    rng = np.random.default_rng(H + hq + d)
+    spec = Spec(2, H, hq, hkv, d, 512, 700, max_pos=512, bias=True, tied=False,
+                num_blocks=64, block_size=16)
+    W = random_weights(spec, rng, std=0.05)
+    gm = gpu_model(backend, spec, W, kv)
+    om = orc.OracleTransformer(spec.L, spec.H, spec.hq, spec.hkv, spec.d, spec.F, spec.V,
+                               spec.max_pos, spec.eps, spec.theta, spec.bias, spec.tied,
+                               spec.num_blocks, spec.block_size, kv_bf16=kv == oh.BF16)
+    for wid, key in [(orc.W_EMBED, "embed"), (orc.W_FINAL_NORM, "final_norm"),
+                     (orc.W_LM_HEAD, "lm_head")]:
+        om.set_weight(wid, -1, W[key])
+    for l, w in enumerate(W["layers"]):
+        for key, wid in KEYS:
+            if w[key] is not None:
+                om.set_weight(wid, l, w[key])
+    lens = [7, 70, 200]
+    tables = [list(range(16 * s, 16 * s + 16)) for s in range(3)]
+    toks = rng.integers(0, spec.V, sum(lens))
+    pos = np.concatenate([np.arange(n) for n in lens])
+    bound = 1e-4 if kv == oh.F32 else 1e-3
+    print(f"[any head_dim] H={H} hq={hq} hkv={hkv} d={d} kv={kv}", flush=True)
+    g = gm.forward(batch(toks, pos, lens, tables)).logits
+    o = om.forward(toks, pos, lens, lens, tables)
+    assert rel_err(g, o) <= bound, rel_err(g, o)
+    for step in range(3):
+        nxt = [orc.argmax(r) for r in o]
+        cur = [n + step for n in lens]
+        g = gm.forward(batch(nxt, cur, [1] * 3, tables, [c + 1 for c in cur])).logits
+        o = om.forward(nxt, cur, [1] * 3, [c + 1 for c in cur], tables)
+        assert rel_err(g, o) <= bound, (step, rel_err(g, o))
+    om.close()
+    gm.close()
+
+
+@pytest.mark.parametrize("d", [63, 258])
+def test_uncovered_head_dims_are_backend_errors(backend, d):
+    # odd head_dim (RoPE rotates halves) and head_dim above 256
+    spec = Spec(1, 256, 2, 1, d, 512, 100, num_blocks=8, block_size=16)
+    with pytest.raises(oh.BackendError):
+        oh.HipTransformerModel(meta_of(spec), 8, 16, backend, oh.F32)

@@ -119,3 +119,14 @@ def test_f32_arena_is_a_backend_error(backend):
     case = PrefillCase(3, [4], [8], 8, 2, 64, 16, dtype="f32")
     with pytest.raises(oh.BackendError):
         run_prefill(backend, case, False)
+
+
+@pytest.mark.parametrize("hq,hkv,d", [(8, 2, 80), (16, 1, 64), (4, 2, 256)])
+def test_uncovered_prefill_shapes_are_backend_errors(backend, hq, hkv, d):
+    # The MFMA prefill kernel covers head_dim 64/128 with groups up to 8; the
+    # model forward sends other shapes' rows to the decode kernel (which
+    # covers every even head_dim up to 256 and any group), and the op-level
+    # entry point refuses them with a Backend error before any launch.
+    case = PrefillCase(4, [20], [8], hq, hkv, d, 16)
+    with pytest.raises(oh.BackendError):
+        run_prefill(backend, case, False)

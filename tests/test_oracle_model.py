@@ -111,3 +111,39 @@ def test_tiny_model_golden_logits():
     assert np.array_equal(fwd(tiny(2), [1, 2, 3, 4, 5], [0, 1, 2, 3, 4], [0, 1]), g["full"])
     two = fwd(tiny(2), [1, 2, 5, 6, 7], [0, 1, 0, 1, 2], [[0], [4]], [2, 3], [2, 3])
     assert np.array_equal(two, g["two"])
+
+
+def test_bf16_kv_arena_holds_the_rounded_f32_values():
+    # kv_bf16 rounds each K/V element to bf16 (nearest even) when it is
+    # written: layer 0 (same inputs in both models) must hold exactly the
+    # rounded values of the f32 arena; every stored value is bf16-exact, and
+    # the logits move only by the rounding.
+    from model_fixtures import bf16_round
+
+    rng = np.random.default_rng(11)
+    spec = Spec(2, 64, 4, 2, 16, 96, 50, max_pos=128, bias=True, tied=False, num_blocks=16,
+                block_size=4)
+    W = random_weights(spec, rng, std=0.2)
+    tokens = rng.integers(0, spec.V, size=13).tolist()
+    m32 = oracle_model(spec, W)
+    m16 = orc.OracleTransformer(spec.L, spec.H, spec.hq, spec.hkv, spec.d, spec.F, spec.V,
+                                spec.max_pos, spec.eps, spec.theta, spec.bias, spec.tied,
+                                spec.num_blocks, spec.block_size, kv_bf16=True)
+    for key, wid in [("input_norm", orc.W_INPUT_NORM), ("q", orc.W_Q), ("k", orc.W_K),
+                     ("v", orc.W_V), ("o", orc.W_O), ("post_norm", orc.W_POST_NORM),
+                     ("gate", orc.W_GATE), ("up", orc.W_UP), ("down", orc.W_DOWN),
+                     ("q_bias", orc.W_Q_BIAS), ("k_bias", orc.W_K_BIAS), ("v_bias", orc.W_V_BIAS)]:
+        for l in range(spec.L):
+            m16.set_weight(wid, l, W["layers"][l][key])
+    m16.set_weight(orc.W_EMBED, -1, W["embed"])
+    m16.set_weight(orc.W_FINAL_NORM, -1, W["final_norm"])
+    m16.set_weight(orc.W_LM_HEAD, -1, W["lm_head"])
+    table = [3, 7, 1, 12]
+    a = m32.forward(tokens, list(range(13)), [13], [13], [table])
+    b = m16.forward(tokens, list(range(13)), [13], [13], [table])
+    kv32, kv16 = m32.kv().copy(), m16.kv().copy()
+    half = kv32.size // spec.L
+    assert np.array_equal(kv16[:half].view(np.uint32), bf16_round(kv32[:half]).view(np.uint32))
+    assert np.all((kv16.view(np.uint32) & 0xFFFF) == 0)
+    assert not np.array_equal(a, b)
+    assert float(np.abs(a - b).max()) <= 2e-2 * float(np.abs(a).max())
