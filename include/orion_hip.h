@@ -392,6 +392,19 @@ int orion_hip_gemm(orion_hip_device* dev, const float* d_x, const uint16_t* d_w,
                    const float* d_bias, int64_t M, int64_t N, int64_t K, int epilogue,
                    float* d_out);
 
+/* orion_hip_gemm that allocates nothing (no counterpart in the reference: it
+ * is for callers that cannot allocate device memory, such as code under HIP
+ * graph capture or a serving loop that forbids hipMalloc).  Same arguments,
+ * kernels and results as orion_hip_gemm; the split-K partial tiles of
+ * decode-shaped calls (M <= 64) go to a fixed 64 MiB device array that each
+ * GPU holds for the life of the process, instead of the device's grown
+ * scratch.  A shape whose partials exceed 64 MiB is refused with
+ * ORION_HIP_ERR_BACKEND.  Every call on one GPU shares that GPU's array:
+ * calls that overlap on one GPU (other streams, other threads) race. */
+int orion_hip_gemm_noalloc(orion_hip_device* dev, const float* d_x, const uint16_t* d_w,
+                           const float* d_bias, int64_t M, int64_t N, int64_t K, int epilogue,
+                           float* d_out);
+
 /* swiglu (tensor.rs:175-189): d_gate = silu(d_gate) * d_up, elementwise. */
 int orion_hip_silu_mul(orion_hip_device* dev, float* d_gate, const float* d_up, int64_t count);
 

@@ -11,6 +11,7 @@
 #include <cstdio>
 #include <cstring>
 #include <memory>
+#include <mutex>
 #include <string>
 #include <vector>
 
@@ -147,6 +148,9 @@ struct orion_hip_device {
   DevBuf gemm_ws;
   DevBuf prefill_order;  // op-level prefill work list
   DevBuf sample_io, sample_ws;  // sampler inputs/outputs and probabilities
+  // This device's address of the file-scope `scratch` array
+  // (orion_hip_gemm_noalloc); never freed.
+  void* noalloc_scratch = nullptr;
   // Per-kernel timing (orion_hip_kernel_timing): event pairs per kernel
   // index, resolved when read.
   bool ktiming = false;
@@ -278,6 +282,36 @@ ORION_EXPORT int orion_hip_device_count(int* count) {
   return ORION_HIP_OK;
 }
 
+// ---------------------------------------------------------------------------
+// Scratch of the no-allocation GEMM entry point (orion_hip_gemm_noalloc)
+// ---------------------------------------------------------------------------
+
+// Split-K partial tiles of orion_hip_gemm_noalloc.  Every GPU the library runs
+// on holds its own copy for the life of the process.  Host code never uses
+// the array's name as an address (on the host it is only a stand-in): the
+// device address is resolved once per device, with that device current, at
+// orion_hip_device_open, and kept in g_noalloc_scratch.
+constexpr size_t kNoAllocScratchBytes = size_t(64) << 20;
+static __device__ __align__(256) char scratch[kNoAllocScratchBytes];
+
+static std::mutex g_noalloc_mu;
+static void* g_noalloc_scratch[256] = {};
+
+// Resolves this device's address of `scratch` (the device must be current).
+static hipError_t resolve_noalloc_scratch(int ordinal, void** out) {
+  if (ordinal < 0 || ordinal >= 256) return hipErrorInvalidDevice;
+  std::lock_guard<std::mutex> lk(g_noalloc_mu);
+  if (!g_noalloc_scratch[ordinal]) {
+    void* p = nullptr;
+    hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) return e;
+    if (!p) return hipErrorInvalidSymbol;
+    g_noalloc_scratch[ordinal] = p;
+  }
+  *out = g_noalloc_scratch[ordinal];
+  return hipSuccess;
+}
+
 ORION_EXPORT int orion_hip_device_open(int ordinal, orion_hip_device** out) {
   *out = nullptr;
   int n = 0;
@@ -300,6 +334,7 @@ ORION_EXPORT int orion_hip_device_open(int ordinal, orion_hip_device** out) {
   HIP_TRY("device_open", hipStreamCreateWithFlags(&dev->stream, hipStreamNonBlocking));
   HIP_TRY("device_open", hipEventCreate(&dev->ev_start));
   HIP_TRY("device_open", hipEventCreate(&dev->ev_stop));
+  HIP_TRY("device_open", resolve_noalloc_scratch(ordinal, &dev->noalloc_scratch));
   *out = dev.release();
   return ORION_HIP_OK;
 }
@@ -1693,6 +1728,31 @@ ORION_EXPORT int orion_hip_gemm(orion_hip_device* dev, const float* d_x, const u
   if (int rc = gemm_args(st, d_bias, N, K, epilogue, &ep)) return rc;
   HIP_TRY(st, hipSetDevice(dev->ordinal));
   HIP_TRY(st, gemm_on(dev, d_x, d_w, d_bias, M, N, K, ep, d_out));
+  return ORION_HIP_OK;
+}
+
+ORION_EXPORT int orion_hip_gemm_noalloc(orion_hip_device* dev, const float* d_x,
+                                        const uint16_t* d_w, const float* d_bias, int64_t M,
+                                        int64_t N, int64_t K, int epilogue, float* d_out) {
+  const char* st = "gemm_noalloc";
+  Epilogue ep;
+  if (int rc = gemm_args(st, d_bias, N, K, epilogue, &ep)) return rc;
+  size_t need = 0;
+  gemm_scratch_need(M, N, K, &need);
+  if (need > kNoAllocScratchBytes)
+    return set_err(ORION_HIP_ERR_BACKEND, st,
+                   "M=%lld N=%lld K=%lld needs %zu bytes of split-K scratch; the "
+                   "no-allocation entry point holds %zu",
+                   (long long)M, (long long)N, (long long)K, need, kNoAllocScratchBytes);
+  if (!dev->noalloc_scratch)
+    return set_err(ORION_HIP_ERR_BACKEND, st, "device scratch address was not resolved");
+  HIP_TRY(st, hipSetDevice(dev->ordinal));
+  // The same kernels as orion_hip_gemm; every partial tile a call reads was
+  // written earlier in the same call, so nothing needs clearing.
+  GemmScratch sc;
+  sc.ws = static_cast<float*>(dev->noalloc_scratch);
+  sc.ws_bytes = kNoAllocScratchBytes;
+  HIP_TRY(st, launch_gemm(dev->stream, d_x, d_w, d_bias, M, N, K, ep, d_out, &sc, nullptr));
   return ORION_HIP_OK;
 }
 

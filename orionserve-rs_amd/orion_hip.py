@@ -51,7 +51,7 @@ EXPORTED = [
     "orion_hip_model_kv_write", "orion_hip_model_kv_arena", "orion_hip_model_kv_layout", "orion_hip_decode_plan_create",
     "orion_hip_decode_plan_destroy", "orion_hip_decode_plan_info", "orion_hip_paged_attention_decode",
     "orion_hip_paged_attention_prefill", "orion_hip_rope_and_cache", "orion_hip_rmsnorm",
-    "orion_hip_gemm", "orion_hip_silu_mul", "orion_hip_argmax",
+    "orion_hip_gemm", "orion_hip_gemm_noalloc", "orion_hip_silu_mul", "orion_hip_argmax",
 ]
 
 
@@ -184,6 +184,7 @@ def load_library(path: str = LIB_PATH) -> C.CDLL:
              vp, vp], C.c_int),
         "orion_hip_rmsnorm": ([vp, vp, vp, i64, i64, f32, vp], C.c_int),
         "orion_hip_gemm": ([vp, vp, vp, vp, i64, i64, i64, C.c_int, vp], C.c_int),
+        "orion_hip_gemm_noalloc": ([vp, vp, vp, vp, i64, i64, i64, C.c_int, vp], C.c_int),
         "orion_hip_silu_mul": ([vp, vp, vp, i64], C.c_int),
         "orion_hip_argmax": ([vp, vp, i64, i64, vp], C.c_int),
     }

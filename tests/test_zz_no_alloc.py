@@ -1,0 +1,68 @@
+"""orion_hip_gemm_noalloc (the GEMM entry point that allocates nothing)
+against orion_hip_gemm, through the C-ABI: identical kernels, so the outputs
+must be bit-identical.  Calls run back to back on one device, each later one
+smaller than the one before, so a call that read partial tiles left by the
+previous (larger) call would show.  A shape whose split-K partials exceed the
+fixed device array is refused with a Backend error before any launch."""
+import ctypes as C
+
+import numpy as np
+import pytest
+
+import orion_hip as oh
+from model_fixtures import bf16_round
+
+pytestmark = pytest.mark.gpu
+
+
+def run_both(be, M, N, K, ep, bias, seed):
+    rng = np.random.default_rng(seed)
+    x = rng.standard_normal((M, K), dtype=np.float32)
+    w = bf16_round(rng.standard_normal((N, K), dtype=np.float32) * 0.05)
+    b = rng.standard_normal(N, dtype=np.float32) if bias else None
+    n_out = N // 2 if ep == oh.GEMM_SWIGLU else N
+    init = rng.standard_normal((M, n_out), dtype=np.float32)
+    dx, dw = be.to_device(x), be.to_device(oh.f32_to_bf16_bits(w))
+    db = be.to_device(b) if bias else None
+    d1, d2 = be.to_device(init), be.to_device(init)
+    print(f"[gemm_noalloc] M={M} N={N} K={K} ep={ep} bias={bias}", flush=True)
+    bp = db.ptr if db else None
+    oh._check(be.lib.orion_hip_gemm(be.handle, dx.ptr, dw.ptr, bp, M, N, K, ep, d1.ptr))
+    oh._check(be.lib.orion_hip_gemm_noalloc(be.handle, dx.ptr, dw.ptr, bp, M, N, K, ep, d2.ptr))
+    a = d1.download(np.float32, (M, n_out))
+    c = d2.download(np.float32, (M, n_out))
+    for buf in (dx, dw, db, d1, d2):
+        if buf:
+            buf.free()
+    return a, c
+
+
+# Larger first, then smaller: LM-head-sized partials (32 MB), then QKV with
+# bias, a down projection (22 K slices), SwiGLU, a residual accumulate, a
+# single-slice shape and one row; a skinny (M = 100) and a tiled (M = 300)
+# shape, which use no partials.
+SEQUENCE = [(32, 32000, 2048, oh.GEMM_STORE, False), (8, 2560, 2048, oh.GEMM_STORE, True),
+            (64, 2048, 5632, oh.GEMM_ACCUMULATE, False), (32, 11264, 2048, oh.GEMM_SWIGLU, False),
+            (17, 2048, 2048, oh.GEMM_ACCUMULATE, False), (5, 96, 256, oh.GEMM_STORE, True),
+            (1, 512, 1024, oh.GEMM_STORE, False), (100, 1024, 512, oh.GEMM_STORE, False),
+            (300, 384, 256, oh.GEMM_ACCUMULATE, False)]
+
+
+def test_noalloc_gemm_matches_gemm_on_consecutive_calls(backend):
+    for i, (M, N, K, ep, bias) in enumerate(SEQUENCE):
+        a, c = run_both(backend, M, N, K, ep, bias, seed=100 + i)
+        assert np.array_equal(a.view(np.uint32), c.view(np.uint32)), (M, N, K, ep)
+
+
+def test_noalloc_gemm_twice_in_a_row_smaller_second(backend):
+    for (M, N, K) in [(48, 16384, 4096), (3, 640, 2048)]:
+        a, c = run_both(backend, M, N, K, oh.GEMM_STORE, False, seed=M)
+        assert np.array_equal(a.view(np.uint32), c.view(np.uint32)), (M, N, K)
+
+
+def test_noalloc_gemm_refuses_shapes_beyond_its_scratch(backend):
+    # 64 rows x 200,000 columns over K = 4096 needs ~800 MB of partials
+    with pytest.raises(oh.BackendError, match="no-allocation entry point holds"):
+        oh._check(backend.lib.orion_hip_gemm_noalloc(backend.handle, C.c_void_p(16),
+                                                     C.c_void_p(16), None, 64, 200000, 4096,
+                                                     oh.GEMM_STORE, C.c_void_p(16)))
