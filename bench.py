@@ -175,10 +175,17 @@ def decode_e2e(steps=64, seqs=32, seed=20261204, cpu=True):
     model.init_synthetic(seed, 0.02)
     toks = [t for p in case.prompts for t in p]
     pos = [i for n in lens for i in range(int(n))]
+    pf_batch = oh.ForwardBatch(toks, pos, list(range(seqs)), [int(n) for n in lens],
+                               [int(n) for n in lens], tables, True)
+    # The first forward also writes the packed weight copies (once per weight
+    # write) and frees the row-major ones; the prefill is then timed again (it
+    # rewrites the same K/V).
     t0 = time.perf_counter()
-    out = model.forward(oh.ForwardBatch(toks, pos, list(range(seqs)), [int(n) for n in lens],
-                                        [int(n) for n in lens], tables, True),
-                        want_logits=False, want_argmax=True)
+    out = model.forward(pf_batch, want_logits=False, want_argmax=True)
+    be.synchronize()
+    prefill_first_s = time.perf_counter() - t0
+    t0 = time.perf_counter()
+    out = model.forward(pf_batch, want_logits=False, want_argmax=True)
     be.synchronize()
     prefill_s = time.perf_counter() - t0
     last = out.argmax.tolist()
@@ -222,7 +229,9 @@ def decode_e2e(steps=64, seqs=32, seed=20261204, cpu=True):
         "step_ms_min_max": [round(min(per_step) * 1e3, 4), round(max(per_step) * 1e3, 4)],
         "timed_steps": n_steps,
         "prefill_tokens": int(sum(lens)),
-        "prefill_s": round(prefill_s, 3),
+        "prefill_s": round(prefill_s, 4),
+        "prefill_tokens_per_s": round(int(sum(lens)) / prefill_s, 1),
+        "prefill_first_s": round(prefill_first_s, 4),
         "workload": "TinyLlama-1.1B shape (22L, hidden 2048, 32q/4kv, d 64, ffn 5632, vocab "
                     "32000), bf16 weights N(0,0.02) synthetic, bf16 KV, 32 seqs, prompts "
                     "U[16,1024], greedy decode",

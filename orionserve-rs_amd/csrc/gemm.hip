@@ -203,10 +203,19 @@ __device__ inline int swz_a(int r) {
 __device__ inline int swz_b(int n) { return (n >> 2) & 3; }
 }  // namespace
 
+// W is either row-major [N, K] (pk.nt == 0) or in the decode GEMM's packed
+// order (launch_gemv_pack with geometry pk): there a 16-column x 32-k MFMA B
+// fragment is one contiguous KiB, lane l's 16 bytes at l * 16, so each of the
+// tile's 8 fragments per k-step is copied to LDS verbatim and read back with
+// one conflict-free ds_read_b128 per lane.
+struct PackedGeom {
+  int nt = 0, ks = 0, n_tiles = 0;  // columns per decode workgroup / 64, k-steps per slice
+};
+
 __global__ void __launch_bounds__(256)
     gemm_tiled_kernel(const float* __restrict__ x, const uint16_t* __restrict__ w,
                       const float* __restrict__ bias, int M, int N, int K, int ep,
-                      float* __restrict__ out) {
+                      float* __restrict__ out, PackedGeom pk) {
   __shared__ __attribute__((aligned(1024))) float As[2][kTM * kTK];
   __shared__ __attribute__((aligned(1024))) uint16_t Bs[2][kTN * kTK];
 
@@ -227,12 +236,25 @@ __global__ void __launch_bounds__(256)
     const int c = (lane & 7) ^ swz_a(r);
     a_src[j] = x + (int64_t)min(m0 + r, M - 1) * K + c * 4;
   }
+  // Packed W: fragment f = wave * 2 + j holds columns n0 + 16 f .. + 16.  Its
+  // chunk (decode workgroup share) within a K slice, and the last fragment
+  // column group the packed copy holds (columns past it are past N anyway).
+  const bool packed = pk.nt > 0;
+  int64_t b_chunk[2] = {0, 0};
 #pragma unroll
   for (int j = 0; j < 2; ++j) {
-    const int r = (wave * 2 + j) * 16 + (lane >> 2);
-    const int c = (lane & 3) ^ swz_b(r);
-    b_src[j] = w + (int64_t)min(n0 + r, N - 1) * K + c * 8;
+    if (packed) {
+      const int c16 = min(n0 / 16 + wave * 2 + j, pk.n_tiles * 4 * pk.nt - 1);
+      const int tile = c16 / (4 * pk.nt), rem = c16 - tile * 4 * pk.nt;
+      b_chunk[j] = ((int64_t)tile * 4 + rem / pk.nt) * pk.nt + rem % pk.nt;
+      b_src[j] = w + (int64_t)lane * 8;
+    } else {
+      const int r = (wave * 2 + j) * 16 + (lane >> 2);
+      const int c = (lane & 3) ^ swz_b(r);
+      b_src[j] = w + (int64_t)min(n0 + r, N - 1) * K + c * 8;
+    }
   }
+  const int64_t slice_elems = (int64_t)pk.n_tiles * 4 * pk.nt * pk.ks * 512;  // one K slice
   const uint32_t as_base = (uint32_t)(uintptr_t)&As[0][0];
   const uint32_t bs_base = (uint32_t)(uintptr_t)&Bs[0][0];
   auto load_tile = [&](int ks, int buf) {
@@ -240,9 +262,17 @@ __global__ void __launch_bounds__(256)
 #pragma unroll
     for (int j = 0; j < 4; ++j)
       lds_load16(a_src[j] + k0, as_base + (uint32_t)(buf * kTM * kTK * 4 + (wave * 4 + j) * 1024));
+    if (packed) {
+      const int slice = ks / pk.ks, step = ks - slice * pk.ks;
 #pragma unroll
-    for (int j = 0; j < 2; ++j)
-      lds_load16(b_src[j] + k0, bs_base + (uint32_t)(buf * kTN * kTK * 2 + (wave * 2 + j) * 1024));
+      for (int j = 0; j < 2; ++j)
+        lds_load16(b_src[j] + slice * slice_elems + (b_chunk[j] * pk.ks + step) * 512,
+                   bs_base + (uint32_t)(buf * kTN * kTK * 2 + (wave * 2 + j) * 1024));
+    } else {
+#pragma unroll
+      for (int j = 0; j < 2; ++j)
+        lds_load16(b_src[j] + k0, bs_base + (uint32_t)(buf * kTN * kTK * 2 + (wave * 2 + j) * 1024));
+    }
   };
 
   // ---- fragment read addresses (bytes, buffer 0) ----
@@ -258,7 +288,8 @@ __global__ void __launch_bounds__(256)
 #pragma unroll
   for (int nt = 0; nt < 4; ++nt) {
     const int n = wn * 64 + nt * 16 + l16;
-    b_rd[nt] = bs_base + (uint32_t)(n * kTK + ((grp ^ swz_b(n)) * 8)) * 2;
+    b_rd[nt] = packed ? bs_base + (uint32_t)((wn * 4 + nt) * 1024 + lane * 16)
+                      : bs_base + (uint32_t)(n * kTK + ((grp ^ swz_b(n)) * 8)) * 2;
   }
 
   f32x4 acc[4][4];
@@ -775,6 +806,25 @@ __global__ void __launch_bounds__(256)
   out[u] = v;
 }
 
+// The inverse of gemv_pack_kernel: unit u goes back to W[col][k .. k+8).
+__global__ void __launch_bounds__(256)
+    gemv_unpack_kernel(const uint4* __restrict__ in, int N, int K, int nt, int ks, int n_tiles,
+                       int64_t units, uint16_t* __restrict__ w) {
+  const int64_t u = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (u >= units) return;
+  const int lane = (int)(u & 63);
+  const int64_t q = u >> 6;
+  const int s = (int)(q % ks);
+  const int64_t chunk = q / ks;
+  const int nti = (int)(chunk % nt);
+  const int wave = (int)((chunk / nt) & 3);
+  const int64_t wg = chunk / (4 * nt);
+  const int bx = (int)(wg % n_tiles), by = (int)(wg / n_tiles);
+  const int col = bx * 64 * nt + (wave * nt + nti) * 16 + (lane & 15);
+  const int k = by * ks * 32 + s * 32 + (lane >> 4) * 8;
+  if (col < N && k < K) *reinterpret_cast<uint4*>(w + (int64_t)col * K + k) = in[u];
+}
+
 size_t gemv_packed_bytes(int64_t N, int64_t K, bool deferred) {
   if (K % 32 != 0 || K <= 0 || N <= 0) return 0;
   const GemvShape g = gemv_shape(1, N, K, deferred);
@@ -789,6 +839,18 @@ hipError_t launch_gemv_pack(hipStream_t st, const uint16_t* w, int64_t N, int64_
   const int64_t units = (int64_t)gemv_packed_bytes(N, K, deferred) / 16;
   hipLaunchKernelGGL(gemv_pack_kernel, dim3((unsigned)((units + 255) / 256)), dim3(256), 0, st, w,
                      (int)N, (int)K, g.nt, g.ks, g.n_tiles, units, reinterpret_cast<uint4*>(out));
+  return hipGetLastError();
+}
+
+hipError_t launch_gemv_unpack(hipStream_t st, const uint16_t* packed, int64_t N, int64_t K,
+                              bool deferred, uint16_t* w) {
+  if (K % 32 != 0 || K <= 0 || N <= 0 || N > INT32_MAX || K > INT32_MAX)
+    return hipErrorInvalidValue;
+  const GemvShape g = gemv_shape(1, N, K, deferred);
+  const int64_t units = (int64_t)gemv_packed_bytes(N, K, deferred) / 16;
+  hipLaunchKernelGGL(gemv_unpack_kernel, dim3((unsigned)((units + 255) / 256)), dim3(256), 0, st,
+                     reinterpret_cast<const uint4*>(packed), (int)N, (int)K, g.nt, g.ks,
+                     g.n_tiles, units, w);
   return hipGetLastError();
 }
 
@@ -857,11 +919,20 @@ hipError_t launch_gemm(hipStream_t st, const float* x, const uint16_t* w, const 
       return hipGetLastError();
     }
   }
-  if (M >= tiled_min_m) {
+  // The LDS-tiled kernel takes every larger M, and every M > 64 when only the
+  // packed copy exists (the skinny kernel reads row-major W).
+  if (M >= tiled_min_m || f.w_packed) {
     if (M > (int64_t)65535 * kTM || N > INT32_MAX || K > INT32_MAX) return hipErrorInvalidValue;
+    PackedGeom pk;
+    if (f.w_packed) {
+      const GemvShape gp = gemv_shape(1, N, K, f.w_packed_deferred);
+      pk.nt = gp.nt;
+      pk.ks = gp.ks;
+      pk.n_tiles = gp.n_tiles;
+    }
     dim3 grid((unsigned)((N + kTN - 1) / kTN), (unsigned)((M + kTM - 1) / kTM));
-    hipLaunchKernelGGL(gemm_tiled_kernel, grid, dim3(256), 0, st, x, w, bias, (int)M, (int)N,
-                       (int)K, (int)ep, out);
+    hipLaunchKernelGGL(gemm_tiled_kernel, grid, dim3(256), 0, st, x, f.w_packed ? f.w_packed : w,
+                       bias, (int)M, (int)N, (int)K, (int)ep, out, pk);
     return hipGetLastError();
   }
   // Rows per tile (MT x 16) and columns per tile (NT x 16): wide column tiles

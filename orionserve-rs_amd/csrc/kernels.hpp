@@ -169,10 +169,12 @@ struct GemmFuse {
   float norm_eps = 0.f;
   double* sumsq_out = nullptr;
   GemmPartials* defer = nullptr;
-  // The same weights in the decode kernel's packed order (launch_gemv_pack,
-  // same shape and `defer` choice); read instead of w when the decode-shaped
-  // split-K kernel runs.
+  // The same weights in the decode kernel's packed order (launch_gemv_pack with
+  // this shape and w_packed_deferred); read instead of w by the decode-shaped
+  // split-K kernel and the LDS-tiled kernel (which then also takes M in
+  // (64, 256)).  w may be null when w_packed is given.
   const uint16_t* w_packed = nullptr;
+  bool w_packed_deferred = false;
 };
 // Bytes of W [N, K] in the decode kernel's packed order (0: K not a multiple
 // of 32), and the kernel that writes it from row-major W.  `deferred` must be
@@ -181,6 +183,9 @@ struct GemmFuse {
 size_t gemv_packed_bytes(int64_t N, int64_t K, bool deferred);
 hipError_t launch_gemv_pack(hipStream_t st, const uint16_t* w, int64_t N, int64_t K,
                             bool deferred, uint16_t* out);
+// The inverse: row-major W [N, K] from its packed copy.
+hipError_t launch_gemv_unpack(hipStream_t st, const uint16_t* packed, int64_t N, int64_t K,
+                              bool deferred, uint16_t* w);
 bool gemm_splitk_fusable(int64_t M, int64_t N, int64_t K);
 int gemm_sumsq_slots(int64_t N);
 

@@ -209,7 +209,8 @@ struct LayerDev {
   uint16_t* w_gu = nullptr;   // [2*ffn, hidden], gate/up rows interleaved by 8
   uint16_t* w_down = nullptr; // [hidden, ffn]
   // The same four matrices in the decode GEMM's packed order (launch_gemv_pack),
-  // made on the first decode-shaped forward after a weight write.
+  // which every GEMM of a forward reads.  The row-major ones above exist only
+  // while weights are written or read back (ensure_rowmajor / release_rowmajor).
   uint16_t* p_qkv = nullptr;
   uint16_t* p_o = nullptr;
   uint16_t* p_gu = nullptr;
@@ -228,6 +229,7 @@ struct orion_hip_model {
   float* final_norm = nullptr;
   uint16_t* p_head = nullptr;  // LM head (or tied embedding) in packed order
   bool packs_valid = false;    // packed copies match the row-major weights
+  bool rowmajor_live = true;   // row-major layer matrices / LM head allocated
   std::vector<LayerDev> layers;
   float* rope_cos = nullptr;
   float* rope_sin = nullptr;
@@ -248,6 +250,23 @@ struct orion_hip_model {
                       &b_positions, &b_rowseq, &b_btoff, &b_btids, &b_last})
       b->release();
     if (pinned) (void)hipHostFree(pinned);
+  }
+
+  // Frees one allocation made by alloc (the device is synchronised first).
+  template <typename T>
+  hipError_t release(T** p) {
+    if (!*p) return hipSuccess;
+    for (size_t i = 0; i < allocations.size(); ++i) {
+      if (allocations[i] == static_cast<void*>(*p)) {
+        hipError_t e = hipStreamSynchronize(dev->stream);
+        if (e == hipSuccess) e = hipFree(allocations[i]);
+        allocations.erase(allocations.begin() + i);
+        alloc_bytes.erase(alloc_bytes.begin() + i);
+        *p = nullptr;
+        return e;
+      }
+    }
+    return hipErrorInvalidValue;
   }
 
   template <typename T>
@@ -626,8 +645,15 @@ struct WeightSlot {
   int64_t group = 0, stride = 0, offset = 0;
 };
 
+static hipError_t ensure_rowmajor(orion_hip_model* m);
+
 static int weight_slot(orion_hip_model* m, int which, int layer, WeightSlot* s) {
   const auto& d = m->desc;
+  const bool matrix = which == ORION_W_LM_HEAD || which == ORION_W_Q || which == ORION_W_K ||
+                      which == ORION_W_V || which == ORION_W_O || which == ORION_W_GATE ||
+                      which == ORION_W_UP || which == ORION_W_DOWN;
+  if (matrix && (which != ORION_W_LM_HEAD || !d.tied_lm_head))
+    HIP_TRY("weight", ensure_rowmajor(m));
   const int64_t H = d.hidden_size, F = d.intermediate_size, V = d.vocab_size;
   if (which >= ORION_W_INPUT_NORM && (layer < 0 || layer >= d.num_layers))
     return internal("upload_weight", "layer %d out of range (have %d)", layer, d.num_layers);
@@ -1240,34 +1266,81 @@ int validate_batch(orion_hip_model* m, const orion_hip_batch* b, HostBatch* hb) 
 
 }  // namespace
 
-// Writes the packed copies of every layer matrix and the LM head
-// (allocated on first use), in the geometry each forward GEMM call uses: the
-// QKV GEMM leaves its partials to RoPE (deferred), the others reduce.  A
-// matrix whose K is not a multiple of 32 keeps no copy.
-static hipError_t make_packs(orion_hip_model* m) {
+// The layer matrices and the (untied) LM head, with their packed copies and
+// geometry.  A tied head's packed copy comes from the embedding, which stays
+// row-major (the embedding gather reads it).
+struct MatrixRef {
+  uint16_t** rowmajor;
+  uint16_t** packed;
+  int64_t N, K;
+  bool deferred;  // QKV: its partials go to RoPE unreduced
+};
+static std::vector<MatrixRef> matrices(orion_hip_model* m) {
   const auto& d = m->desc;
   const int64_t H = d.hidden_size, F = d.intermediate_size, V = d.vocab_size;
+  std::vector<MatrixRef> v;
+  for (LayerDev& L : m->layers) {
+    v.push_back({&L.w_qkv, &L.p_qkv, m->qkvd, H, true});
+    v.push_back({&L.w_o, &L.p_o, H, m->qd, false});
+    v.push_back({&L.w_gu, &L.p_gu, 2 * F, H, false});
+    v.push_back({&L.w_down, &L.p_down, H, F, false});
+  }
+  if (!d.tied_lm_head) v.push_back({&m->w_lm, &m->p_head, V, H, false});
+  return v;
+}
+
+// Writes the packed copy of every layer matrix and the LM head (allocated on
+// first use) from the row-major weights, in the geometry each forward GEMM
+// call uses.
+static hipError_t make_packs(orion_hip_model* m) {
+  const auto& d = m->desc;
   hipStream_t stream = m->dev->stream;
   auto one = [&](uint16_t** dst, const uint16_t* w, int64_t N, int64_t K,
                  bool deferred) -> hipError_t {
     const size_t bytes = gemv_packed_bytes(N, K, deferred);
-    if (!bytes) return hipSuccess;
+    if (!bytes) return hipErrorInvalidValue;
     if (!*dst) {
       hipError_t e = m->alloc(dst, bytes / 2);
       if (e != hipSuccess) return e;
     }
     return launch_gemv_pack(stream, w, N, K, deferred, *dst);
   };
-  for (LayerDev& L : m->layers) {
-    hipError_t e = one(&L.p_qkv, L.w_qkv, m->qkvd, H, true);
-    if (e == hipSuccess) e = one(&L.p_o, L.w_o, H, m->qd, false);
-    if (e == hipSuccess) e = one(&L.p_gu, L.w_gu, 2 * F, H, false);
-    if (e == hipSuccess) e = one(&L.p_down, L.w_down, H, F, false);
+  if (!m->rowmajor_live) return hipErrorInvalidValue;
+  for (const MatrixRef& r : matrices(m)) {
+    hipError_t e = one(r.packed, *r.rowmajor, r.N, r.K, r.deferred);
     if (e != hipSuccess) return e;
   }
-  hipError_t e = one(&m->p_head, m->w_lm ? m->w_lm : m->w_embed, V, H, false);
-  if (e != hipSuccess) return e;
+  if (d.tied_lm_head) {
+    hipError_t e = one(&m->p_head, m->w_embed, d.vocab_size, d.hidden_size, false);
+    if (e != hipSuccess) return e;
+  }
   m->packs_valid = true;
+  return hipSuccess;
+}
+
+// Frees the row-major layer matrices and LM head once the packed copies hold
+// the weights (one copy of every weight in HBM).
+static hipError_t release_rowmajor(orion_hip_model* m) {
+  if (!m->rowmajor_live || !m->packs_valid) return hipSuccess;
+  for (const MatrixRef& r : matrices(m)) {
+    hipError_t e = m->release(r.rowmajor);
+    if (e != hipSuccess) return e;
+  }
+  m->rowmajor_live = false;
+  return hipSuccess;
+}
+
+// Brings the row-major matrices back (unpacked from the packed copies) before
+// a weight is written or read back.
+static hipError_t ensure_rowmajor(orion_hip_model* m) {
+  if (m->rowmajor_live) return hipSuccess;
+  for (const MatrixRef& r : matrices(m)) {
+    hipError_t e = m->alloc(r.rowmajor, (size_t)(r.N * r.K));
+    if (e == hipSuccess)
+      e = launch_gemv_unpack(m->dev->stream, *r.packed, r.N, r.K, r.deferred, *r.rowmajor);
+    if (e != hipSuccess) return e;
+  }
+  m->rowmajor_live = true;
   return hipSuccess;
 }
 
@@ -1306,15 +1379,22 @@ ORION_EXPORT int orion_hip_model_forward(orion_hip_model* m, const orion_hip_bat
                      gemm_splitk_fusable(n, H, F);
   const int nslots = gemm_sumsq_slots(H);
   if (fused) HIP_TRY(st, m->sumsq.reserve(n * nslots * 8));
-  // Decode-shaped GEMMs (<= 64 rows) read the packed weight copies, made on
-  // the first such forward after a weight write.  ORION_GEMV_PACK=0 keeps
-  // them on the row-major matrices (A/B knob).
+  // Every GEMM reads the packed weight copies (the decode kernel's order),
+  // made on the first forward after a weight write, after which the row-major
+  // matrices are freed: one copy of each weight stays in HBM.
+  // ORION_GEMV_PACK=0 keeps the row-major matrices and reads them instead
+  // (A/B knob, read once).
   static const bool allow_pack = [] {
     const char* v = getenv("ORION_GEMV_PACK");
     return !(v && v[0] == '0');
   }();
-  const bool pack_layers = allow_pack && n <= 64, pack_head = allow_pack && S <= 64;
-  if ((pack_layers || pack_head) && !m->packs_valid) HIP_TRY(st, make_packs(m));
+  const bool pack_layers = allow_pack, pack_head = allow_pack;
+  if (allow_pack) {
+    if (!m->packs_valid) HIP_TRY(st, make_packs(m));
+    HIP_TRY(st, release_rowmajor(m));
+  } else {
+    HIP_TRY(st, ensure_rowmajor(m));
+  }
   // Attention routing, shared by every layer.  A sequence whose rows are a
   // chunk of consecutive positions with at least half a prefill tile of
   // (row, query head) pairs goes to the MFMA prefill kernel (bf16 arena);
@@ -1457,7 +1537,7 @@ ORION_EXPORT int orion_hip_model_forward(orion_hip_model* m, const orion_hip_bat
       qkv_x = xn;
     }
     qkv_f.defer = &part;
-    if (pack_layers) qkv_f.w_packed = L.p_qkv;
+    if (pack_layers) qkv_f.w_packed = L.p_qkv, qkv_f.w_packed_deferred = true;
     HIP_TRY(st, gemm_on(m->dev, qkv_x, L.w_qkv, L.b_qkv, n, m->qkvd, H, Epilogue::kStore, qkv,
                         &qkv_f));
     HIP_TRY(st, launch_rope_and_cache(stream, m->kv, m->arena, l, n, Hq, qkv, m->qkvd, qrot,
