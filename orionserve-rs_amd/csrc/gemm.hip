@@ -212,6 +212,9 @@ struct PackedGeom {
   int nt = 0, ks = 0, n_tiles = 0;  // columns per decode workgroup / 64, k-steps per slice
 };
 
+// HILO: x carried as a truncated hi + lo bf16 pair (two MFMAs, ~16 bits of
+// x per product); otherwise rounded to bf16 (nearest even, one MFMA).
+template <bool HILO>
 __global__ void __launch_bounds__(256)
     gemm_tiled_kernel(const float* __restrict__ x, const uint16_t* __restrict__ w,
                       const float* __restrict__ bias, int M, int N, int K, int ep,
@@ -320,11 +323,21 @@ __global__ void __launch_bounds__(256)
                           __uint_as_float(hi4.x), __uint_as_float(hi4.y),
                           __uint_as_float(hi4.z), __uint_as_float(hi4.w)};
       bf16x8 ahi, alo;
-      split8(a, ahi, alo);
+      if constexpr (HILO) {
+        split8(a, ahi, alo);
+      } else {
+        typedef __bf16 bf16x8v __attribute__((ext_vector_type(8)));
+        typedef float f32x8 __attribute__((ext_vector_type(8)));
+        const f32x8 av = {a[0], a[1], a[2], a[3], a[4], a[5], a[6], a[7]};
+        ahi = __builtin_bit_cast(bf16x8, __builtin_convertvector(av, bf16x8v));
+        (void)alo;
+      }
 #pragma unroll
       for (int nt = 0; nt < 4; ++nt) {
         acc[mt][nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ahi, bw[nt], acc[mt][nt], 0, 0, 0);
-        acc[mt][nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(alo, bw[nt], acc[mt][nt], 0, 0, 0);
+        if constexpr (HILO)
+          acc[mt][nt] =
+              __builtin_amdgcn_mfma_f32_16x16x32_bf16(alo, bw[nt], acc[mt][nt], 0, 0, 0);
       }
     }
     wait_vmem_all();
@@ -931,8 +944,17 @@ hipError_t launch_gemm(hipStream_t st, const float* x, const uint16_t* w, const 
       pk.n_tiles = gp.n_tiles;
     }
     dim3 grid((unsigned)((N + kTN - 1) / kTN), (unsigned)((M + kTM - 1) / kTM));
-    hipLaunchKernelGGL(gemm_tiled_kernel, grid, dim3(256), 0, st, x, f.w_packed ? f.w_packed : w,
-                       bias, (int)M, (int)N, (int)K, (int)ep, out, pk);
+    // ORION_GEMM_ACT=bf16 rounds the activations to bf16 (one MFMA per
+    // fragment) instead of the hi/lo pair (measurement knob, read per call).
+    const char* act = getenv("ORION_GEMM_ACT");
+    if (act && act[0] == 'b')
+      hipLaunchKernelGGL(gemm_tiled_kernel<false>, grid, dim3(256), 0, st, x,
+                         f.w_packed ? f.w_packed : w, bias, (int)M, (int)N, (int)K, (int)ep, out,
+                         pk);
+    else
+      hipLaunchKernelGGL(gemm_tiled_kernel<true>, grid, dim3(256), 0, st, x,
+                         f.w_packed ? f.w_packed : w, bias, (int)M, (int)N, (int)K, (int)ep, out,
+                         pk);
     return hipGetLastError();
   }
   // Rows per tile (MT x 16) and columns per tile (NT x 16): wide column tiles

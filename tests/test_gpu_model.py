@@ -503,3 +503,37 @@ def test_uncovered_head_dims_are_backend_errors(backend, d):
     spec = Spec(1, 256, 2, 1, d, 512, 100, num_blocks=8, block_size=16)
     with pytest.raises(oh.BackendError):
         oh.HipTransformerModel(meta_of(spec), 8, 16, backend, oh.F32)
+
+
+def test_weights_are_kept_once_and_read_back_after_packing(backend):
+    # After the first forward the layer matrices and LM head live only in the
+    # packed order (the row-major copies are freed); reading a weight back
+    # unpacks them bit-exactly, rewriting one invalidates the packs, and the
+    # logits follow.
+    spec = Spec(4, 1024, 8, 2, 128, 2816, 8000, max_pos=256, num_blocks=16, block_size=16)
+    gm = oh.HipTransformerModel(meta_of(spec), 16, 16, backend, oh.F32)
+    gm.init_synthetic(5, 0.02)
+    H, F = spec.H, spec.F
+    qd = spec.hq * spec.d
+    w_o = gm.download_weight(oh.W_O, 2, H * qd)
+    per_layer = (qd + 2 * spec.hkv * spec.d) * H + H * qd + 3 * F * H
+    weight_bytes = (spec.L * per_layer + spec.V * H) * 2
+    free0 = backend.available_memory()
+    toks, pos = [1, 2, 3], [0, 1, 2]
+    b = batch(toks, pos, [3], [[0]])
+    g1 = gm.forward(b).logits
+    backend.synchronize()
+    free1 = backend.available_memory()
+    print(f"[one layout] weights {weight_bytes / 1e6:.0f} MB, free before {free0 / 1e9:.2f} GB, "
+          f"after the first forward {free1 / 1e9:.2f} GB", flush=True)
+    # packed copies replaced the row-major ones: far less than a second copy
+    assert free0 - free1 < weight_bytes // 2
+    assert np.array_equal(gm.download_weight(oh.W_O, 2, H * qd).view(np.uint32),
+                          w_o.view(np.uint32))
+    assert np.array_equal(gm.forward(b).logits, g1)
+    gm.upload_weight(oh.W_O, 2, np.zeros(H * qd, np.float32))
+    g2 = gm.forward(b).logits
+    assert not np.array_equal(g2, g1)
+    gm.upload_weight(oh.W_O, 2, w_o)
+    assert np.array_equal(gm.forward(b).logits, g1)
+    gm.close()
