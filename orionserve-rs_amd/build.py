@@ -16,6 +16,7 @@ HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 
 SOURCES = [
     "attention_decode.hip",
+    "decode_plan.cpp",
     "attention_prefill.hip",
     "gemm.hip",
     "elementwise.hip",

@@ -27,8 +27,6 @@
 #include "kernels.hpp"
 
 #include <algorithm>
-#include <cstdlib>
-#include <functional>
 #include <type_traits>
 #include <vector>
 
@@ -231,7 +229,7 @@ __global__ void __launch_bounds__(256)
                         const DecodeWork* __restrict__ work, int num_work, const float* __restrict__ q,
                         const uint32_t* __restrict__ positions, const int32_t* __restrict__ row_seq,
                         const int64_t* __restrict__ bt_off, const uint32_t* __restrict__ bt_ids,
-                        int chunk, int max_splits, float scale, float* __restrict__ out,
+                        int max_splits, float scale, float* __restrict__ out,
                         float* __restrict__ ws_o, float* __restrict__ ws_ml) {
   const int w = blockIdx.x * 4 + (threadIdx.x >> 6);
   if (w >= num_work) return;
@@ -240,7 +238,7 @@ __global__ void __launch_bounds__(256)
   decode_wave_valu<T, D, G>(kv_layer, blk_stride, v_off, slot_stride, head_stride, bs_log2,
                             num_q_heads, q,
                             bt_ids + wk.tbl_off, max_splits, scale, out, ws_o, ws_ml, row, kvh,
-                            wk.start, wk.end, wk.start / chunk, wk.nsplit);
+                            wk.start, wk.end, wk.split, wk.nsplit);
 }
 
 // Second-generation bf16 decode wave: both contractions on MFMA.
@@ -513,7 +511,7 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3)))
                               const float* __restrict__ q, const uint32_t* __restrict__ positions,
                               const int32_t* __restrict__ row_seq,
                               const int64_t* __restrict__ bt_off,
-                              const uint32_t* __restrict__ bt_ids, int chunk, int max_splits,
+                              const uint32_t* __restrict__ bt_ids, int max_splits,
                               float scale, float* __restrict__ out, float* __restrict__ ws_o,
                               float* __restrict__ ws_ml) {
   __shared__ __attribute__((aligned(16))) uint16_t lds_v[4][16 * (D + 8)];
@@ -528,7 +526,7 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3)))
     decode_wave_mfma2<D, G, decltype(stream_tag)::value, BIG_BLOCKS>(
         kv_layer, blk_stride, v_off, slot_stride, head_stride, bs_log2, num_q_heads, q,
         bt_ids + wk.tbl_off, wk.blk0, max_splits, scale, out, ws_o, ws_ml, lds_v[wv], lds_q[wv],
-        lds_k[wv], row, kvh, wk.start, wk.end, wk.start / chunk, wk.nsplit);
+        lds_k[wv], row, kvh, wk.start, wk.end, wk.split, wk.nsplit);
   };
   if constexpr (KV == 2) {
     if (__builtin_amdgcn_readfirstlane(wk.shared))
@@ -546,9 +544,10 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3)))
 // before any reduction, so the merge costs one memory round trip.
 template <int D>
 __global__ void __launch_bounds__(256)
-    paged_decode_combine_kernel(int num_rows, int num_q_heads, const uint32_t* __restrict__ positions,
+    paged_decode_combine_kernel(int num_rows, int num_q_heads,
+                                const int32_t* __restrict__ row_nsplit,
                                 const int32_t* __restrict__ row_list,
-                                int partition, int max_splits, const float* __restrict__ ws_o,
+                                int max_splits, const float* __restrict__ ws_o,
                                 const float* __restrict__ ws_ml, float* __restrict__ out) {
   constexpr int PER = D / 64;
   constexpr int MAXS = 16;
@@ -559,8 +558,7 @@ __global__ void __launch_bounds__(256)
   const int li = (int)(slot / num_q_heads);
   const int row = row_list ? row_list[li] : li;
   const int64_t item = (int64_t)row * num_q_heads + (slot - (int64_t)li * num_q_heads);
-  const int len = (int)positions[row] + 1;
-  const int nsplit = (len + partition - 1) / partition;
+  const int nsplit = row_nsplit[row];
   if (nsplit <= 1) return;
   const float* ml = ws_ml + item * max_splits * 2;
   const float* ob = ws_o + item * max_splits * D;
@@ -650,7 +648,7 @@ __global__ void __launch_bounds__(256)
                             int num_kv_heads, int num_q_heads, int D,
                             const DecodeWork* __restrict__ work, int num_work,
                             const float* __restrict__ q, const uint32_t* __restrict__ bt_ids,
-                            int chunk, int max_splits, float scale, float* __restrict__ out,
+                            int max_splits, float scale, float* __restrict__ out,
                             float* __restrict__ ws_o, float* __restrict__ ws_ml) {
   const int w = blockIdx.x * 4 + (threadIdx.x >> 6);
   if (w >= num_work) return;
@@ -661,7 +659,7 @@ __global__ void __launch_bounds__(256)
   const int d0 = 2 * lane, d1 = 128 + 2 * lane;
   const bool has0 = d0 < D, has1 = d1 < D;
   const int start = wk.start, end = wk.end;
-  const int split = start / chunk;
+  const int split = wk.split;
   const int bs_mask = (1 << bs_log2) - 1;
   const int first_blk = start >> bs_log2;
   const int nblk = ((end - 1) >> bs_log2) - first_blk + 1;
@@ -733,8 +731,8 @@ __global__ void __launch_bounds__(256)
 // (row, query head), splits in order, lane l holding dimensions l + 64 i.
 __global__ void __launch_bounds__(256)
     paged_decode_combine_any_kernel(int num_rows, int num_q_heads, int D,
-                                    const uint32_t* __restrict__ positions,
-                                    const int32_t* __restrict__ row_list, int partition,
+                                    const int32_t* __restrict__ row_nsplit,
+                                    const int32_t* __restrict__ row_list,
                                     int max_splits, const float* __restrict__ ws_o,
                                     const float* __restrict__ ws_ml, float* __restrict__ out) {
   const int lane = threadIdx.x & 63;
@@ -743,8 +741,7 @@ __global__ void __launch_bounds__(256)
   const int li = (int)(slot / num_q_heads);
   const int row = row_list ? row_list[li] : li;
   const int64_t item = (int64_t)row * num_q_heads + (slot - (int64_t)li * num_q_heads);
-  const int len = (int)positions[row] + 1;
-  const int nsplit = (len + partition - 1) / partition;
+  const int nsplit = row_nsplit[row];
   if (nsplit <= 1) return;
   const float* ml = ws_ml + item * max_splits * 2;
   const float* ob = ws_o + item * max_splits * D;
@@ -767,154 +764,20 @@ __global__ void __launch_bounds__(256)
 }
 
 // ---------------------------------------------------------------------------
-// Host side: decode plans and launch
+// Host side: launch (the work list comes from decode_plan.cpp)
 // ---------------------------------------------------------------------------
-
-// Decode work decomposition.  A work item is (row, KV head, chunk of the
-// row's context) and runs on one wave.  All full chunks come first and the
-// partial tail chunks last, longest first, so the final waves to be
-// dispatched are the shortest.  The chunk length C is chosen with a fluid
-// model of the split kernel, in token-equivalents of one wave's streaming:
-//   time(C) = max((sum of item sizes + items * kItemOverhead) / wave_slots
-//                 + C / 2,                       (bandwidth-bound, mean tail)
-//                 largest item + kItemOverhead)  (latency-bound: one wave)
-// The per-item overhead (setup, split-K partial write and merge read) and the
-// half-item tail were fitted to the measured config-2 times at C = 128 ...
-// 1024 (best: 256).
-static int64_t estimate_split_time(const std::vector<int>& lens, int64_t hkv, int C,
-                                   int64_t slots) {
-  constexpr int64_t kItemOverhead = 96;
-  int64_t total = 0, items = 0, largest = 0;
-  for (int L : lens) {
-    const int64_t full = L / C, tail = L % C;
-    items += hkv * (full + (tail ? 1 : 0));
-    total += (int64_t)hkv * L;
-    largest = std::max<int64_t>(largest, full ? C : tail);
-  }
-  if (items == 0) return 0;
-  const int64_t fluid = (total + items * kItemOverhead) / std::max<int64_t>(slots, 1) +
-                        std::min<int64_t>(C, largest) / 2;
-  return std::max(fluid, largest + kItemOverhead);
-}
-
-void build_decode_plan(const uint32_t* positions, const int32_t* row_seq,
-                       const int64_t* bt_offsets, const uint32_t* bt_ids, int64_t rows,
-                       int64_t hkv, int64_t block_size, int64_t wave_slots,
-                       const uint8_t* skip_rows, DecodePlanHost* plan) {
-  int bs_log2 = 0;
-  while ((1 << bs_log2) < block_size) ++bs_log2;
-  // Rows flagged in skip_rows get no work (another kernel covers them);
-  // their length counts as 0 for the chunk choice and the split bound.
-  std::vector<int> lens(rows);
-  int max_len = 0;
-  plan->rows.clear();
-  for (int64_t r = 0; r < rows; ++r) {
-    const bool skip = skip_rows && skip_rows[r];
-    lens[r] = skip ? 0 : (int)positions[r] + 1;
-    max_len = std::max(max_len, lens[r]);
-    if (skip_rows && !skip) plan->rows.push_back((int32_t)r);
-  }
-  int best_c = 0;
-  int64_t best_t = 0;
-  for (int C = 64; C <= 2048; C <<= 1) {
-    if (C < block_size || C / block_size > 64) continue;
-    const int64_t t = estimate_split_time(lens, hkv, C, wave_slots);
-    if (best_c == 0 || t < best_t) {
-      best_c = C;
-      best_t = t;
-    }
-  }
-  if (best_c == 0) best_c = (int)std::max<int64_t>(block_size, 64);
-  // ORION_DECODE_CHUNK overrides the choice (measurement knob).
-  static const int forced = [] {
-    const char* e = getenv("ORION_DECODE_CHUNK");
-    return e ? atoi(e) : 0;
-  }();
-  if (forced >= 16 && (forced & (forced - 1)) == 0 && forced >= block_size &&
-      forced / block_size <= 64)
-    best_c = forced;
-  const int C = best_c;
-  plan->chunk = C;
-  plan->max_splits = rows ? (max_len + C - 1) / C : 0;
-  plan->work.clear();
-  auto push = [&](int64_t r, int start) {
-    const int len = lens[r];
-    const int64_t tbl_off = bt_offsets[row_seq[r]] + (start >> bs_log2);
-    const int nsplit = (len + C - 1) / C;
-    for (int64_t h = 0; h < hkv; ++h)
-      plan->work.push_back({(int32_t)(r * hkv + h), start, std::min(len, start + C), nsplit,
-                            (int32_t)tbl_off, (int32_t)bt_ids[tbl_off], 0, 0});
-  };
-  std::vector<std::pair<int, int>> tails;  // (tail length, row)
-  for (int64_t r = 0; r < rows; ++r) {
-    const int full = lens[r] / C;
-    for (int s = 0; s < full; ++s) push(r, s * C);
-    if (lens[r] % C) tails.push_back({lens[r] % C, (int)r});
-  }
-  std::stable_sort(tails.begin(), tails.end(),
-                   [](const std::pair<int, int>& a, const std::pair<int, int>& b) {
-                     return a.first > b.first;
-                   });
-  for (const auto& t : tails) push(t.second, (lens[t.second] / C) * C);
-  // Shared blocks: a block id attended by two planned rows (two rows of one
-  // sequence share their prefix blocks too).  One pass over the attended
-  // ids with two bitmaps (seen, seen again) that are cleared afterwards;
-  // then each work item is flagged when its token range reads a shared
-  // block.
-  static thread_local std::vector<uint64_t> seen, again;
-  bool shared = false;
-  auto attended = [&](auto&& f) {
-    for (int64_t r = 0; r < rows; ++r) {
-      if (lens[r] == 0) continue;
-      const int64_t o = bt_offsets[row_seq[r]];
-      const int64_t nb = ((int64_t)lens[r] + block_size - 1) >> bs_log2;
-      for (int64_t j = 0; j < nb; ++j) f(bt_ids[o + j]);
-    }
-  };
-  attended([&](uint32_t id) {
-    const size_t w = id >> 6;
-    if (w >= seen.size()) seen.resize(w + 1, 0), again.resize(w + 1, 0);
-    const uint64_t bit = 1ull << (id & 63);
-    if (seen[w] & bit) {
-      again[w] |= bit;
-      shared = true;
-    }
-    seen[w] |= bit;
-  });
-  int64_t shared_items = 0;
-  if (shared) {
-    for (DecodeWork& wk : plan->work) {
-      const int nb = ((wk.end - 1) >> bs_log2) - (wk.start >> bs_log2) + 1;
-      bool s = false;
-      for (int j = 0; j < nb && !s; ++j) {
-        const uint32_t id = bt_ids[wk.tbl_off + j];
-        s = (again[id >> 6] >> (id & 63)) & 1;
-      }
-      wk.shared = s ? 1 : 0;
-      shared_items += s;
-    }
-  }
-  attended([&](uint32_t id) { seen[id >> 6] = 0, again[id >> 6] = 0; });
-  plan->stream_kv = !shared;
-  plan->mixed_kv = shared && shared_items < (int64_t)plan->work.size();
-}
-
-size_t decode_workspace_bytes(int64_t rows, int64_t hq, int64_t D, int64_t max_splits) {
-  if (max_splits <= 1) return 0;
-  return (size_t)(rows * hq * max_splits) * (size_t)(D + 2) * sizeof(float);
-}
 
 template <typename T, int D>
 static hipError_t launch_valu(int G, dim3 grid, hipStream_t st, const T* kv, const ArenaStrides& a,
                               int bsl, int hkv, int hq, const DecodeWork* work, int nwork,
                               const float* q, const uint32_t* pos, const int32_t* rs,
-                              const int64_t* bo, const uint32_t* bi, int C, int ms, float scale,
+                              const int64_t* bo, const uint32_t* bi, int ms, float scale,
                               float* out, float* wo, float* wml) {
 #define ORION_VALU_CASE(GG)                                                                   \
   case GG:                                                                                    \
     hipLaunchKernelGGL((paged_decode_kernel<T, D, GG>), grid, dim3(256), 0, st, kv, a.blk,    \
                        a.v_off, a.slot, a.head, bsl, hkv, hq, work, nwork, q, pos, rs, bo, bi, \
-                       C, ms, scale, out, wo, wml);                                           \
+                       ms, scale, out, wo, wml);                                              \
     break;
   switch (G) {
     ORION_VALU_CASE(1)
@@ -937,14 +800,14 @@ static hipError_t launch_mfma2(int G, dim3 grid, hipStream_t st, const uint16_t*
                                const ArenaStrides& a, int bsl, int hkv, int hq,
                                const DecodeWork* work, int nwork, const float* q,
                                const uint32_t* pos, const int32_t* rs, const int64_t* bo,
-                               const uint32_t* bi, int C, int ms, float scale, float* out,
+                               const uint32_t* bi, int ms, float scale, float* out,
                                float* wo, float* wml) {
 #define ORION_MFMA2_CASE(GG)                                                                   \
   case GG:                                                                                     \
     hipLaunchKernelGGL((paged_decode_mfma2_kernel<D, GG, KV, BIG>), grid, dim3(256), 0, st,     \
                        kv,                                                                     \
                        (uint32_t)a.blk, (uint32_t)a.v_off, (uint32_t)a.slot, (uint32_t)a.head, \
-                       bsl, hkv, hq, work, nwork, q, pos, rs, bo, bi, C, ms, scale, out, wo,   \
+                       bsl, hkv, hq, work, nwork, q, pos, rs, bo, bi, ms, scale, out, wo,      \
                        wml);                                                                   \
     break;
   switch (G) {
@@ -965,20 +828,20 @@ static hipError_t launch_mfma2(int G, dim3 grid, hipStream_t st, const uint16_t*
 
 // Merges the split-K partials of every row (or of plan.rows) into out.
 static hipError_t launch_combine(hipStream_t st, int64_t D, int64_t rows, int64_t hq,
-                                 const uint32_t* positions, const DecodePlanDev& plan, int C,
-                                 int ms, const float* ws_o, const float* ws_ml, float* out) {
+                                 const DecodePlanDev& plan, int ms, const float* ws_o,
+                                 const float* ws_ml, float* out) {
   const int64_t nr = plan.rows ? plan.num_rows : rows;
   if (nr == 0) return hipSuccess;
   dim3 cgrid((unsigned)((nr * hq + 3) / 4));
   if (D != 64 && D != 128)
     hipLaunchKernelGGL(paged_decode_combine_any_kernel, cgrid, dim3(256), 0, st, (int)nr,
-                       (int)hq, (int)D, positions, plan.rows, C, ms, ws_o, ws_ml, out);
+                       (int)hq, (int)D, plan.row_nsplit, plan.rows, ms, ws_o, ws_ml, out);
   else if (D == 128)
     hipLaunchKernelGGL(paged_decode_combine_kernel<128>, cgrid, dim3(256), 0, st, (int)nr,
-                       (int)hq, positions, plan.rows, C, ms, ws_o, ws_ml, out);
+                       (int)hq, plan.row_nsplit, plan.rows, ms, ws_o, ws_ml, out);
   else
     hipLaunchKernelGGL(paged_decode_combine_kernel<64>, cgrid, dim3(256), 0, st, (int)nr,
-                       (int)hq, positions, plan.rows, C, ms, ws_o, ws_ml, out);
+                       (int)hq, plan.row_nsplit, plan.rows, ms, ws_o, ws_ml, out);
   return hipGetLastError();
 }
 
@@ -991,14 +854,14 @@ hipError_t launch_paged_decode(hipStream_t st, const KvGeom& kv, const void* are
   const int64_t hkv = kv.num_kv_heads, D = kv.head_dim;
   if (hkv <= 0 || hq % hkv != 0) return hipErrorInvalidValue;
   const int G = (int)(hq / hkv);
-  const int C = plan.chunk, ms = plan.max_splits;
+  const int ms = plan.max_splits;
   if (ms > 1 && plan.ws_bytes < decode_workspace_bytes(rows, hq, D, ms))
     return hipErrorInvalidValue;
   float* ws_o = plan.ws;
   float* ws_ml = ws_o ? ws_o + rows * hq * ms * D : nullptr;
   if (phase == DecodePhase::kMerge) {
     if (ms <= 1) return hipSuccess;
-    return launch_combine(st, D, rows, hq, positions, plan, C, ms, ws_o, ws_ml, out);
+    return launch_combine(st, D, rows, hq, plan, ms, ws_o, ws_ml, out);
   }
   int bs_log2 = 0;
   while ((1 << bs_log2) < kv.block_size) ++bs_log2;
@@ -1012,12 +875,12 @@ hipError_t launch_paged_decode(hipStream_t st, const KvGeom& kv, const void* are
       hipLaunchKernelGGL(paged_decode_any_kernel<uint16_t>, grid, dim3(256), 0, st,
                          static_cast<const uint16_t*>(arena) + layer * a.layer, a.blk, a.v_off,
                          a.slot, a.head, bs_log2, (int)hkv, (int)hq, (int)D, plan.work,
-                         plan.num_work, q, bt_ids, C, ms, scale, out, ws_o, ws_ml);
+                         plan.num_work, q, bt_ids, ms, scale, out, ws_o, ws_ml);
     else
       hipLaunchKernelGGL(paged_decode_any_kernel<float>, grid, dim3(256), 0, st,
                          static_cast<const float*>(arena) + layer * a.layer, a.blk, a.v_off,
                          a.slot, a.head, bs_log2, (int)hkv, (int)hq, (int)D, plan.work,
-                         plan.num_work, q, bt_ids, C, ms, scale, out, ws_o, ws_ml);
+                         plan.num_work, q, bt_ids, ms, scale, out, ws_o, ws_ml);
     e = hipGetLastError();
   } else if (kv.dtype_bf16) {
     if (a.layer > (int64_t)UINT32_MAX) return hipErrorInvalidValue;
@@ -1025,7 +888,7 @@ hipError_t launch_paged_decode(hipStream_t st, const KvGeom& kv, const void* are
     const bool big = kv.block_size >= 16;
 #define ORION_MFMA2(DD, SS, BB)                                                                      \
   launch_mfma2<DD, SS, BB>(G, grid, st, base, a, bs_log2, (int)hkv, (int)hq, plan.work,          \
-                       plan.num_work, q, positions, row_seq, bt_off, bt_ids, C, ms, scale, out, \
+                       plan.num_work, q, positions, row_seq, bt_off, bt_ids, ms, scale, out,    \
                        ws_o, ws_ml)
     // per-item load flavour only with whole-block steps (blocks of >= 16 slots)
     const int kvm = plan.stream_kv ? 1 : (plan.mixed_kv && big) ? 2 : 0;
@@ -1044,17 +907,17 @@ hipError_t launch_paged_decode(hipStream_t st, const KvGeom& kv, const void* are
     const float* base = static_cast<const float*>(arena) + layer * a.layer;
     if (D == 128)
       e = launch_valu<float, 128>(G, grid, st, base, a, bs_log2, (int)hkv, (int)hq, plan.work,
-                                  plan.num_work, q, positions, row_seq, bt_off, bt_ids, C, ms,
+                                  plan.num_work, q, positions, row_seq, bt_off, bt_ids, ms,
                                   scale, out, ws_o, ws_ml);
     else if (D == 64)
       e = launch_valu<float, 64>(G, grid, st, base, a, bs_log2, (int)hkv, (int)hq, plan.work,
-                                 plan.num_work, q, positions, row_seq, bt_off, bt_ids, C, ms,
+                                 plan.num_work, q, positions, row_seq, bt_off, bt_ids, ms,
                                  scale, out, ws_o, ws_ml);
     else
       return hipErrorInvalidValue;
   }
   if (e != hipSuccess || ms == 1 || phase == DecodePhase::kSplit) return e;
-  return launch_combine(st, D, rows, hq, positions, plan, C, ms, ws_o, ws_ml, out);
+  return launch_combine(st, D, rows, hq, plan, ms, ws_o, ws_ml, out);
 }
 
 }  // namespace orion

@@ -42,19 +42,22 @@ inline ArenaStrides arena_strides(const KvGeom& kv) {
 
 // ---- attention --------------------------------------------------------------
 // One decode work item: KV head `item % Hkv` of query row `item / Hkv` over
-// context tokens [start, end).  The block table slice of the chunk starts at
-// block_table_ids[tbl_off]; blk0 is its first entry, so the first step's loads
-// can be issued before the slice arrives.
+// context tokens [start, end), the row's piece `split` of `nsplit`.  The block
+// table slice of the piece starts at block_table_ids[tbl_off]; blk0 is its
+// first entry, so the first step's loads can be issued before the slice
+// arrives.
 struct DecodeWork {
   // shared: the item reads a block that another planned row also reads
-  int32_t item, start, end, nsplit, tbl_off, blk0, shared, pad1;
+  int32_t item, start, end, nsplit, tbl_off, blk0, shared, split;
 };
 // Decode work plan: items in longest-first order; built on the host from the
 // query positions and block tables, shared by every layer of a forward.
 struct DecodePlanHost {
-  int chunk = 0;       // tokens per chunk (power of two)
-  int max_splits = 0;  // chunks of the longest row
+  int chunk = 0;       // longest piece, in tokens
+  int max_splits = 0;  // most pieces of any row
+  bool balanced = false;  // per-row piece lengths (else fixed chunks)
   std::vector<DecodeWork> work;
+  std::vector<int32_t> row_nsplit;  // pieces per row (0: row not planned)
   std::vector<int32_t> rows;  // rows covered when a skip mask was given (else all)
   // No block is attended by two planned rows: K/V are then read once and
   // streamed past the caches; shared (prefix) blocks keep cached loads.
@@ -65,6 +68,7 @@ struct DecodePlanHost {
 };
 struct DecodePlanDev {
   const DecodeWork* work = nullptr;
+  const int32_t* row_nsplit = nullptr;  // DecodePlanHost::row_nsplit on the device
   int num_work = 0;
   int chunk = 0;
   int max_splits = 0;

@@ -189,6 +189,8 @@ struct orion_hip_decode_plan {
   DecodePlanDev view() const {
     DecodePlanDev d;
     d.work = work.as<const DecodeWork>();
+    d.row_nsplit = reinterpret_cast<const int32_t*>(
+        work.as<const char>() + host.work.size() * sizeof(DecodeWork));
     d.num_work = (int)host.work.size();
     d.chunk = host.chunk;
     d.max_splits = host.max_splits;
@@ -1443,7 +1445,8 @@ ORION_EXPORT int orion_hip_model_forward(orion_hip_model* m, const orion_hip_bat
   const size_t o_btoff = (o_last + S * 4 + 7) & ~(size_t)7;
   const size_t o_btids = o_btoff + (S + 1) * 8;
   const size_t o_work = (o_btids + nbt * 4 + 31) & ~(size_t)31;
-  const size_t o_pfoff = (o_work + plan.work.size() * sizeof(DecodeWork) + 7) & ~(size_t)7;
+  const size_t o_nsplit = o_work + plan.work.size() * sizeof(DecodeWork);
+  const size_t o_pfoff = (o_nsplit + plan.row_nsplit.size() * 4 + 7) & ~(size_t)7;
   const size_t o_pfstart = o_pfoff + npf * 8;
   const size_t o_pfcount = o_pfstart + npf * 4;
   const size_t o_pfpos = o_pfcount + npf * 4;
@@ -1470,6 +1473,7 @@ ORION_EXPORT int orion_hip_model_forward(orion_hip_model* m, const orion_hip_bat
   std::memcpy(hp + o_btoff, b->block_table_offsets, (S + 1) * 8);
   std::memcpy(hp + o_btids, b->block_table_ids, nbt * 4);
   std::memcpy(hp + o_work, plan.work.data(), plan.work.size() * sizeof(DecodeWork));
+  std::memcpy(hp + o_nsplit, plan.row_nsplit.data(), plan.row_nsplit.size() * 4);
   std::memcpy(hp + o_pfoff, pf_btoff.data(), npf * 8);
   std::memcpy(hp + o_pfstart, pf_start.data(), npf * 4);
   std::memcpy(hp + o_pfcount, pf_count.data(), npf * 4);
@@ -1486,6 +1490,7 @@ ORION_EXPORT int orion_hip_model_forward(orion_hip_model* m, const orion_hip_bat
   const uint32_t* d_btids = reinterpret_cast<const uint32_t*>(dp + o_btids);
   DecodePlanDev dplan;
   dplan.work = reinterpret_cast<const DecodeWork*>(dp + o_work);
+  dplan.row_nsplit = reinterpret_cast<const int32_t*>(dp + o_nsplit);
   dplan.num_work = (int)plan.work.size();
   dplan.chunk = plan.chunk;
   dplan.max_splits = plan.max_splits;
@@ -1636,10 +1641,15 @@ ORION_EXPORT int orion_hip_decode_plan_create(orion_hip_device* dev, const uint3
   }
   build_decode_plan(positions, row_seq, block_table_offsets, block_table_ids, num_rows,
                     num_kv_heads, block_size, dev->wave_slots, nullptr, &p->host);
+  // work items, then the pieces per row, in one buffer
   const size_t wbytes = p->host.work.size() * sizeof(DecodeWork);
-  HIP_TRY(st, p->work.reserve(wbytes));
-  if (wbytes)
-    HIP_TRY(st, hipMemcpyAsync(p->work.ptr, p->host.work.data(), wbytes, hipMemcpyHostToDevice,
+  const size_t nbytes = p->host.row_nsplit.size() * sizeof(int32_t);
+  HIP_TRY(st, p->work.reserve(wbytes + nbytes));
+  std::vector<char> staged(wbytes + nbytes);
+  std::memcpy(staged.data(), p->host.work.data(), wbytes);
+  std::memcpy(staged.data() + wbytes, p->host.row_nsplit.data(), nbytes);
+  if (!staged.empty())
+    HIP_TRY(st, hipMemcpyAsync(p->work.ptr, staged.data(), staged.size(), hipMemcpyHostToDevice,
                                dev->stream));
   HIP_TRY(st, p->ws.reserve(
                   decode_workspace_bytes(num_rows, num_q_heads, head_dim, p->host.max_splits)));

@@ -1,0 +1,110 @@
+// Property check of the decode work planner (orionserve-rs_amd/csrc/
+// decode_plan.cpp), host only.  For random batches (rows, contexts, block
+// sizes, KV heads, wave slots, skipped rows) every plan must:
+//   * cover each planned (row, KV head) context [0, position] exactly once,
+//     and plan nothing for a skipped row;
+//   * give each piece a 16-token-aligned start, at most 64 table entries, the
+//     table offset of its first block, and split indices 0 .. n-1 of the
+//     row's n = row_nsplit pieces, with n <= max_splits;
+//   * cut every row into pieces of one length, the last piece no longer;
+//   * when balanced, fit in one round of wave slots.
+// Prints one line per failure and a summary; exit status 1 on any failure.
+#include "kernels.hpp"
+
+#include <algorithm>
+#include <cstdio>
+#include <map>
+#include <random>
+#include <vector>
+
+using orion::DecodePlanHost;
+using orion::DecodeWork;
+
+int main(int argc, char** argv) {
+  const int trials = argc > 1 ? atoi(argv[1]) : 2000;
+  std::mt19937 rng(20261202);
+  int fails = 0, balanced = 0;
+  auto fail = [&](int trial, const char* what, int row) {
+    if (fails++ < 20) printf("trial %d: %s (row %d)\n", trial, what, row);
+  };
+  for (int trial = 0; trial < trials; ++trial) {
+    const int rows = 1 + rng() % 200;
+    const int bs = 1 << (rng() % 9);  // 1 .. 256
+    const int hkv = 1 + rng() % 8;
+    const int64_t slots = (trial % 3 == 0) ? 2048 : (64 + rng() % 4000);
+    const int maxctx = (trial % 4 == 0) ? 16384 : (trial % 4 == 1 ? 64 : 4096);
+    std::vector<uint32_t> pos(rows);
+    std::vector<int32_t> row_seq(rows);
+    std::vector<int64_t> off(rows + 1, 0);
+    std::vector<uint32_t> ids;
+    for (int r = 0; r < rows; ++r) {
+      pos[r] = rng() % maxctx;
+      row_seq[r] = r;
+      const int nb = (int)pos[r] / bs + 1;
+      for (int j = 0; j < nb; ++j) ids.push_back(rng() % 100000);
+      off[r + 1] = off[r] + nb;
+    }
+    std::vector<uint8_t> skip(rows, 0);
+    const bool use_skip = trial % 5 == 0;
+    if (use_skip)
+      for (int r = 0; r < rows; ++r) skip[r] = rng() % 3 == 0;
+    DecodePlanHost plan;
+    orion::build_decode_plan(pos.data(), row_seq.data(), off.data(), ids.data(), rows, hkv, bs,
+                             slots, use_skip ? skip.data() : nullptr, &plan);
+    balanced += plan.balanced;
+    int bs_log2 = 0;
+    while ((1 << bs_log2) < bs) ++bs_log2;
+    std::map<int, std::vector<std::pair<int, int>>> cover;  // item -> [start, end)
+    std::map<std::pair<int, int>, int> seen_split;
+    for (const DecodeWork& w : plan.work) {
+      const int row = w.item / hkv;
+      if (row < 0 || row >= rows) {
+        fail(trial, "row out of range", row);
+        continue;
+      }
+      const int nblk = ((w.end - 1) >> bs_log2) - (w.start >> bs_log2) + 1;
+      if (w.start % 16 || w.end <= w.start || nblk > 64) fail(trial, "bad piece bounds", row);
+      if (w.tbl_off != off[row] + (w.start >> bs_log2) || (uint32_t)w.blk0 != ids[w.tbl_off])
+        fail(trial, "bad table slice", row);
+      if (w.nsplit != plan.row_nsplit[row] || w.split < 0 || w.split >= w.nsplit ||
+          w.nsplit > plan.max_splits)
+        fail(trial, "bad split index", row);
+      if (seen_split[{w.item, w.split}]++) fail(trial, "split index repeated", row);
+      cover[w.item].push_back({w.start, w.end});
+    }
+    for (int r = 0; r < rows; ++r) {
+      const bool planned = !(use_skip && skip[r]);
+      if (!planned && plan.row_nsplit[r] != 0) fail(trial, "skipped row has pieces", r);
+      for (int h = 0; h < hkv; ++h) {
+        auto it = cover.find(r * hkv + h);
+        if (!planned) {
+          if (it != cover.end()) fail(trial, "skipped row planned", r);
+          continue;
+        }
+        if (it == cover.end()) {
+          fail(trial, "row not planned", r);
+          continue;
+        }
+        auto v = it->second;
+        std::sort(v.begin(), v.end());
+        int at = 0, lo = 1 << 30, hi = 0;
+        for (size_t i = 0; i < v.size(); ++i) {
+          if (v[i].first != at) fail(trial, "gap or overlap", r);
+          at = v[i].second;
+          if (i + 1 < v.size()) {  // all but the last piece
+            lo = std::min(lo, v[i].second - v[i].first);
+            hi = std::max(hi, v[i].second - v[i].first);
+          }
+        }
+        if (at != (int)pos[r] + 1) fail(trial, "context not covered", r);
+        if ((int)v.size() != plan.row_nsplit[r]) fail(trial, "row_nsplit mismatch", r);
+        if (v.size() > 1 && (lo != hi || v.back().second - v.back().first > hi))
+          fail(trial, "uneven pieces", r);
+      }
+    }
+    if (plan.balanced && (int64_t)plan.work.size() > slots)
+      fail(trial, "balanced plan overfills one round", -1);
+  }
+  printf("%d trials, %d balanced, %d failures\n", trials, balanced, fails);
+  return fails ? 1 : 0;
+}

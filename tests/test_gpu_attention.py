@@ -51,6 +51,35 @@ def test_cfg2_full_size_bf16_kv(backend, head_major):
     assert err <= 1e-4, err          # what f32 accumulation over exact bf16 values gives
 
 
+@pytest.mark.parametrize("which", ["cfg2", "few_long_rows"])
+def test_balanced_and_fixed_plans_agree(backend, monkeypatch, which):
+    # The planner cuts each row into equal pieces that fit one round of wave
+    # slots (the default) or into fixed power-of-two chunks
+    # (ORION_DECODE_BALANCE=0).  Both must match the oracle; their split
+    # boundaries differ, so they agree to f32 rounding, not bit for bit.
+    # few_long_rows: rows of 16,384 and 12,000 tokens over 8 KV heads are cut
+    # into more than 64 pieces per row (the merge's general path).
+    case = cfg2() if which == "cfg2" else PagedCase(77, [16384, 12000], 32, 8, 128, 16,
+                                                    dtype="bf16")
+    want = case.oracle()
+    outs, infos = {}, {}
+    for bal in ("1", "0"):
+        monkeypatch.setenv("ORION_DECODE_BALANCE", bal)
+        plan = oh.DecodePlan(backend, case.positions, case.row_seq, case.bt_offsets,
+                             case.bt_ids, case.hq, case.hkv, case.d, case.bs)
+        infos[bal] = plan.info()
+        plan.close()
+        outs[bal] = run_decode(backend, case)
+        err = float(np.abs(outs[bal] - want).max())
+        print(f"[plans] {which} balance={bal} {infos[bal]} err {err:.2e}", flush=True)
+        assert err <= 1e-4, (bal, err)
+    assert np.abs(outs["1"] - outs["0"]).max() <= 2e-5
+    if which == "cfg2":
+        assert infos["1"]["num_work"] <= 2048 < infos["0"]["num_work"]
+    else:
+        assert infos["1"]["max_splits"] > 64
+
+
 @pytest.mark.parametrize("hq,hkv,d,bs,dtype", [
     (8, 8, 64, 16, "f32"), (16, 8, 128, 16, "bf16"), (12, 4, 128, 8, "bf16"),
     (28, 4, 128, 16, "bf16"), (32, 4, 64, 16, "bf16"), (20, 4, 64, 32, "f32"),
