@@ -14,8 +14,9 @@ namespace orion {
 // merged afterwards by the combine kernel.  Items are ordered longest first,
 // so the last waves to be dispatched are the shortest.  Two ways to cut:
 //  * balanced (the default when it applies): each row is cut into equal
-//    pieces, as few as keep every item within one round of the resident wave
-//    slots (see build_decode_plan);
+//    pieces, as few as keep the items within one round of the resident wave
+//    slots (or within R rounds when one cannot hold them; see
+//    build_decode_plan);
 //  * fixed chunks of C tokens, C a power of two chosen with a fluid model of
 //    the split kernel, in token-equivalents of one wave's streaming:
 //      time(C) = max((sum of item sizes + items * kItemOverhead) / wave_slots
@@ -23,11 +24,14 @@ namespace orion {
 //                    largest item + kItemOverhead)  (latency-bound: one wave)
 //    The per-item overhead (setup, split-K partial write and merge read) and
 //    the half-item tail were fitted to measured config-2 times at C = 128 ...
-//    1024.  Used when even the longest allowed pieces overfill one round.
+//    1024.  Used when even the longest allowed pieces overfill
+//    kMaxBalancedRounds rounds.
 
 // Shortest piece a balanced plan cuts: below it the per-item set-up and the
 // merge of many partials cost more than the even spread gains.
 constexpr int kMinBalancedPiece = 128;
+// Most rounds of wave slots a balanced plan fills (beyond: fixed chunks).
+constexpr int64_t kMaxBalancedRounds = 4;
 
 static int64_t estimate_split_time(const std::vector<int>& lens, int64_t hkv, int C,
                                    int64_t slots) {
@@ -87,6 +91,8 @@ void build_decode_plan(const uint32_t* positions, const int32_t* row_seq,
   // bound P the smallest for which every item fits in one round of the
   // resident wave slots, so no wave starts after the first round and the
   // pieces of a row end together.  ORION_DECODE_BALANCE=0 keeps fixed chunks.
+  // (Pieces are at most 64 table entries: the waves hold a piece's block ids
+  // one per lane.)
   const char* balance_env = getenv("ORION_DECODE_BALANCE");
   const bool balance_knob = !(balance_env && balance_env[0] == '0');
   const int unit = (int)std::max<int64_t>(16, block_size);
@@ -104,15 +110,23 @@ void build_decode_plan(const uint32_t* positions, const int32_t* row_seq,
     }
     return items;
   };
+  // Rounds: when even the longest pieces overfill one round of wave slots,
+  // the pieces fill R rounds instead (R <= kMaxBalancedRounds), again as
+  // evenly as the smallest bound P for R * slots items allows.
   int bal_p = 0;
-  if (balance_knob && forced == 0 && max_len > 0 && items_at(max_piece) <= wave_slots) {
-    int lo = 1, hi = max_piece / unit;  // P = k * unit; items_at is non-increasing in k
-    while (lo < hi) {
-      const int mid = (lo + hi) / 2;
-      if (items_at(mid * unit) <= wave_slots) hi = mid; else lo = mid + 1;
+  if (balance_knob && forced == 0 && max_len > 0) {
+    const int64_t slots = std::max<int64_t>(wave_slots, 1);
+    const int64_t rounds = (items_at(max_piece) + slots - 1) / slots;
+    if (rounds <= kMaxBalancedRounds) {
+      const int64_t target = rounds * slots;
+      int lo = 1, hi = max_piece / unit;  // P = k * unit; items_at is non-increasing in k
+      while (lo < hi) {
+        const int mid = (lo + hi) / 2;
+        if (items_at(mid * unit) <= target) hi = mid; else lo = mid + 1;
+      }
+      bal_p = std::max(lo * unit, kMinBalancedPiece);
+      if (bal_p > max_piece) bal_p = 0;
     }
-    bal_p = std::max(lo * unit, kMinBalancedPiece);
-    if (bal_p > max_piece) bal_p = 0;
   }
   plan->balanced = bal_p > 0;
   plan->work.clear();

@@ -1,9 +1,9 @@
 """Host-side properties of the decode work planner (csrc/decode_plan.cpp):
 tests/plan/plan_check.cpp builds plans for random batches and checks that
 every planned (row, KV head) context is covered exactly once, by pieces with
-valid table slices and split indices, and that balanced plans fit one round of
-wave slots.  Run for both cutting modes (balanced, and fixed chunks with
-ORION_DECODE_BALANCE=0)."""
+valid table slices and split indices, and that balanced plans fit at most four
+rounds of wave slots.  Run for both cutting modes (balanced, and fixed chunks
+with ORION_DECODE_BALANCE=0)."""
 import os
 import subprocess
 
