@@ -13,10 +13,10 @@ namespace orion {
 // row's context) and runs on one wave; a row split into several pieces is
 // merged afterwards by the combine kernel.  Items are ordered longest first,
 // so the last waves to be dispatched are the shortest.  Two ways to cut:
-//  * balanced (the default when it applies): each row is cut into equal
-//    pieces, as few as keep the items within one round of the resident wave
-//    slots (or within R rounds when one cannot hold them; see
-//    build_decode_plan);
+//  * balanced: each row is cut into equal pieces, as few as keep the items
+//    within one round of the resident wave slots (or within R rounds when
+//    one cannot hold them; see build_decode_plan), when the same fluid model
+//    rates it faster than the best fixed chunk (bandwidth-bound batches);
 //  * fixed chunks of C tokens, C a power of two chosen with a fluid model of
 //    the split kernel, in token-equivalents of one wave's streaming:
 //      time(C) = max((sum of item sizes + items * kItemOverhead) / wave_slots
@@ -24,8 +24,8 @@ namespace orion {
 //                    largest item + kItemOverhead)  (latency-bound: one wave)
 //    The per-item overhead (setup, split-K partial write and merge read) and
 //    the half-item tail were fitted to measured config-2 times at C = 128 ...
-//    1024.  Used when even the longest allowed pieces overfill
-//    kMaxBalancedRounds rounds.
+//    1024.  Latency-bound (small) batches keep them: short chunks give
+//    short dependent chains per wave.
 
 // Shortest piece a balanced plan cuts: below it the per-item set-up and the
 // merge of many partials cost more than the even spread gains.
@@ -33,9 +33,12 @@ constexpr int kMinBalancedPiece = 128;
 // Most rounds of wave slots a balanced plan fills (beyond: fixed chunks).
 constexpr int64_t kMaxBalancedRounds = 4;
 
+// Per-item overhead of the fluid model, in token-equivalents of one wave's
+// streaming (set-up, split-K partial write and merge read).
+constexpr int64_t kItemOverhead = 96;
+
 static int64_t estimate_split_time(const std::vector<int>& lens, int64_t hkv, int C,
                                    int64_t slots) {
-  constexpr int64_t kItemOverhead = 96;
   int64_t total = 0, items = 0, largest = 0;
   for (int L : lens) {
     const int64_t full = L / C, tail = L % C;
@@ -126,6 +129,25 @@ void build_decode_plan(const uint32_t* positions, const int32_t* row_seq,
       }
       bal_p = std::max(lo * unit, kMinBalancedPiece);
       if (bal_p > max_piece) bal_p = 0;
+      // Keep it only where the fluid model prefers it: evenly cut rounds
+      // (R rounds of the longest piece, or the bandwidth term) against the
+      // best fixed chunk.  Small batches are latency-bound and keep short
+      // fixed chunks.
+      if (bal_p) {
+        int64_t items = 0, total = 0, largest = 0;
+        for (int L : lens) {
+          if (!L) continue;
+          int piece;
+          const int n = pieces_of(L, bal_p, &piece);
+          items += hkv * n;
+          total += hkv * (int64_t)L;
+          largest = std::max<int64_t>(largest, std::min(piece, L));
+        }
+        const int64_t r = (items + slots - 1) / slots;
+        const int64_t t_bal = std::max((total + items * kItemOverhead) / slots,
+                                       r * (largest + kItemOverhead));
+        if (t_bal >= best_t) bal_p = 0;
+      }
     }
   }
   plan->balanced = bal_p > 0;
