@@ -98,14 +98,15 @@ int orion_hip_memset(orion_hip_device* dev, void* d_dst, int value, size_t bytes
 int orion_hip_timer_start(orion_hip_device* dev);
 int orion_hip_timer_stop(orion_hip_device* dev, float* ms);
 
-/* Per-kernel timing of the attention ops (no counterpart in the reference: a
- * measurement aid for roofline figures).  While enabled, every
+/* Per-kernel timing of the attention and GEMM ops (no counterpart in the
+ * reference: a measurement aid for roofline figures).  While enabled, every
  * orion_hip_paged_attention_decode / _prefill call records HIP events on the
  * device stream around its main kernel and around the split-K merge kernel
- * (decode only); nothing synchronises until _read, which waits for the
- * recorded events and returns the summed milliseconds and the call count
- * since the last enable.  Kernel indices: 0 = decode split-K kernel,
- * 1 = decode merge kernel, 2 = prefill kernel. */
+ * (decode only), and every orion_hip_gemm call around its launches (the GEMM
+ * and, when it splits K, its reduce); nothing synchronises until _read, which
+ * waits for the recorded events and returns the summed milliseconds and the
+ * call count since the last enable.  Kernel indices: 0 = decode split-K
+ * kernel, 1 = decode merge kernel, 2 = prefill kernel, 3 = orion_hip_gemm. */
 int orion_hip_kernel_timing(orion_hip_device* dev, int enable);
 int orion_hip_kernel_timing_read(orion_hip_device* dev, int kernel, double* total_ms,
                                  int64_t* calls);

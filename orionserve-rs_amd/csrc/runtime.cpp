@@ -154,7 +154,7 @@ struct orion_hip_device {
   // Per-kernel timing (orion_hip_kernel_timing): event pairs per kernel
   // index, resolved when read.
   bool ktiming = false;
-  std::vector<std::pair<hipEvent_t, hipEvent_t>> kevents[3];
+  std::vector<std::pair<hipEvent_t, hipEvent_t>> kevents[4];
   std::vector<hipEvent_t> event_pool;
   hipEvent_t take_event() {
     if (!event_pool.empty()) {
@@ -461,7 +461,7 @@ ORION_EXPORT int orion_hip_kernel_timing(orion_hip_device* dev, int enable) {
 ORION_EXPORT int orion_hip_kernel_timing_read(orion_hip_device* dev, int kernel, double* total_ms,
                                               int64_t* calls) {
   const char* st = "kernel_timing";
-  if (kernel < 0 || kernel > 2) return internal(st, "kernel index %d is not 0, 1 or 2", kernel);
+  if (kernel < 0 || kernel > 3) return internal(st, "kernel index %d is not 0 .. 3", kernel);
   double sum = 0.0;
   for (auto& p : dev->kevents[kernel]) {
     HIP_TRY(st, hipEventSynchronize(p.second));
@@ -477,7 +477,7 @@ ORION_EXPORT int orion_hip_kernel_timing_read(orion_hip_device* dev, int kernel,
 ORION_EXPORT int orion_hip_kernel_timing_samples(orion_hip_device* dev, int kernel, float* ms_out,
                                                  int64_t capacity, int64_t* calls) {
   const char* st = "kernel_timing";
-  if (kernel < 0 || kernel > 2) return internal(st, "kernel index %d is not 0, 1 or 2", kernel);
+  if (kernel < 0 || kernel > 3) return internal(st, "kernel index %d is not 0 .. 3", kernel);
   int64_t i = 0;
   for (auto& p : dev->kevents[kernel]) {
     if (i >= capacity) break;
@@ -1817,7 +1817,7 @@ ORION_EXPORT int orion_hip_gemm(orion_hip_device* dev, const float* d_x, const u
   Epilogue ep;
   if (int rc = gemm_args(st, d_bias, N, K, epilogue, &ep)) return rc;
   HIP_TRY(st, hipSetDevice(dev->ordinal));
-  HIP_TRY(st, gemm_on(dev, d_x, d_w, d_bias, M, N, K, ep, d_out));
+  HIP_TRY(st, timed_launch(dev, 3, [&] { return gemm_on(dev, d_x, d_w, d_bias, M, N, K, ep, d_out); }));
   return ORION_HIP_OK;
 }
 

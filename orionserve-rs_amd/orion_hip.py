@@ -312,7 +312,7 @@ class HipBackend:
         return ms.value
 
     # Kernel indices for kernel_timing_read.
-    K_DECODE_SPLIT, K_DECODE_MERGE, K_PREFILL = 0, 1, 2
+    K_DECODE_SPLIT, K_DECODE_MERGE, K_PREFILL, K_GEMM = 0, 1, 2, 3
 
     def kernel_timing(self, enable: bool) -> None:
         """Start (and reset) or stop per-kernel event timing of the attention ops."""
