@@ -218,7 +218,8 @@ template <bool HILO>
 __global__ void __launch_bounds__(256)
     gemm_tiled_kernel(const float* __restrict__ x, const uint16_t* __restrict__ w,
                       const float* __restrict__ bias, int M, int N, int K, int ep,
-                      float* __restrict__ out, PackedGeom pk, int gm) {
+                      float* __restrict__ out, PackedGeom pk, int gm, int kspan,
+                      float* __restrict__ partial) {
   __shared__ __attribute__((aligned(1024))) float As[2][kTM * kTK];
   __shared__ __attribute__((aligned(1024))) uint16_t Bs[2][kTN * kTK];
 
@@ -318,12 +319,14 @@ __global__ void __launch_bounds__(256)
 #pragma unroll
     for (int nt = 0; nt < 4; ++nt) acc[mt][nt] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-  const int ksteps = K / kTK;
-  load_tile(0, 0);
+  // K split z = blockIdx.z covers k-steps [z * kspan, min(ksteps, (z + 1) * kspan))
+  const int ks_begin = blockIdx.z * kspan;
+  const int ksteps = min(K / kTK, ks_begin + kspan);
+  load_tile(ks_begin, 0);
   wait_vmem_all();
   __syncthreads();
-  for (int ks = 0; ks < ksteps; ++ks) {
-    const int buf = ks & 1;
+  for (int ks = ks_begin; ks < ksteps; ++ks) {
+    const int buf = (ks - ks_begin) & 1;
     if (ks + 1 < ksteps) load_tile(ks + 1, buf ^ 1);
     const uint32_t aoff = (uint32_t)(buf * kTM * kTK * 4);
     const uint32_t boff = (uint32_t)(buf * kTN * kTK * 2);
@@ -362,6 +365,21 @@ __global__ void __launch_bounds__(256)
   }
 
   // ---- epilogue: acc[mt][nt][i] = C[m0 + wm*64 + mt*16 + 4*grp + i][n0 + wn*64 + nt*16 + l16] ----
+  if (partial) {  // one K split: raw sums, reduced by gemm_tiled_reduce_kernel
+    float* pz = partial + (int64_t)blockIdx.z * M * N;
+#pragma unroll
+    for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+      for (int nt = 0; nt < 4; ++nt) {
+        const int col = n0 + wn * 64 + nt * 16 + l16;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int row = m0 + wm * 64 + mt * 16 + 4 * grp + i;
+          if (row < M && col < N) pz[(int64_t)row * N + col] = acc[mt][nt][i];
+        }
+      }
+    return;
+  }
 #pragma unroll
   for (int mt = 0; mt < 4; ++mt) {
 #pragma unroll
@@ -387,6 +405,23 @@ __global__ void __launch_bounds__(256)
         }
       }
     }
+  }
+}
+
+// Sums the K splits of gemm_tiled_kernel in split order, then the store (+
+// bias) or accumulate epilogue.
+__global__ void __launch_bounds__(256)
+    gemm_tiled_reduce_kernel(const float* __restrict__ partial, int splits, int64_t M, int64_t N,
+                             const float* __restrict__ bias, int ep, float* __restrict__ out) {
+  const int64_t total = M * N;
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < total;
+       i += (int64_t)gridDim.x * 256) {
+    float v = 0.f;
+    for (int z = 0; z < splits; ++z) v += partial[z * total + i];
+    if (ep == (int)Epilogue::kAccumulate)
+      out[i] += v;
+    else
+      out[i] = bias ? v + bias[i % N] : v;
   }
 }
 
@@ -894,9 +929,36 @@ int gemm_sumsq_slots(int64_t N) {
   return (int)((N + 63) / 64);
 }
 
+// K splits of the LDS-tiled GEMM.  A call with fewer output tiles than CUs
+// leaves CUs idle, so its K is split until the tiles x splits reach
+// kTiledFill workgroups, up to 8 splits of at least 16 k-steps each; the
+// splits' raw sums go to the scratch and gemm_tiled_reduce_kernel adds them.
+// (Measured on config 5: the 16-tile LM head went 108 -> 28 us with 4
+// splits; splitting the 504-tile O and down projections saved about what
+// their 31 us reduce launches cost, so they stay whole.)  Not for the SwiGLU
+// epilogue (its column pairs sit in one tile).  ORION_GEMM_TILED_SPLIT=n
+// forces n (measurement knob, read per call).
+namespace {
+constexpr int64_t kTiledFill = 256;
+int tiled_ksplits(int64_t M, int64_t N, int64_t K) {
+  const int64_t tiles = ((N + kTN - 1) / kTN) * ((M + kTM - 1) / kTM);
+  const int64_t ksteps = K / kTK;
+  if (const char* e = getenv("ORION_GEMM_TILED_SPLIT")) {
+    const int64_t f = atoll(e);
+    return (int)std::max<int64_t>(1, std::min<int64_t>(f, std::max<int64_t>(1, ksteps / 4)));
+  }
+  int s = 1;
+  while (s < 8 && tiles * s < kTiledFill && ksteps / (2 * s) >= 16) s *= 2;
+  return s;
+}
+}  // namespace
+
 void gemm_scratch_need(int64_t M, int64_t N, int64_t K, size_t* ws_bytes) {
-  if (M < 1 || M > 64 || K % 32 != 0) {
-    *ws_bytes = 0;
+  *ws_bytes = 0;
+  if (M < 1 || K % 32 != 0) return;
+  if (M > 64) {
+    const int s = tiled_ksplits(M, N, K);
+    if (s > 1) *ws_bytes = (size_t)s * (size_t)M * (size_t)N * sizeof(float);
     return;
   }
   const GemvShape g = gemv_shape(M, N, K), gd = gemv_shape(M, N, K, true);
@@ -972,17 +1034,30 @@ hipError_t launch_gemm(hipStream_t st, const float* x, const uint16_t* w, const 
       const int64_t total = (int64_t)grid.x * grid.y;
       grid = dim3((unsigned)(((total + 7) / 8) * 8), 1);
     }
+    // K splits (tiled_ksplits), when the scratch holds their sums
+    int splits = ep == Epilogue::kSwiGLU ? 1 : tiled_ksplits(M, N, K);
+    const size_t split_bytes = (size_t)splits * (size_t)M * (size_t)N * sizeof(float);
+    if (splits > 1 && (!scratch || scratch->ws_bytes < split_bytes)) splits = 1;
+    const int ksteps = (int)(K / kTK), kspan = (ksteps + splits - 1) / splits;
+    grid.z = (unsigned)splits;
+    float* partial = splits > 1 ? scratch->ws : nullptr;
     // ORION_GEMM_ACT=bf16 rounds the activations to bf16 (one MFMA per
     // fragment) instead of the hi/lo pair (measurement knob, read per call).
     const char* act = getenv("ORION_GEMM_ACT");
     if (act && act[0] == 'b')
       hipLaunchKernelGGL(gemm_tiled_kernel<false>, grid, dim3(256), 0, st, x,
                          f.w_packed ? f.w_packed : w, bias, (int)M, (int)N, (int)K, (int)ep, out,
-                         pk, gm);
+                         pk, gm, kspan, partial);
     else
       hipLaunchKernelGGL(gemm_tiled_kernel<true>, grid, dim3(256), 0, st, x,
                          f.w_packed ? f.w_packed : w, bias, (int)M, (int)N, (int)K, (int)ep, out,
-                         pk, gm);
+                         pk, gm, kspan, partial);
+    if (splits > 1) {
+      const int64_t total = M * N;
+      const unsigned blocks = (unsigned)std::min<int64_t>((total + 255) / 256, 8192);
+      hipLaunchKernelGGL(gemm_tiled_reduce_kernel, dim3(blocks), dim3(256), 0, st, partial,
+                         splits, M, N, bias, (int)ep, out);
+    }
     return hipGetLastError();
   }
   // Rows per tile (MT x 16) and columns per tile (NT x 16): wide column tiles

@@ -53,6 +53,22 @@ def test_gemm_bias_and_accumulate_epilogues(backend, M):
     assert np.abs(got - ref64).max() <= 1e-4
 
 
+@pytest.mark.parametrize("M,N,K", [(400, 272, 2048), (1100, 1024, 3584), (200, 1024, 3584)])
+def test_tiled_gemm_k_splits(backend, monkeypatch, M, N, K):
+    # LDS-tiled shapes with few output tiles split K (sums reduced in split
+    # order by a second kernel): store with bias, and accumulate, against
+    # float64 and against the unsplit kernel (ORION_GEMM_TILED_SPLIT=1).
+    # 200 x 1024 x 3584 is config 5's LM head on the last rows.
+    for kw in (dict(bias=True), dict(accumulate=True)):
+        got, want, ref64 = gemm_case(backend, M, N, K, seed=M + K, **kw)
+        monkeypatch.setenv("ORION_GEMM_TILED_SPLIT", "1")
+        one, _, _ = gemm_case(backend, M, N, K, seed=M + K, **kw)
+        monkeypatch.delenv("ORION_GEMM_TILED_SPLIT")
+        scale = np.abs(ref64).max()
+        assert np.abs(got - ref64).max() <= 2e-5 * scale + 1e-6, kw
+        assert np.abs(got - one).max() <= 2e-5 * scale + 1e-6, kw
+
+
 @pytest.mark.parametrize("M,F,K", [(5, 48, 64), (32, 5632, 2048), (300, 176, 256), (600, 5632, 2048)])
 def test_gemm_swiglu_epilogue(backend, M, F, K):
     # Gate and up rows interleaved in groups of 8 (the model's fused W_gu
