@@ -37,11 +37,13 @@ def run_both(be, M, N, K, ep, bias, seed):
     return a, c
 
 
-# Larger first, then smaller: LM-head-sized partials (32 MB), then QKV with
+# Larger first, then smaller: LM-head-sized partials (32 MB), a tiled shape
+# with few output tiles (its K split 8 ways, sums in the array), then QKV with
 # bias, a down projection (22 K slices), SwiGLU, a residual accumulate, a
 # single-slice shape and one row; a skinny (M = 100) and a tiled (M = 300)
 # shape, which use no partials.
-SEQUENCE = [(32, 32000, 2048, oh.GEMM_STORE, False), (8, 2560, 2048, oh.GEMM_STORE, True),
+SEQUENCE = [(32, 32000, 2048, oh.GEMM_STORE, False), (400, 256, 4096, oh.GEMM_STORE, True),
+            (8, 2560, 2048, oh.GEMM_STORE, True),
             (64, 2048, 5632, oh.GEMM_ACCUMULATE, False), (32, 11264, 2048, oh.GEMM_SWIGLU, False),
             (17, 2048, 2048, oh.GEMM_ACCUMULATE, False), (5, 96, 256, oh.GEMM_STORE, True),
             (1, 512, 1024, oh.GEMM_STORE, False), (100, 1024, 512, oh.GEMM_STORE, False),
