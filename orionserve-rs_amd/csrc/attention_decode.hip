@@ -845,6 +845,17 @@ static hipError_t launch_combine(hipStream_t st, int64_t D, int64_t rows, int64_
   return hipGetLastError();
 }
 
+hipError_t launch_split_merge(hipStream_t st, int64_t D, int64_t rows, int64_t hq,
+                              const DecodePlanDev& plan, float* out) {
+  const int ms = plan.max_splits;
+  if (rows == 0 || ms <= 1 || (plan.rows && plan.num_rows == 0)) return hipSuccess;
+  if (!plan.ws || plan.ws_bytes < decode_workspace_bytes(rows, hq, D, ms) || !plan.row_nsplit)
+    return hipErrorInvalidValue;
+  const float* ws_o = plan.ws;
+  const float* ws_ml = ws_o + rows * hq * ms * D;
+  return launch_combine(st, D, rows, hq, plan, ms, ws_o, ws_ml, out);
+}
+
 hipError_t launch_paged_decode(hipStream_t st, const KvGeom& kv, const void* arena, int64_t layer,
                                const float* q, int64_t rows, int64_t hq,
                                const uint32_t* positions, const int32_t* row_seq,

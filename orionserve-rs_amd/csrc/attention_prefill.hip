@@ -104,7 +104,7 @@ __global__ void __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu
                          const uint32_t* __restrict__ first_pos,
                          const int64_t* __restrict__ bt_offsets,
                          const uint32_t* __restrict__ bt_ids, float scale_log2,
-                         float* __restrict__ out) {
+                         float* __restrict__ out, PrefillSplitOut split) {
   constexpr int kWaves = WAVES;
   constexpr int kBM = kWaves * 16 * kNR;  // packed rows per workgroup
   constexpr int kStages = STAGES;
@@ -145,6 +145,8 @@ __global__ void __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu
   const int kv_len = pos0 + p_hi / G + 1;          // keys this workgroup reads
   const int min_pos = pos0 + p_lo / G;             // no masking below this key
   const int ntiles = (kv_len + kBN - 1) / kBN;
+  // this entry's key tiles [t0, t_end)
+  const int t0 = pt.kt0, t_end = min(pt.kt1, ntiles), nloc = t_end - t0;
 
   // ---- this lane's queries (packed rows of its two row tiles) ----
   int qpos[kNR];
@@ -233,14 +235,14 @@ __global__ void __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu
     uint32_t ids0[NID];
 #pragma unroll
     for (int i = 0; i < kAhead; ++i) {
-      if (i < ntiles) {
-        load_ids(i, ids0);
-        load_tile(i, i, ids0);
+      if (i < nloc) {
+        load_ids(t0 + i, ids0);
+        load_tile(t0 + i, i, ids0);
       }
     }
-    load_ids(kAhead, ids_next);
+    load_ids(t0 + kAhead, ids_next);
   }
-  if (ntiles >= kAhead)
+  if (nloc >= kAhead)
     wait_vmcnt<kBehind>();  // tile 0 has landed (the later ones and the ids may not)
   else
     wait_vmcnt<0>();
@@ -282,7 +284,7 @@ __global__ void __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu
     constexpr uint32_t kBufOff = BUF * TILE * 2;
     // Tile t + kAhead goes into the buffer tile t - 1 used (every wave passed
     // the barrier that ended step t - 1, so its reads are done).
-    if (t + kAhead < ntiles) {
+    if (t + kAhead < t_end) {
       load_tile(t + kAhead, (BUF + kAhead) % kStages, ids_next);
       load_ids(t + kAhead + 1, ids_next);
     }
@@ -346,7 +348,9 @@ __global__ void __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu
 #pragma unroll
         for (int d = 0; d < DT; ++d) o[rt][d] *= alpha;
       }
-      const float nm = -m[rt] * scale_log2;
+      // (a part that starts past some rows' positions sees no key of theirs:
+      // m stays -inf and every weight must come out 0, not NaN)
+      const float nm = m[rt] == -INFINITY ? 0.f : -m[rt] * scale_log2;
 #pragma unroll
       for (int kp = 0; kp < 2; ++kp) {
         float pv[8];
@@ -419,25 +423,38 @@ __global__ void __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu
 
     // Tile t + 1 must have landed; the tiles after it (and their ids) may
     // still be in flight.
-    if (t + kAhead < ntiles)
+    if (t + kAhead < t_end)
       wait_vmcnt<kBehind>();
     else
       wait_vmcnt<0>();
     __syncthreads();
   };
 
-  for (int t = 0; t < ntiles; t += kStages) {
-    step(t, std::integral_constant<int, 0>{});
-    if (t + 1 < ntiles) step(t + 1, std::integral_constant<int, 1>{});
+  for (int u = 0; u < nloc; u += kStages) {
+    step(t0 + u, std::integral_constant<int, 0>{});
+    if (u + 1 < nloc) step(t0 + u + 1, std::integral_constant<int, 1>{});
     if constexpr (kStages > 2)
-      if (t + 2 < ntiles) step(t + 2, std::integral_constant<int, 2>{});
+      if (u + 2 < nloc) step(t0 + u + 2, std::integral_constant<int, 2>{});
   }
 
   // ---- normalise and store: lane holds dims 16d + 4*grp .. +3 of query l16 ----
 #pragma unroll
   for (int rt = 0; rt < kNR; ++rt) {
     const int p = p_lo + wave * 16 * kNR + rt * 16 + l16;
-    if (p < P) {
+    if (pt.nparts > 1 && p < P) {  // unnormalised part, merged afterwards
+      const int r = p / G;
+      const int64_t slot =
+          ((rs + r) * num_q_heads + (int64_t)kvh * G + (p - r * G)) * split.max_parts + pt.part;
+      float* op = split.ws_o + slot * D + 4 * grp;
+#pragma unroll
+      for (int d = 0; d < DT; ++d)
+        *reinterpret_cast<float4*>(op + 16 * d) =
+            make_float4(o[rt][d][0], o[rt][d][1], o[rt][d][2], o[rt][d][3]);
+      // max in scaled-score units (natural exp), as the decode waves write it
+      if (grp == 0)
+        *reinterpret_cast<float2*>(split.ws_ml + slot * 2) =
+            make_float2(m[rt] * (scale_log2 / kLog2e), lsum[rt][0]);
+    } else if (p < P) {
       const int r = p / G;
       const float inv = 1.0f / lsum[rt][0];
       float* op = out + ((rs + r) * num_q_heads + (int64_t)kvh * G + (p - r * G)) * D + 4 * grp;
@@ -463,21 +480,74 @@ static int prefill_waves() {
 
 int prefill_tile_rows() { return prefill_waves() * 16 * kNR; }
 
-void build_prefill_order(const int32_t* row_count, const uint32_t* first_pos, int64_t num_seqs,
-                         int64_t group, std::vector<PrefillTile>* order) {
+// Key parts: a sequence is cut into nparts key ranges when its longest tile
+// reads more than an even share of all the tiles' key reads over the CUs
+// (and at least kMinPartTiles key tiles per part), so one long-prefix chunk
+// no longer sets the launch's length while the other CUs idle.  Every tile
+// of the sequence gets the same nparts (a row's heads can straddle two
+// tiles, and the merge counts parts per row).
+constexpr int kMinPartTiles = 16;
+
+void build_prefill_order(const int32_t* row_start, const int32_t* row_count,
+                         const uint32_t* first_pos, int64_t num_seqs, int64_t group, int64_t hkv,
+                         int64_t cus, PrefillPlan* plan) {
   const int64_t kBM = prefill_tile_rows();
-  std::vector<std::pair<int64_t, PrefillTile>> items;
+  struct Tile {
+    int64_t seq, tile, kv_tiles;
+  };
+  std::vector<Tile> tiles;
+  int64_t total = 0;
   for (int64_t s = 0; s < num_seqs; ++s) {
     const int64_t packed = (int64_t)row_count[s] * group;
     for (int64_t t = 0; t * kBM < packed; ++t) {
-      const int64_t last_row = std::min(packed, (t + 1) * kBM) / group;  // rows, exclusive
-      items.push_back({(int64_t)first_pos[s] + last_row, PrefillTile{(int32_t)s, (int32_t)t}});
+      // keys the tile's last packed row attends (the kernel's kv_len)
+      const int64_t kv_len = (int64_t)first_pos[s] + (std::min(packed, (t + 1) * kBM) - 1) / group + 1;
+      const int64_t kvt = (kv_len + 63) / 64;
+      tiles.push_back({s, t, kvt});
+      total += kvt;
+    }
+  }
+  // ORION_PREFILL_SPLIT=0 keeps every sequence whole (measurement knob, read per call)
+  const char* split_env = getenv("ORION_PREFILL_SPLIT");
+  if (split_env && split_env[0] == '0') cus = 0;
+  const int64_t share = cus > 0 ? std::max<int64_t>((total * hkv + cus - 1) / cus, kMinPartTiles)
+                                : INT64_MAX;
+  std::vector<int64_t> seq_parts(num_seqs, 1);
+  for (const Tile& t : tiles)
+    if (t.kv_tiles > share)
+      seq_parts[t.seq] = std::max(seq_parts[t.seq], (t.kv_tiles + share - 1) / share);
+  std::vector<std::pair<int64_t, PrefillTile>> items;
+  for (const Tile& t : tiles) {
+    // every tile of a split sequence writes all nparts parts (a short tile's
+    // last parts may read no key: they write empty partials the merge weighs 0)
+    const int64_t np = seq_parts[t.seq];
+    const int64_t per = (t.kv_tiles + np - 1) / np;
+    const int32_t nparts = (int32_t)np;
+    for (int64_t k = 0; k < np; ++k) {
+      const int64_t a = std::min(t.kv_tiles, k * per), b = std::min(t.kv_tiles, a + per);
+      items.push_back({b - a, PrefillTile{(int32_t)t.seq, (int32_t)t.tile, (int32_t)a, (int32_t)b,
+                                          (int32_t)k, nparts}});
     }
   }
   std::stable_sort(items.begin(), items.end(),
                    [](const auto& a, const auto& b) { return a.first > b.first; });
-  order->clear();
-  for (const auto& it : items) order->push_back(it.second);
+  plan->order.clear();
+  for (const auto& it : items) plan->order.push_back(it.second);
+  // rows whose results come in parts
+  int64_t rows = 0;
+  for (int64_t s = 0; s < num_seqs; ++s)
+    rows = std::max<int64_t>(rows, (int64_t)row_start[s] + row_count[s]);
+  plan->row_parts.assign(rows, 0);
+  plan->split_rows.clear();
+  plan->max_parts = 1;
+  for (int64_t s = 0; s < num_seqs; ++s) {
+    if (seq_parts[s] < 2) continue;
+    plan->max_parts = std::max<int>(plan->max_parts, (int)seq_parts[s]);
+    for (int64_t r = 0; r < row_count[s]; ++r) {
+      plan->row_parts[row_start[s] + r] = (int32_t)seq_parts[s];
+      plan->split_rows.push_back((int32_t)(row_start[s] + r));
+    }
+  }
 }
 
 hipError_t launch_paged_prefill(hipStream_t st, const KvGeom& kv, const void* arena,
@@ -485,7 +555,8 @@ hipError_t launch_paged_prefill(hipStream_t st, const KvGeom& kv, const void* ar
                                 const PrefillTile* order, int64_t num_tiles,
                                 const int32_t* row_start, const int32_t* row_count,
                                 const uint32_t* first_pos, const int64_t* bt_offsets,
-                                const uint32_t* bt_ids, bool hilo, float* out) {
+                                const uint32_t* bt_ids, bool hilo, float* out,
+                                const PrefillSplitOut& split) {
   if (num_tiles == 0) return hipSuccess;
   if (!kv.dtype_bf16) return hipErrorNotSupported;
   const int64_t hkv = kv.num_kv_heads, D = kv.head_dim;
@@ -505,7 +576,7 @@ hipError_t launch_paged_prefill(hipStream_t st, const KvGeom& kv, const void* ar
                      (uint32_t)a.blk, (uint32_t)a.v_off, (uint32_t)a.slot, (uint32_t)a.head,   \
                      bs_log2,                                                                  \
                      (int)hkv, (int)hq, q, order, row_start, row_count, first_pos, bt_offsets, \
-                     bt_ids, scale_log2, out)
+                     bt_ids, scale_log2, out, split)
 #define ORION_PREFILL_B(DD, HH, BB)           \
   do {                                        \
     if (waves == 4)                           \

@@ -87,6 +87,12 @@ size_t decode_workspace_bytes(int64_t rows, int64_t hq, int64_t D, int64_t max_s
 // Which launches of a decode pass to issue (the merge only runs when the
 // plan splits some row).
 enum class DecodePhase { kBoth, kSplit, kMerge };
+// Merges split partials held in plan.ws (the decode split layout over `rows`
+// batch rows, plan.max_splits slots per (row, head)) of the rows plan.rows
+// lists, plan.row_nsplit[row] parts each, into out (the chunked-prefill key
+// parts use it too).
+hipError_t launch_split_merge(hipStream_t st, int64_t D, int64_t rows, int64_t hq,
+                              const DecodePlanDev& plan, float* out);
 hipError_t launch_paged_decode(hipStream_t st, const KvGeom& kv, const void* arena, int64_t layer,
                                const float* q, int64_t rows, int64_t hq,
                                const uint32_t* positions, const int32_t* row_seq,
@@ -94,22 +100,45 @@ hipError_t launch_paged_decode(hipStream_t st, const KvGeom& kv, const void* are
                                const DecodePlanDev& plan, float* out,
                                DecodePhase phase = DecodePhase::kBoth);
 
-// Prefill work list: one entry per (sequence, tile of packed rows), longest
-// first (by the keys its last row attends), so the longest workgroups are
-// dispatched first.  Built on the host from the chunk lengths and first
+// Prefill work list: one entry per (sequence, tile of packed rows, part of
+// its keys), longest first (by the key tiles it reads), so the longest
+// workgroups are dispatched first.  A sequence whose tiles would read far
+// more keys than an even share of the CUs is cut into nparts key ranges; each
+// part writes unnormalised partial results (the decode split layout) that a
+// merge combines.  Built on the host from the chunk lengths and first
 // positions; the device copy is what launch_paged_prefill takes.
 struct PrefillTile {
   int32_t seq, tile;
+  int32_t kt0, kt1;      // key tiles [kt0, kt1) (64 keys each) this workgroup reads
+  int32_t part, nparts;  // nparts > 1: partial results of part `part`
+};
+struct PrefillPlan {
+  std::vector<PrefillTile> order;
+  int max_parts = 1;
+  // batch rows whose results come in parts, and parts per batch row (0 for
+  // rows of unsplit sequences; sized to the batch's rows)
+  std::vector<int32_t> split_rows, row_parts;
 };
 int prefill_tile_rows();  // packed rows per prefill workgroup
-void build_prefill_order(const int32_t* row_count, const uint32_t* first_pos, int64_t num_seqs,
-                         int64_t group, std::vector<PrefillTile>* order);
+// cus: compute units (one prefill workgroup each); hkv: KV heads (workgroups
+// per work-list entry); cus = 0 never splits.
+void build_prefill_order(const int32_t* row_start, const int32_t* row_count,
+                         const uint32_t* first_pos, int64_t num_seqs, int64_t group, int64_t hkv,
+                         int64_t cus, PrefillPlan* plan);
+// Where split parts go: the decode split workspace layout over the batch's
+// rows (slot = (row * hq + head) * max_parts + part).
+struct PrefillSplitOut {
+  float* ws_o = nullptr;
+  float* ws_ml = nullptr;
+  int max_parts = 1;
+};
 hipError_t launch_paged_prefill(hipStream_t st, const KvGeom& kv, const void* arena,
                                 int64_t layer, const float* q, int64_t hq,
                                 const PrefillTile* order, int64_t num_tiles,
                                 const int32_t* row_start, const int32_t* row_count,
                                 const uint32_t* first_pos, const int64_t* bt_off,
-                                const uint32_t* bt_ids, bool hilo, float* out);
+                                const uint32_t* bt_ids, bool hilo, float* out,
+                                const PrefillSplitOut& split = PrefillSplitOut{});
 // Packed (row, query head) rows per prefill workgroup tile.
 
 // ---- GEMM -------------------------------------------------------------------

@@ -146,7 +146,8 @@ struct orion_hip_device {
   // Split-K GEMM scratch (partial tiles), shared by every call on this
   // device's stream.
   DevBuf gemm_ws;
-  DevBuf prefill_order;  // op-level prefill work list
+  DevBuf prefill_order;  // op-level prefill work list (+ key-part merge lists)
+  DevBuf prefill_ws;     // op-level prefill key-part partials
   DevBuf sample_io, sample_ws;  // sampler inputs/outputs and probabilities
   // This device's address of the file-scope `scratch` array
   // (orion_hip_gemm_noalloc); never freed.
@@ -370,6 +371,7 @@ ORION_EXPORT void orion_hip_device_close(orion_hip_device* dev) {
   for (hipEvent_t e : dev->event_pool) (void)hipEventDestroy(e);
   dev->gemm_ws.release();
   dev->prefill_order.release();
+  dev->prefill_ws.release();
   dev->sample_io.release();
   dev->sample_ws.release();
   (void)hipStreamDestroy(dev->stream);
@@ -1428,14 +1430,22 @@ ORION_EXPORT int orion_hip_model_forward(orion_hip_model* m, const orion_hip_bat
     }
   }
   const int64_t npf = (int64_t)pf_start.size();
-  std::vector<PrefillTile> pf_order;
-  if (npf) build_prefill_order(pf_count.data(), pf_pos.data(), npf, G, &pf_order);
+  PrefillPlan pfp;
+  if (npf)
+    build_prefill_order(pf_start.data(), pf_count.data(), pf_pos.data(), npf, G, d.num_kv_heads,
+                        m->dev->wave_slots / 8, &pfp);
+  const std::vector<PrefillTile>& pf_order = pfp.order;
+  const bool pf_split = pfp.max_parts > 1;
   // Decode plan (longest-first chunk list) over the remaining rows.
   DecodePlanHost plan;
   build_decode_plan(b->positions, hb.row_seq.data(), b->block_table_offsets, b->block_table_ids, n,
                     d.num_kv_heads, d.block_size, m->dev->wave_slots,
                     npf ? skip.data() : nullptr, &plan);
-  HIP_TRY(st, m->ws.reserve(decode_workspace_bytes(n, Hq, d.head_dim, plan.max_splits)));
+  // One workspace for the decode splits and the prefill key parts (their
+  // launches are ordered on the stream: the decode merge has read the splits
+  // before the prefill kernel writes its parts).
+  HIP_TRY(st, m->ws.reserve(std::max(decode_workspace_bytes(n, Hq, d.head_dim, plan.max_splits),
+                                     decode_workspace_bytes(n, Hq, d.head_dim, pfp.max_parts))));
 
   // ---- upload the batch: one pinned staging area, one copy ----
   const size_t o_tok = 0;
@@ -1452,7 +1462,9 @@ ORION_EXPORT int orion_hip_model_forward(orion_hip_model* m, const orion_hip_bat
   const size_t o_pfpos = o_pfcount + npf * 4;
   const size_t o_drows = o_pfpos + npf * 4;
   const size_t o_pforder = (o_drows + plan.rows.size() * 4 + 7) & ~(size_t)7;
-  const size_t total = o_pforder + pf_order.size() * sizeof(PrefillTile);
+  const size_t o_pfsplit = o_pforder + pf_order.size() * sizeof(PrefillTile);
+  const size_t o_pfparts = o_pfsplit + (pf_split ? pfp.split_rows.size() * 4 : 0);
+  const size_t total = o_pfparts + (pf_split ? pfp.row_parts.size() * 4 : 0);
   if (total > m->pinned_bytes) {
     if (m->pinned) {
       HIP_TRY(st, hipStreamSynchronize(stream));
@@ -1480,6 +1492,10 @@ ORION_EXPORT int orion_hip_model_forward(orion_hip_model* m, const orion_hip_bat
   std::memcpy(hp + o_pfpos, pf_pos.data(), npf * 4);
   std::memcpy(hp + o_drows, plan.rows.data(), plan.rows.size() * 4);
   std::memcpy(hp + o_pforder, pf_order.data(), pf_order.size() * sizeof(PrefillTile));
+  if (pf_split) {
+    std::memcpy(hp + o_pfsplit, pfp.split_rows.data(), pfp.split_rows.size() * 4);
+    std::memcpy(hp + o_pfparts, pfp.row_parts.data(), pfp.row_parts.size() * 4);
+  }
   char* dp = m->b_tokens.as<char>();
   HIP_TRY(st, hipMemcpyAsync(dp, hp, total, hipMemcpyHostToDevice, stream));
   const uint32_t* d_tok = reinterpret_cast<const uint32_t*>(dp + o_tok);
@@ -1507,6 +1523,20 @@ ORION_EXPORT int orion_hip_model_forward(orion_hip_model* m, const orion_hip_bat
   const int32_t* d_pfcount = reinterpret_cast<const int32_t*>(dp + o_pfcount);
   const uint32_t* d_pfpos = reinterpret_cast<const uint32_t*>(dp + o_pfpos);
   const PrefillTile* d_pforder = reinterpret_cast<const PrefillTile*>(dp + o_pforder);
+  // the prefill key parts' merge (split rows, parts per row, the workspace)
+  DecodePlanDev pf_merge;
+  PrefillSplitOut pf_out;
+  if (pf_split) {
+    pf_merge.rows = reinterpret_cast<const int32_t*>(dp + o_pfsplit);
+    pf_merge.num_rows = (int)pfp.split_rows.size();
+    pf_merge.row_nsplit = reinterpret_cast<const int32_t*>(dp + o_pfparts);
+    pf_merge.max_splits = pfp.max_parts;
+    pf_merge.ws = m->ws.as<float>();
+    pf_merge.ws_bytes = m->ws.bytes;
+    pf_out.ws_o = pf_merge.ws;
+    pf_out.ws_ml = pf_merge.ws + n * Hq * pfp.max_parts * d.head_dim;
+    pf_out.max_parts = pfp.max_parts;
+  }
 
   float* hidden = m->hidden.as<float>();
   float* xn = m->xn.as<float>();
@@ -1550,10 +1580,13 @@ ORION_EXPORT int orion_hip_model_forward(orion_hip_model* m, const orion_hip_bat
                                       d_rs, d_btoff, d_btids, m->rope_cos, m->rope_sin, &part));
     HIP_TRY(st, launch_paged_decode(stream, m->kv, m->arena, l, qrot, n, Hq, d_pos, d_rs, d_btoff,
                                     d_btids, dplan, attn));
-    if (npf)
+    if (npf) {
       HIP_TRY(st, launch_paged_prefill(stream, m->kv, m->arena, l, qrot, Hq, d_pforder,
                                        (int64_t)pf_order.size(), d_pfstart, d_pfcount, d_pfpos,
-                                       d_pfoff, d_btids, /*hilo=*/true, attn));
+                                       d_pfoff, d_btids, /*hilo=*/true, attn, pf_out));
+      if (pf_split)
+        HIP_TRY(st, launch_split_merge(stream, d.head_dim, n, Hq, pf_merge, attn));
+    }
     GemmFuse o_f = accumulate;
     if (pack_layers) o_f.w_packed = L.p_o;
     HIP_TRY(st, gemm_on(m->dev, attn, L.w_o, nullptr, n, H, m->qd, Epilogue::kAccumulate,
@@ -1739,28 +1772,61 @@ ORION_EXPORT int orion_hip_paged_attention_prefill(
   // The work list is built on the host: fetch the chunk lengths and first
   // positions (a synchronous copy; this entry point is for tests and timing,
   // the model forward builds the list from host data).
-  std::vector<int32_t> h_count(num_seqs > 0 ? num_seqs : 0);
+  std::vector<int32_t> h_count(num_seqs > 0 ? num_seqs : 0), h_start(h_count.size());
   std::vector<uint32_t> h_first(h_count.size());
   if (num_seqs > 0) {
     HIP_TRY(st, hipMemcpyAsync(h_count.data(), d_row_count, num_seqs * 4, hipMemcpyDeviceToHost,
+                               dev->stream));
+    HIP_TRY(st, hipMemcpyAsync(h_start.data(), d_row_start, num_seqs * 4, hipMemcpyDeviceToHost,
                                dev->stream));
     HIP_TRY(st, hipMemcpyAsync(h_first.data(), d_first_pos, num_seqs * 4, hipMemcpyDeviceToHost,
                                dev->stream));
     HIP_TRY(st, hipStreamSynchronize(dev->stream));
   }
-  std::vector<PrefillTile> order;
-  build_prefill_order(h_count.data(), h_first.data(), num_seqs, num_q_heads / g.num_kv_heads,
-                      &order);
-  HIP_TRY(st, dev->prefill_order.reserve(std::max<size_t>(order.size(), 1) * sizeof(PrefillTile)));
-  if (!order.empty())
-    HIP_TRY(st, hipMemcpyAsync(dev->prefill_order.ptr, order.data(),
-                               order.size() * sizeof(PrefillTile), hipMemcpyHostToDevice,
-                               dev->stream));
+  PrefillPlan pfp;
+  build_prefill_order(h_start.data(), h_count.data(), h_first.data(), num_seqs,
+                      num_q_heads / g.num_kv_heads, g.num_kv_heads, dev->wave_slots / 8, &pfp);
+  const std::vector<PrefillTile>& order = pfp.order;
+  // work list, then (when sequences are split into key parts) the merge's
+  // row list and parts per row, in one device buffer
+  const size_t ob = order.size() * sizeof(PrefillTile);
+  const bool split = pfp.max_parts > 1;
+  const size_t sb = split ? pfp.split_rows.size() * 4 : 0, pb = split ? pfp.row_parts.size() * 4 : 0;
+  std::vector<char> staged(ob + sb + pb);
+  if (ob) std::memcpy(staged.data(), order.data(), ob);
+  if (sb) std::memcpy(staged.data() + ob, pfp.split_rows.data(), sb);
+  if (pb) std::memcpy(staged.data() + ob + sb, pfp.row_parts.data(), pb);
+  HIP_TRY(st, dev->prefill_order.reserve(std::max<size_t>(staged.size(), 1)));
+  if (!staged.empty())
+    HIP_TRY(st, hipMemcpy(dev->prefill_order.ptr, staged.data(), staged.size(),
+                          hipMemcpyHostToDevice));
+  const int64_t rows = (int64_t)pfp.row_parts.size();
+  DecodePlanDev merge;
+  PrefillSplitOut out_parts;
+  if (split) {
+    HIP_TRY(st, dev->prefill_ws.reserve(
+                    decode_workspace_bytes(rows, num_q_heads, g.head_dim, pfp.max_parts)));
+    const char* base = dev->prefill_order.as<const char>();
+    merge.rows = reinterpret_cast<const int32_t*>(base + ob);
+    merge.num_rows = (int)pfp.split_rows.size();
+    merge.row_nsplit = reinterpret_cast<const int32_t*>(base + ob + sb);
+    merge.max_splits = pfp.max_parts;
+    merge.ws = dev->prefill_ws.as<float>();
+    merge.ws_bytes = dev->prefill_ws.bytes;
+    out_parts.ws_o = merge.ws;
+    out_parts.ws_ml = merge.ws + rows * num_q_heads * pfp.max_parts * g.head_dim;
+    out_parts.max_parts = pfp.max_parts;
+  }
+  // (timed together: the kernel and, for split sequences, the merge of parts)
   HIP_TRY(st, timed_launch(dev, 2, [&] {
-            return launch_paged_prefill(dev->stream, g, d_arena, layer, d_q, num_q_heads,
-                                        dev->prefill_order.as<const PrefillTile>(),
-                                        (int64_t)order.size(), d_row_start, d_row_count,
-                                        d_first_pos, d_bt_offsets, d_bt_ids, hilo != 0, d_out);
+            hipError_t e = launch_paged_prefill(dev->stream, g, d_arena, layer, d_q, num_q_heads,
+                                                dev->prefill_order.as<const PrefillTile>(),
+                                                (int64_t)order.size(), d_row_start, d_row_count,
+                                                d_first_pos, d_bt_offsets, d_bt_ids, hilo != 0,
+                                                d_out, out_parts);
+            if (e == hipSuccess && split)
+              e = launch_split_merge(dev->stream, g.head_dim, rows, num_q_heads, merge, d_out);
+            return e;
           }));
   return ORION_HIP_OK;
 }

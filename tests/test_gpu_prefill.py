@@ -82,6 +82,31 @@ def test_shapes_against_oracle(backend, hq, hkv, d, bs, hilo, head_major):
     assert float(np.abs(got - want).max()) <= (1e-4 if hilo else 1e-2)
 
 
+@pytest.mark.parametrize("hilo", [False, True])
+def test_key_parts_for_long_prefixes(backend, monkeypatch, hilo):
+    # Sequences whose tiles read far more keys than an even share of the CUs
+    # are cut into key parts (partial results merged afterwards): one chunk on
+    # a 9,000-token prefix beside short ones (config 5's imbalance), and a
+    # prefix-0 chunk of 1,500 rows whose first tiles read fewer key tiles than
+    # the sequence has parts (empty parts).  Against the oracle on sampled
+    # rows and against ORION_PREFILL_SPLIT=0 (whole sequences).
+    case = PrefillCase(31, [9000, 400, 60, 0], [256, 256, 100, 1500], 28, 4, 128, 16)
+    rows = sample_rows(case, 24, seed=3)
+    want = case.oracle_rows(rows)
+    got = run_prefill(backend, case, hilo)
+    monkeypatch.setenv("ORION_PREFILL_SPLIT", "0")
+    whole = run_prefill(backend, case, hilo)
+    monkeypatch.delenv("ORION_PREFILL_SPLIT")
+    tol = 1e-4 if hilo else 1e-2
+    err = float(np.abs(got[rows] - want).max())
+    print(f"[prefill parts] hilo={hilo} err {err:.2e} "
+          f"vs whole {float(np.abs(got - whole).max()):.2e}", flush=True)
+    assert err <= tol
+    assert float(np.abs(whole[rows] - want).max()) <= tol
+    assert float(np.abs(got - whole).max()) <= (2e-5 if hilo else 2e-3)
+    assert np.isfinite(got).all()
+
+
 def test_matches_decode_kernel_on_same_rows(backend):
     # The two kernels restate the same per-row computation; with hi/lo
     # operands they agree to f32-class rounding.
