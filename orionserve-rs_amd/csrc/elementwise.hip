@@ -7,19 +7,35 @@
 namespace orion {
 
 // TransformerModel::embed (transformer.rs:208-223): row gather, bf16 -> f32.
-// Token ids are range-checked on the host before launch.
-__global__ void embed_kernel(const uint32_t* __restrict__ tokens, const uint16_t* __restrict__ table,
-                             int64_t hidden, float* __restrict__ out) {
+// Token ids are range-checked on the host before launch.  With `sumsq`, also
+// the row's f64 sums of squares, one slot per 64 consecutive columns (the
+// slots the residual GEMMs leave for the fused RMSNorm of the next GEMM), so
+// layer 0's QKV GEMM applies its norm the same way: each wave takes 64-column
+// chunks in turn.
+__global__ void __launch_bounds__(256)
+    embed_kernel(const uint32_t* __restrict__ tokens, const uint16_t* __restrict__ table,
+                 int64_t hidden, float* __restrict__ out, double* __restrict__ sumsq) {
   const int64_t row = blockIdx.x;
   const uint16_t* src = table + (int64_t)tokens[row] * hidden;
   float* dst = out + row * hidden;
-  for (int64_t i = threadIdx.x; i < hidden; i += blockDim.x) dst[i] = bf16_to_f32(src[i]);
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int64_t nslots = (hidden + 63) >> 6;
+  for (int64_t c = wave; c < nslots; c += 4) {
+    const int64_t i = c * 64 + lane;
+    const float v = i < hidden ? bf16_to_f32(src[i]) : 0.f;
+    if (i < hidden) dst[i] = v;
+    if (sumsq) {
+      const double q = wave_sum_f64((double)v * (double)v);
+      if (lane == 0) sumsq[row * nslots + c] = q;
+    }
+  }
 }
 
 hipError_t launch_embed(hipStream_t st, const uint32_t* tokens, int64_t n, const uint16_t* table,
-                        int64_t hidden, float* out) {
+                        int64_t hidden, float* out, double* sumsq) {
   if (n == 0) return hipSuccess;
-  hipLaunchKernelGGL(embed_kernel, dim3((unsigned)n), dim3(256), 0, st, tokens, table, hidden, out);
+  hipLaunchKernelGGL(embed_kernel, dim3((unsigned)n), dim3(256), 0, st, tokens, table, hidden, out,
+                     sumsq);
   return hipGetLastError();
 }
 

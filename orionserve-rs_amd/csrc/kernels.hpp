@@ -248,8 +248,10 @@ hipError_t launch_sample(hipStream_t st, float* logits, int64_t rows, int64_t vo
                          int32_t* out);
 
 // ---- elementwise / normalisation -------------------------------------------
+// sumsq: when set, also the row sums of squares in the residual GEMMs' slot
+// layout (gemm_sumsq_slots(hidden) f64 per row).
 hipError_t launch_embed(hipStream_t st, const uint32_t* tokens, int64_t n, const uint16_t* table,
-                        int64_t hidden, float* out);
+                        int64_t hidden, float* out, double* sumsq = nullptr);
 // rows selected by `row_index` (nullptr = identity)
 hipError_t launch_rmsnorm(hipStream_t st, const float* x, const int32_t* row_index,
                           const float* weight, int64_t rows, int64_t cols, float eps, float* out);

@@ -1560,12 +1560,15 @@ ORION_EXPORT int orion_hip_model_forward(orion_hip_model* m, const orion_hip_bat
   GemmFuse accumulate;  // residual-add GEMMs: out += x W^T (+ row sums of squares)
   accumulate.sumsq_out = sumsq;
   GemmPartials part{};
-  HIP_TRY(st, launch_embed(stream, d_tok, n, m->w_embed, H, hidden));
+  // (the fused route's embed also leaves the row sums of squares, so layer
+  // 0's QKV GEMM applies its RMSNorm like every later layer's)
+  HIP_TRY(st, launch_embed(stream, d_tok, n, m->w_embed, H, hidden, sumsq));
   for (int64_t l = 0; l < d.num_layers; ++l) {
     const LayerDev& L = m->layers[l];
-    // QKV input: rms_norm(hidden) * input_norm -- a kernel of its own unless
-    // the previous layer's down GEMM left the sums of squares.
-    GemmFuse qkv_f = l > 0 ? norm_in(L.input_norm) : GemmFuse{};
+    // QKV input: rms_norm(hidden) * input_norm -- inside the QKV GEMM when
+    // the embed or the previous layer's down GEMM left the sums of squares,
+    // else a kernel of its own.
+    GemmFuse qkv_f = norm_in(L.input_norm);
     const float* qkv_x = hidden;
     if (!qkv_f.norm_sumsq) {
       HIP_TRY(st, launch_rmsnorm(stream, hidden, nullptr, L.input_norm, n, H, d.rms_norm_eps, xn));
