@@ -4,14 +4,17 @@
 #include "common.hpp"
 #include "kernels.hpp"
 
+#include <algorithm>
+
 namespace orion {
 
 // TransformerModel::embed (transformer.rs:208-223): row gather, bf16 -> f32.
 // Token ids are range-checked on the host before launch.  With `sumsq`, also
 // the row's f64 sums of squares, one slot per 64 consecutive columns (the
 // slots the residual GEMMs leave for the fused RMSNorm of the next GEMM), so
-// layer 0's QKV GEMM applies its norm the same way: each wave takes 64-column
-// chunks in turn.
+// layer 0's QKV GEMM applies its norm the same way.  Workgroup (row, y) takes
+// 64-column chunks 4y .. 4y + 3, one per wave (one load and at most one
+// reduction per wave).
 __global__ void __launch_bounds__(256)
     embed_kernel(const uint32_t* __restrict__ tokens, const uint16_t* __restrict__ table,
                  int64_t hidden, float* __restrict__ out, double* __restrict__ sumsq) {
@@ -20,7 +23,7 @@ __global__ void __launch_bounds__(256)
   float* dst = out + row * hidden;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int64_t nslots = (hidden + 63) >> 6;
-  for (int64_t c = wave; c < nslots; c += 4) {
+  for (int64_t c = (int64_t)blockIdx.y * 4 + wave; c < nslots; c += (int64_t)gridDim.y * 4) {
     const int64_t i = c * 64 + lane;
     const float v = i < hidden ? bf16_to_f32(src[i]) : 0.f;
     if (i < hidden) dst[i] = v;
@@ -34,8 +37,10 @@ __global__ void __launch_bounds__(256)
 hipError_t launch_embed(hipStream_t st, const uint32_t* tokens, int64_t n, const uint16_t* table,
                         int64_t hidden, float* out, double* sumsq) {
   if (n == 0) return hipSuccess;
-  hipLaunchKernelGGL(embed_kernel, dim3((unsigned)n), dim3(256), 0, st, tokens, table, hidden, out,
-                     sumsq);
+  const int64_t nslots = (hidden + 63) >> 6;
+  const unsigned gy = (unsigned)std::min<int64_t>((nslots + 3) / 4, 64);
+  hipLaunchKernelGGL(embed_kernel, dim3((unsigned)n, gy), dim3(256), 0, st, tokens, table, hidden,
+                     out, sumsq);
   return hipGetLastError();
 }
 
