@@ -24,6 +24,7 @@
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
+#include <type_traits>
 #include <utility>
 
 namespace orion {
@@ -676,8 +677,8 @@ __global__ void __launch_bounds__(256)
   const int rem = (int)(idx - tile * per_tile);
   const int row = rem / BN, c = rem - row * BN;
   const int col = tile * BN + c;
-  // The residual (accumulate) or bias (store) first, then the slices 8 at a
-  // time with every load of a group in flight, added in slice order (a slice
+  // The residual (accumulate) or bias (store) first, then the slices 8 (or
+  // 24) at a time with every load of a group in flight, added in slice order (a slice
   // past the end adds +0, which leaves the sum unchanged).
   float pre = 0.f;
   if (col < N && ep == (int)Epilogue::kAccumulate)
@@ -687,13 +688,22 @@ __global__ void __launch_bounds__(256)
   const float* pp = partial + (int64_t)tile * tile_elems + row * BN + c;
   const int64_t slice_stride = (int64_t)n_tiles * tile_elems;
   float v = 0.f;
-  for (int ks0 = 0; ks0 < kslices; ks0 += 8) {
-    float t[8];
+  auto sum_slices = [&](auto group) {
+    constexpr int NG = decltype(group)::value;
+    for (int ks0 = 0; ks0 < kslices; ks0 += NG) {
+      float t[NG];
 #pragma unroll
-    for (int j = 0; j < 8; ++j) t[j] = ks0 + j < kslices ? pp[(ks0 + j) * slice_stride] : 0.f;
+      for (int j = 0; j < NG; ++j)
+        t[j] = ks0 + j < kslices ? pp[(ks0 + j) * slice_stride] : 0.f;
 #pragma unroll
-    for (int j = 0; j < 8; ++j) v += t[j];
-  }
+      for (int j = 0; j < NG; ++j) v += t[j];
+    }
+  };
+  // up to 24 slices (config 4's down projection has 22) in one round of loads
+  if (kslices > 8)
+    sum_slices(std::integral_constant<int, 24>{});
+  else
+    sum_slices(std::integral_constant<int, 8>{});
   if (ep == (int)Epilogue::kSwiGLU) {
     const float u = __shfl_xor(v, 8);
     if ((c & 15) < 8 && col < N)
