@@ -321,7 +321,8 @@ __device__ __forceinline__ void decode_wave_mfma2(
       const int blk = blk_hint >= 0
                           ? blk_hint
                           : __builtin_amdgcn_readlane(my_blk, (b >> bs_log2) - first_blk);
-      const uint16_t* bb = base_k + (uint32_t)blk * blk_stride;
+      // 64-bit block offset (a layer may exceed 2^32 elements); uniform
+      const uint16_t* bb = base_k + (size_t)(uint32_t)blk * blk_stride;
 #pragma unroll
       for (int r = 0; r < RV; ++r) {
         const int jv = min(b + r * TPW + vt, end - 1);
@@ -334,7 +335,7 @@ __device__ __forceinline__ void decode_wave_mfma2(
       for (int r = 0; r < RV; ++r) {
         const int jv = min(b + r * TPW + vt, end - 1);
         const int bv = __shfl(my_blk, (jv >> bs_log2) - first_blk);
-        const uint16_t* rp = base_k + (uint32_t)bv * blk_stride +
+        const uint16_t* rp = base_k + (size_t)(uint32_t)bv * blk_stride +
                              (uint32_t)(jv & bs_mask) * slot_stride + vc * 8;
         ks[r] = kv_load16<STREAM>(rp);
         vs[r] = kv_load16<STREAM>(rp + v_off);
@@ -894,7 +895,8 @@ hipError_t launch_paged_decode(hipStream_t st, const KvGeom& kv, const void* are
                          plan.num_work, q, bt_ids, ms, scale, out, ws_o, ws_ml);
     e = hipGetLastError();
   } else if (kv.dtype_bf16) {
-    if (a.layer > (int64_t)UINT32_MAX) return hipErrorInvalidValue;
+    // in-block strides travel as 32-bit values; block offsets are 64-bit
+    if (a.blk > (int64_t)UINT32_MAX) return hipErrorInvalidValue;
     const uint16_t* base = static_cast<const uint16_t*>(arena) + layer * a.layer;
     const bool big = kv.block_size >= 16;
 #define ORION_MFMA2(DD, SS, BB)                                                                      \

@@ -210,8 +210,10 @@ __global__ void __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu
   auto load_tile = [&](int t, int buf, const uint32_t (&ids)[NID]) {
 #pragma unroll
     for (int j = 0; j < LPW; ++j) {
-      const uint32_t off = __umul24(ids[BIG ? 0 : j], blk_stride) +
-                           __umul24((uint32_t)(key_of(t, j) & bs_mask), slot_stride);
+      // block offset in 64 bits (a layer may exceed 2^32 elements), the
+      // in-block offset in 32
+      const size_t off = (size_t)ids[BIG ? 0 : j] * blk_stride +
+                         __umul24((uint32_t)(key_of(t, j) & bs_mask), slot_stride);
       const uint32_t dk =
           lds_base + (uint32_t)((buf * TILE + (wave_u * LPW + j) * RPI * D) * 2);
       lds_load16(head_base + off + ld_off_k[j], __builtin_amdgcn_readfirstlane(dk));
@@ -565,7 +567,10 @@ hipError_t launch_paged_prefill(hipStream_t st, const KvGeom& kv, const void* ar
   while ((1 << bs_log2) < kv.block_size) ++bs_log2;
   const ArenaStrides a = arena_strides(kv);
   const int64_t layer_elems = a.layer;
-  if (layer_elems > (int64_t)UINT32_MAX) return hipErrorInvalidValue;
+  // in-block strides travel as 32-bit values (the slot product as a 24-bit
+  // multiply); block offsets are 64-bit
+  if (a.blk > (int64_t)UINT32_MAX || a.slot >= (1 << 24) || kv.block_size >= (1 << 24))
+    return hipErrorInvalidValue;
   const uint16_t* base = static_cast<const uint16_t*>(arena) + layer * layer_elems;
   if (num_tiles * hkv > INT32_MAX) return hipErrorInvalidValue;
   const float scale_log2 = kLog2e / sqrtf((float)D);
