@@ -57,6 +57,44 @@ __global__ void __launch_bounds__(256)
   const int64_t orow = blockIdx.x;
   const int64_t irow = row_index ? row_index[orow] : orow;
   const float* xr = x + irow * cols;
+  float* orow_p = out + orow * cols;
+  // Fast path: the row in registers (float4 loads, up to 8 per thread), read
+  // once; the output is the same f32 expression as the general path.
+  constexpr int kMaxV = 8;
+  if ((cols & 3) == 0 && cols <= 1024 * kMaxV &&
+      ((reinterpret_cast<uintptr_t>(xr) | reinterpret_cast<uintptr_t>(orow_p) |
+        reinterpret_cast<uintptr_t>(weight)) & 15) == 0) {
+    const int n4 = (int)(cols >> 2);
+    const float4* x4 = reinterpret_cast<const float4*>(xr);
+    float4 v[kMaxV];
+#pragma unroll
+    for (int j = 0; j < kMaxV; ++j) {
+      const int i = (int)threadIdx.x + 256 * j;
+      v[j] = i < n4 ? x4[i] : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+    double s = 0.0;
+#pragma unroll
+    for (int j = 0; j < kMaxV; ++j)
+      s += (double)v[j].x * (double)v[j].x + (double)v[j].y * (double)v[j].y +
+           (double)v[j].z * (double)v[j].z + (double)v[j].w * (double)v[j].w;
+    s = wave_sum_f64(s);
+    if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = s;
+    __syncthreads();
+    const double total = part[0] + part[1] + part[2] + part[3];
+    const float scale = (float)(1.0 / sqrt(total / (double)cols + (double)eps));
+    const float4* w4 = reinterpret_cast<const float4*>(weight);
+    float4* o4 = reinterpret_cast<float4*>(orow_p);
+#pragma unroll
+    for (int j = 0; j < kMaxV; ++j) {
+      const int i = (int)threadIdx.x + 256 * j;
+      if (i < n4) {
+        const float4 w = w4[i];
+        o4[i] = make_float4(v[j].x * scale * w.x, v[j].y * scale * w.y, v[j].z * scale * w.z,
+                            v[j].w * scale * w.w);
+      }
+    }
+    return;
+  }
   double s = 0.0;
   for (int64_t i = threadIdx.x; i < cols; i += 256) {
     const double v = (double)xr[i];
@@ -67,7 +105,6 @@ __global__ void __launch_bounds__(256)
   __syncthreads();
   const double total = part[0] + part[1] + part[2] + part[3];
   const float scale = (float)(1.0 / sqrt(total / (double)cols + (double)eps));
-  float* orow_p = out + orow * cols;
   for (int64_t i = threadIdx.x; i < cols; i += 256) orow_p[i] = xr[i] * scale * weight[i];
 }
 
