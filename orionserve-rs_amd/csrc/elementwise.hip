@@ -185,6 +185,78 @@ __global__ void __launch_bounds__(256)
     store_kv<T>(kdst + i, y);
 }
 
+// The same RoPE + KV write for inputs in the q/k/v buffers (the prefill
+// route), vectorised: thread t of a (row, head) takes dims 4t .. 4t+3 and
+// their rotate-half partners 4t + D/2 .. (no LDS, no barrier; the same f32
+// expressions per element as rope_cache_kernel).  One thread per 8 elements,
+// a flat grid over (row, head, t); needs D % 8 == 0 and 16-byte aligned rows.
+template <typename T>
+__device__ inline void store_kv4(T* p, float4 v);
+template <>
+__device__ inline void store_kv4<float>(float* p, float4 v) { *reinterpret_cast<float4*>(p) = v; }
+template <>
+__device__ inline void store_kv4<uint16_t>(uint16_t* p, float4 v) {
+  *reinterpret_cast<uint2*>(p) = make_uint2(
+      (uint32_t)f32_to_bf16(v.x) | ((uint32_t)f32_to_bf16(v.y) << 16),
+      (uint32_t)f32_to_bf16(v.z) | ((uint32_t)f32_to_bf16(v.w) << 16));
+}
+
+template <typename T>
+__global__ void __launch_bounds__(256)
+    rope_cache_vec_kernel(T* __restrict__ kv_layer, int64_t blk_stride, int64_t v_off,
+                          int64_t slot_stride, int64_t head_stride, int bs_log2, int hq, int hkv,
+                          int D, int64_t rows, const float* __restrict__ q_in, int64_t q_stride,
+                          float* __restrict__ q_out, const float* __restrict__ k,
+                          int64_t k_stride, const float* __restrict__ v, int64_t v_stride,
+                          const uint32_t* __restrict__ positions,
+                          const int32_t* __restrict__ row_seq,
+                          const int64_t* __restrict__ bt_off, const uint32_t* __restrict__ bt_ids,
+                          const float* __restrict__ cos_t, const float* __restrict__ sin_t) {
+#pragma clang fp contract(off)
+  const int half = D >> 1, tpu = D >> 3;  // threads per (row, head)
+  const int units = hq + 2 * hkv;
+  const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (idx >= rows * units * tpu) return;
+  const int64_t row = idx / ((int64_t)units * tpu);
+  const int rem = (int)(idx - row * units * tpu);
+  const int unit = rem / tpu, t = rem - unit * tpu;
+  const bool is_q = unit < hq, is_k = !is_q && unit < hq + hkv;
+  const int h = is_q ? unit : is_k ? unit - hq : unit - hq - hkv;
+  const float* src = is_q ? q_in + row * q_stride + h * D
+                     : is_k ? k + row * k_stride + h * D
+                            : v + row * v_stride + h * D;
+  const float4 x0 = *reinterpret_cast<const float4*>(src + 4 * t);
+  const float4 x1 = *reinterpret_cast<const float4*>(src + half + 4 * t);
+  const uint32_t pos = positions[row];
+  if (is_q || is_k) {
+    const float4 c = *reinterpret_cast<const float4*>(cos_t + (int64_t)pos * half + 4 * t);
+    const float4 sn = *reinterpret_cast<const float4*>(sin_t + (int64_t)pos * half + 4 * t);
+    const float4 y0 = make_float4(x0.x * c.x - x1.x * sn.x, x0.y * c.y - x1.y * sn.y,
+                                  x0.z * c.z - x1.z * sn.z, x0.w * c.w - x1.w * sn.w);
+    const float4 y1 = make_float4(x0.x * sn.x + x1.x * c.x, x0.y * sn.y + x1.y * c.y,
+                                  x0.z * sn.z + x1.z * c.z, x0.w * sn.w + x1.w * c.w);
+    if (is_q) {
+      float* dst = q_out + row * (int64_t)hq * D + h * D;
+      *reinterpret_cast<float4*>(dst + 4 * t) = y0;
+      *reinterpret_cast<float4*>(dst + half + 4 * t) = y1;
+      return;
+    }
+    const int seq = row_seq[row];
+    const uint32_t blk = bt_ids[bt_off[seq] + (pos >> bs_log2)];
+    T* kdst = kv_layer + (int64_t)blk * blk_stride +
+              (int64_t)(pos & ((1u << bs_log2) - 1)) * slot_stride + h * head_stride;
+    store_kv4<T>(kdst + 4 * t, y0);
+    store_kv4<T>(kdst + half + 4 * t, y1);
+    return;
+  }
+  const int seq = row_seq[row];
+  const uint32_t blk = bt_ids[bt_off[seq] + (pos >> bs_log2)];
+  T* vdst = kv_layer + (int64_t)blk * blk_stride +
+            (int64_t)(pos & ((1u << bs_log2) - 1)) * slot_stride + h * head_stride + v_off;
+  store_kv4<T>(vdst + 4 * t, x0);
+  store_kv4<T>(vdst + half + 4 * t, x1);
+}
+
 hipError_t launch_rope_and_cache(hipStream_t st, const KvGeom& kv, void* arena, int64_t layer,
                                  int64_t rows, int64_t hq, const float* q_in, int64_t q_stride,
                                  float* q_out, const float* k, int64_t k_stride, const float* v,
@@ -200,6 +272,30 @@ hipError_t launch_rope_and_cache(hipStream_t st, const KvGeom& kv, void* arena, 
   if (kv.head_dim > 256 || kv.head_dim % 2 || hq + 2 * kv.num_kv_heads > 65535 ||
       rows > INT32_MAX)
     return hipErrorInvalidValue;
+  // Inputs in the q/k/v buffers with 16-byte aligned rows: the vectorised
+  // kernel (one thread per 8 elements instead of one per element).
+  const int64_t D = kv.head_dim, units = hq + 2 * kv.num_kv_heads;
+  auto al16 = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; };
+  if (!qp.ws && D % 8 == 0 && q_stride % 4 == 0 && k_stride % 4 == 0 && v_stride % 4 == 0 &&
+      al16(q_in) && al16(k) && al16(v) && al16(q_out) && al16(cos_t) && al16(sin_t) &&
+      al16(arena)) {
+    const int64_t threads = rows * units * (D / 8);
+    if ((threads + 255) / 256 > INT32_MAX) return hipErrorInvalidValue;
+    const dim3 vgrid((unsigned)((threads + 255) / 256));
+    if (kv.dtype_bf16)
+      hipLaunchKernelGGL(rope_cache_vec_kernel<uint16_t>, vgrid, dim3(256), 0, st,
+                         static_cast<uint16_t*>(arena) + layer * a.layer, a.blk, a.v_off, a.slot,
+                         a.head, bs_log2, (int)hq, (int)kv.num_kv_heads, (int)D, rows, q_in,
+                         q_stride, q_out, k, k_stride, v, v_stride, positions, row_seq, bt_off,
+                         bt_ids, cos_t, sin_t);
+    else
+      hipLaunchKernelGGL(rope_cache_vec_kernel<float>, vgrid, dim3(256), 0, st,
+                         static_cast<float*>(arena) + layer * a.layer, a.blk, a.v_off, a.slot,
+                         a.head, bs_log2, (int)hq, (int)kv.num_kv_heads, (int)D, rows, q_in,
+                         q_stride, q_out, k, k_stride, v, v_stride, positions, row_seq, bt_off,
+                         bt_ids, cos_t, sin_t);
+    return hipGetLastError();
+  }
   const dim3 grid((unsigned)rows, (unsigned)(hq + 2 * kv.num_kv_heads));
   const dim3 block((unsigned)((kv.head_dim + 63) & ~63));
   if (kv.dtype_bf16) {
