@@ -215,14 +215,17 @@ struct PackedGeom {
 
 // HILO: x carried as a truncated hi + lo bf16 pair (two MFMAs, ~16 bits of
 // x per product); otherwise rounded to bf16 (nearest even, one MFMA).
-template <bool HILO>
-__global__ void __launch_bounds__(256)
+// NTW: 16-column tiles per wave (4: 128-column workgroup tiles; 8: 256).
+template <bool HILO, int NTW>
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(NTW == 8 ? 2 : 1)))
     gemm_tiled_kernel(const float* __restrict__ x, const uint16_t* __restrict__ w,
                       const float* __restrict__ bias, int M, int N, int K, int ep,
                       float* __restrict__ out, PackedGeom pk, int gm, int kspan,
                       float* __restrict__ partial) {
+  constexpr int TN = 32 * NTW;   // workgroup columns
+  constexpr int BJ = NTW / 2;    // B copies (1 KiB each) per wave per k-step
   __shared__ __attribute__((aligned(1024))) float As[2][kTM * kTK];
-  __shared__ __attribute__((aligned(1024))) uint16_t Bs[2][kTN * kTK];
+  __shared__ __attribute__((aligned(1024))) uint16_t Bs[2][TN * kTK];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -236,7 +239,7 @@ __global__ void __launch_bounds__(256)
   // tiles in flight on one XCD share A and B slabs in its L2.
   int mt_i = blockIdx.y, nt_i = blockIdx.x;
   if (gm > 0) {
-    const int gx = (N + kTN - 1) / kTN, gy = (M + kTM - 1) / kTM, total = gx * gy;
+    const int gx = (N + TN - 1) / TN, gy = (M + kTM - 1) / kTM, total = gx * gy;
     const int b = blockIdx.x;
     const int per = (total + 7) / 8;
     const int t = (b & 7) * per + (b >> 3);
@@ -246,12 +249,12 @@ __global__ void __launch_bounds__(256)
     mt_i = g * gm + within % gm_eff;
     nt_i = within / gm_eff;
   }
-  const int m0 = mt_i * kTM, n0 = nt_i * kTN;
+  const int m0 = mt_i * kTM, n0 = nt_i * TN;
 
   // ---- DMA addressing: A = 4 wave instructions (8 rows x 128 B each),
   // B = 2 wave instructions (16 rows x 64 B each). ----
   const float* a_src[4];
-  const uint16_t* b_src[2];
+  const uint16_t* b_src[BJ];
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
     const int r = (wave * 4 + j) * 8 + (lane >> 3);
@@ -262,16 +265,16 @@ __global__ void __launch_bounds__(256)
   // chunk (decode workgroup share) within a K slice, and the last fragment
   // column group the packed copy holds (columns past it are past N anyway).
   const bool packed = pk.nt > 0;
-  int64_t b_chunk[2] = {0, 0};
+  int64_t b_chunk[BJ] = {};
 #pragma unroll
-  for (int j = 0; j < 2; ++j) {
+  for (int j = 0; j < BJ; ++j) {
     if (packed) {
-      const int c16 = min(n0 / 16 + wave * 2 + j, pk.n_tiles * 4 * pk.nt - 1);
+      const int c16 = min(n0 / 16 + wave * BJ + j, pk.n_tiles * 4 * pk.nt - 1);
       const int tile = c16 / (4 * pk.nt), rem = c16 - tile * 4 * pk.nt;
       b_chunk[j] = ((int64_t)tile * 4 + rem / pk.nt) * pk.nt + rem % pk.nt;
       b_src[j] = w + (int64_t)lane * 8;
     } else {
-      const int r = (wave * 2 + j) * 16 + (lane >> 2);
+      const int r = (wave * BJ + j) * 16 + (lane >> 2);
       const int c = (lane & 3) ^ swz_b(r);
       b_src[j] = w + (int64_t)min(n0 + r, N - 1) * K + c * 8;
     }
@@ -287,20 +290,20 @@ __global__ void __launch_bounds__(256)
     if (packed) {
       const int slice = ks / pk.ks, step = ks - slice * pk.ks;
 #pragma unroll
-      for (int j = 0; j < 2; ++j)
+      for (int j = 0; j < BJ; ++j)
         lds_load16(b_src[j] + slice * slice_elems + (b_chunk[j] * pk.ks + step) * 512,
-                   bs_base + (uint32_t)(buf * kTN * kTK * 2 + (wave * 2 + j) * 1024));
+                   bs_base + (uint32_t)(buf * TN * kTK * 2 + (wave * BJ + j) * 1024));
     } else {
 #pragma unroll
-      for (int j = 0; j < 2; ++j)
-        lds_load16(b_src[j] + k0, bs_base + (uint32_t)(buf * kTN * kTK * 2 + (wave * 2 + j) * 1024));
+      for (int j = 0; j < BJ; ++j)
+        lds_load16(b_src[j] + k0, bs_base + (uint32_t)(buf * TN * kTK * 2 + (wave * BJ + j) * 1024));
     }
   };
 
   // ---- fragment read addresses (bytes, buffer 0) ----
   typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
   typedef __attribute__((address_space(3))) u32x4 lds_u32x4;
-  uint32_t a_rd0[4], a_rd1[4], b_rd[4];
+  uint32_t a_rd0[4], a_rd1[4], b_rd[NTW];
 #pragma unroll
   for (int mt = 0; mt < 4; ++mt) {
     const int r = wm * 64 + mt * 16 + l16;
@@ -308,17 +311,17 @@ __global__ void __launch_bounds__(256)
     a_rd1[mt] = as_base + (uint32_t)(r * kTK + (((2 * grp + 1) ^ swz_a(r)) * 4)) * 4;
   }
 #pragma unroll
-  for (int nt = 0; nt < 4; ++nt) {
-    const int n = wn * 64 + nt * 16 + l16;
-    b_rd[nt] = packed ? bs_base + (uint32_t)((wn * 4 + nt) * 1024 + lane * 16)
+  for (int nt = 0; nt < NTW; ++nt) {
+    const int n = wn * 16 * NTW + nt * 16 + l16;
+    b_rd[nt] = packed ? bs_base + (uint32_t)((wn * NTW + nt) * 1024 + lane * 16)
                       : bs_base + (uint32_t)(n * kTK + ((grp ^ swz_b(n)) * 8)) * 2;
   }
 
-  f32x4 acc[4][4];
+  f32x4 acc[4][NTW];
 #pragma unroll
   for (int mt = 0; mt < 4; ++mt)
 #pragma unroll
-    for (int nt = 0; nt < 4; ++nt) acc[mt][nt] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int nt = 0; nt < NTW; ++nt) acc[mt][nt] = f32x4{0.f, 0.f, 0.f, 0.f};
 
   // K split z = blockIdx.z covers k-steps [z * kspan, min(ksteps, (z + 1) * kspan))
   const int ks_begin = blockIdx.z * kspan;
@@ -330,10 +333,10 @@ __global__ void __launch_bounds__(256)
     const int buf = (ks - ks_begin) & 1;
     if (ks + 1 < ksteps) load_tile(ks + 1, buf ^ 1);
     const uint32_t aoff = (uint32_t)(buf * kTM * kTK * 4);
-    const uint32_t boff = (uint32_t)(buf * kTN * kTK * 2);
-    bf16x8 bw[4];
+    const uint32_t boff = (uint32_t)(buf * TN * kTK * 2);
+    bf16x8 bw[NTW];
 #pragma unroll
-    for (int nt = 0; nt < 4; ++nt)
+    for (int nt = 0; nt < NTW; ++nt)
       bw[nt] = __builtin_bit_cast(bf16x8, *(const lds_u32x4*)(uintptr_t)(b_rd[nt] + boff));
 #pragma unroll
     for (int mt = 0; mt < 4; ++mt) {
@@ -354,7 +357,7 @@ __global__ void __launch_bounds__(256)
         (void)alo;
       }
 #pragma unroll
-      for (int nt = 0; nt < 4; ++nt) {
+      for (int nt = 0; nt < NTW; ++nt) {
         acc[mt][nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ahi, bw[nt], acc[mt][nt], 0, 0, 0);
         if constexpr (HILO)
           acc[mt][nt] =
@@ -371,8 +374,8 @@ __global__ void __launch_bounds__(256)
 #pragma unroll
     for (int mt = 0; mt < 4; ++mt)
 #pragma unroll
-      for (int nt = 0; nt < 4; ++nt) {
-        const int col = n0 + wn * 64 + nt * 16 + l16;
+      for (int nt = 0; nt < NTW; ++nt) {
+        const int col = n0 + wn * 16 * NTW + nt * 16 + l16;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
           const int row = m0 + wm * 64 + mt * 16 + 4 * grp + i;
@@ -384,8 +387,8 @@ __global__ void __launch_bounds__(256)
 #pragma unroll
   for (int mt = 0; mt < 4; ++mt) {
 #pragma unroll
-    for (int nt = 0; nt < 4; ++nt) {
-      const int col = n0 + wn * 64 + nt * 16 + l16;
+    for (int nt = 0; nt < NTW; ++nt) {
+      const int col = n0 + wn * 16 * NTW + nt * 16 + l16;
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const int row = m0 + wm * 64 + mt * 16 + 4 * grp + i;
@@ -395,7 +398,7 @@ __global__ void __launch_bounds__(256)
           const float u = __shfl_xor(v, 8);
           if (l16 < 8 && row < M && col < N) {
             const float act = v / (1.0f + __expf(-v)) * u;
-            out[(int64_t)row * (N >> 1) + ((n0 + wn * 64 + nt * 16) >> 1) + l16] = act;
+            out[(int64_t)row * (N >> 1) + ((n0 + wn * 16 * NTW + nt * 16) >> 1) + l16] = act;
           }
         } else if (row < M && col < N) {
           float* op = out + (int64_t)row * N + col;
@@ -1032,7 +1035,16 @@ hipError_t launch_gemm(hipStream_t st, const float* x, const uint16_t* w, const 
       pk.ks = gp.ks;
       pk.n_tiles = gp.n_tiles;
     }
-    dim3 grid((unsigned)((N + kTN - 1) / kTN), (unsigned)((M + kTM - 1) / kTM));
+    // 128 x 256 workgroup tiles (64 x 128 per wave, 2 workgroups per CU) for
+    // wide outputs: per MFMA a third less LDS traffic (copies + fragment
+    // reads) than 128 x 128 tiles at 3 per CU.  Measured at config 4's prefill
+    // shapes: gate/up (N 11264) 649-673 -> 692-700 TFLOP/s; QKV (2560) even,
+    // down (2048) -3 %, O (2048) -13 % (too few tiles for 2 per CU).
+    // ORION_GEMM_WIDE=0/1 forces the choice (measurement knob, read per call).
+    const char* wide_env = getenv("ORION_GEMM_WIDE");
+    const bool wide = wide_env ? wide_env[0] == '1' : N >= 8192;
+    const int tn = wide ? 2 * kTN : kTN;
+    dim3 grid((unsigned)((N + tn - 1) / tn), (unsigned)((M + kTM - 1) / kTM));
     // XCD-aware grouped tile order with groups of 4 m tiles (measured at the
     // config-4 prefill shapes against the row-major grid: QKV 529 -> 563, O
     // 405 -> 443, down 513 -> 536 TFLOP/s, gate/up unchanged; groups of 8 and
@@ -1054,14 +1066,11 @@ hipError_t launch_gemm(hipStream_t st, const float* x, const uint16_t* w, const 
     // ORION_GEMM_ACT=bf16 rounds the activations to bf16 (one MFMA per
     // fragment) instead of the hi/lo pair (measurement knob, read per call).
     const char* act = getenv("ORION_GEMM_ACT");
-    if (act && act[0] == 'b')
-      hipLaunchKernelGGL(gemm_tiled_kernel<false>, grid, dim3(256), 0, st, x,
-                         f.w_packed ? f.w_packed : w, bias, (int)M, (int)N, (int)K, (int)ep, out,
-                         pk, gm, kspan, partial);
-    else
-      hipLaunchKernelGGL(gemm_tiled_kernel<true>, grid, dim3(256), 0, st, x,
-                         f.w_packed ? f.w_packed : w, bias, (int)M, (int)N, (int)K, (int)ep, out,
-                         pk, gm, kspan, partial);
+    const bool hilo = !(act && act[0] == 'b');
+    auto kern = wide ? (hilo ? gemm_tiled_kernel<true, 8> : gemm_tiled_kernel<false, 8>)
+                     : (hilo ? gemm_tiled_kernel<true, 4> : gemm_tiled_kernel<false, 4>);
+    hipLaunchKernelGGL(kern, grid, dim3(256), 0, st, x, f.w_packed ? f.w_packed : w, bias,
+                       (int)M, (int)N, (int)K, (int)ep, out, pk, gm, kspan, partial);
     if (splits > 1) {
       const int64_t total = M * N;
       const unsigned blocks = (unsigned)std::min<int64_t>((total + 255) / 256, 8192);
