@@ -2,13 +2,14 @@
 
 The reference's arena (attention.rs:34-104) is one Vec indexed with usize, so
 a block id anywhere in the pool is valid.  On a 288 GB MI355X a serving pool
-can exceed 2^32 bf16 elements (8.59 GB) per layer (260 GB of KV over a 22-layer
-model is 11.8 GB per layer), so the kernels form block offsets in 64 bits.  This test allocates a 1,050,000-
-block bf16 layer (hkv 1, d 128, block 16: 4096 elements per block, 8.6 GB,
-4.30e9 elements) and reads sequences whose tables mix blocks below and above
-the 2^32-element boundary (including the pool's last block), through the
-decode and the prefill kernels, against the oracle on a compacted copy of the
-same blocks (block ids remapped, contents identical).
+can exceed 2^32 bf16 elements (8.59 GB) per layer (260 GB of KV over a
+22-layer model is 11.8 GB per layer), so the kernels form block offsets in 64
+bits.  This test allocates a 1,050,000-block bf16 layer (hkv 1, d 128, block
+16: 4096 elements per block, 8.6 GB, 4.30e9 elements) and reads sequences
+whose tables mix blocks below and above the 2^32-element boundary (including
+the pool's last block), through the decode and the prefill kernels, against
+the oracle on a compacted copy of the same blocks (block ids remapped,
+contents identical).
 """
 import numpy as np
 import pytest
