@@ -4,6 +4,7 @@
 #include "kernels.hpp"
 
 #include <algorithm>
+#include <cstdint>
 #include <cstdlib>
 #include <vector>
 
@@ -177,6 +178,7 @@ void build_decode_plan(const uint32_t* positions, const int32_t* row_seq,
   }
   std::stable_sort(pcs.begin(), pcs.end(),
                    [](const Piece& a, const Piece& b) { return a.len > b.len; });
+  plan->work.reserve(pcs.size() * hkv);
   for (const Piece& pc : pcs) {
     const int64_t tbl_off = bt_offsets[row_seq[pc.row]] + (pc.start >> bs_log2);
     const int32_t n = plan->row_nsplit[pc.row];
@@ -192,6 +194,7 @@ void build_decode_plan(const uint32_t* positions, const int32_t* row_seq,
   // block.
   static thread_local std::vector<uint64_t> seen, again;
   bool shared = false;
+  size_t w_lo = SIZE_MAX, w_hi = 0;  // words touched (cleared afterwards)
   auto attended = [&](auto&& f) {
     for (int64_t r = 0; r < rows; ++r) {
       if (lens[r] == 0) continue;
@@ -203,6 +206,8 @@ void build_decode_plan(const uint32_t* positions, const int32_t* row_seq,
   attended([&](uint32_t id) {
     const size_t w = id >> 6;
     if (w >= seen.size()) seen.resize(w + 1, 0), again.resize(w + 1, 0);
+    w_lo = std::min(w_lo, w);
+    w_hi = std::max(w_hi, w);
     const uint64_t bit = 1ull << (id & 63);
     if (seen[w] & bit) {
       again[w] |= bit;
@@ -212,18 +217,23 @@ void build_decode_plan(const uint32_t* positions, const int32_t* row_seq,
   });
   int64_t shared_items = 0;
   if (shared) {
-    for (DecodeWork& wk : plan->work) {
+    // the hkv items of a piece are adjacent and read the same blocks
+    for (size_t i = 0; i < plan->work.size(); i += hkv) {
+      const DecodeWork& wk = plan->work[i];
       const int nb = ((wk.end - 1) >> bs_log2) - (wk.start >> bs_log2) + 1;
       bool s = false;
       for (int j = 0; j < nb && !s; ++j) {
         const uint32_t id = bt_ids[wk.tbl_off + j];
         s = (again[id >> 6] >> (id & 63)) & 1;
       }
-      wk.shared = s ? 1 : 0;
-      shared_items += s;
+      for (int64_t h = 0; h < hkv; ++h) plan->work[i + h].shared = s ? 1 : 0;
+      shared_items += s ? hkv : 0;
     }
   }
-  attended([&](uint32_t id) { seen[id >> 6] = 0, again[id >> 6] = 0; });
+  if (w_lo <= w_hi) {
+    std::fill(seen.begin() + w_lo, seen.begin() + w_hi + 1, 0);
+    std::fill(again.begin() + w_lo, again.begin() + w_hi + 1, 0);
+  }
   plan->stream_kv = !shared;
   plan->mixed_kv = shared && shared_items < (int64_t)plan->work.size();
 }

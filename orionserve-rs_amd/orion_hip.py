@@ -393,6 +393,17 @@ class ForwardBatch:
             raise InternalError(f"ForwardBatch slot token counts sum to {s} but there are "
                                 f"{len(self.tokens)} tokens")
 
+    def prepare(self) -> "ForwardBatch":
+        """Validates and flattens the batch once, for a caller that runs the
+        same batch repeatedly: forward() then reuses the arrays instead of
+        rebuilding them from the Python lists (about a millisecond for 34 k
+        block-table entries).  A caller that edits the lists afterwards calls
+        prepare() again.  The library validates the flattened batch on every
+        forward either way."""
+        self.validate()
+        self._prepared = self.to_csr()
+        return self
+
     def to_csr(self):
         """Flattened arrays in the layout of orion_hip_batch.  Built with
         array.array (straight from Python ints; an out-of-range value raises
@@ -607,12 +618,14 @@ class HipTransformerModel:
     def forward(self, batch: ForwardBatch, want_logits: bool = True,
                 want_argmax: bool = False) -> ForwardOutput:
         """LanguageModel::forward (transformer.rs:359-442)."""
-        batch.validate()
+        prepared = getattr(batch, "_prepared", None)
+        if prepared is None:
+            batch.validate()
         S = batch.num_sequences()
         V = self.meta.vocab_size
         if batch.is_empty():
             return ForwardOutput(np.zeros((0, V), np.float32), V, [])
-        tokens, positions, counts, ctx, offs, ids = batch.to_csr()
+        tokens, positions, counts, ctx, offs, ids = prepared or batch.to_csr()
         bd = BatchDesc(len(tokens), S, tokens.ctypes.data, positions.ctypes.data,
                        counts.ctypes.data, ctx.ctypes.data, offs.ctypes.data, ids.ctypes.data,
                        int(batch.has_prefill))

@@ -6,6 +6,7 @@ import subprocess
 import ctypes as C
 
 import numpy as np
+import pytest
 
 from conftest import ROOT
 
@@ -83,3 +84,18 @@ def test_c_struct_layouts_match_the_ctypes_binding():
         assert list(lay[cname]["offsets"]) == fields, cname
         for f in fields:
             assert lay[cname]["offsets"][f] == getattr(py, f).offset, (cname, f)
+
+
+def test_prepared_batch_reuses_the_flattened_arrays():
+    """ForwardBatch.prepare validates once and keeps the CSR arrays that
+    forward() would otherwise rebuild on every call (traits.rs:193-261)."""
+    oh = orion_hip
+    b = oh.ForwardBatch([5, 6, 7], [0, 1, 9], [0, 1], [2, 1], [2, 10], [[3], [4]], True)
+    want = b.to_csr()
+    assert b.prepare() is b
+    for got, w in zip(b._prepared, want):
+        assert np.array_equal(got, w)
+    assert list(want[4]) == [0, 1, 2] and list(want[5]) == [3, 4]
+    bad = oh.ForwardBatch([5], [0, 1], [0], [1], [1], [[3]], True)
+    with pytest.raises(oh.InternalError):
+        bad.prepare()
