@@ -537,3 +537,21 @@ def test_weights_are_kept_once_and_read_back_after_packing(backend):
     gm.upload_weight(oh.W_O, 2, w_o)
     assert np.array_equal(gm.forward(b).logits, g1)
     gm.close()
+
+
+def test_prepared_batch_forward_is_identical(backend):
+    """A batch flattened once (ForwardBatch.prepare) gives bitwise the same
+    logits as one flattened per call; the library still validates it."""
+    spec = small_spec()
+    W = random_weights(spec, np.random.default_rng(77))
+    m = gpu_model(backend, spec, W)
+    toks = [3, 9, 27, 81, 243, 5, 7]
+    pos = [0, 1, 2, 3, 4, 0, 1]
+    b1 = batch(toks, pos, [5, 2], [[0], [1]])
+    b2 = batch(toks, pos, [5, 2], [[0], [1]]).prepare()
+    g1 = m.forward(b1).logits
+    g2 = m.forward(b2).logits
+    assert np.array_equal(g1, g2)
+    g3 = m.forward(b2).logits  # reused arrays, same KV writes
+    assert np.array_equal(g1, g3)
+    m.close()
