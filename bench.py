@@ -31,6 +31,27 @@ BF16_PEAK_TFLOPS = 2500.0  # MI355X dense bf16 MFMA, published
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "paged_decode_cfg2_pmc.txt")
 
 
+def copy_ceiling(be, achieved_gbs, nbytes=1 << 30, reps=10):
+    """This box's HBM copy rate: a 1 GiB device-to-device copy (read + write
+    bytes), median of `reps` event-timed copies after two warm-ups.  A copy
+    moves read and write traffic at once, so it is a practical ceiling for
+    mixed traffic; the read-only decode kernel can pass it."""
+    src, dst = be.alloc(nbytes), be.alloc(nbytes)
+    for _ in range(2):
+        be.memcpy_d2d(dst.ptr, src.ptr, nbytes)
+    be.synchronize()
+    samples = []
+    for _ in range(reps):
+        be.timer_start()
+        be.memcpy_d2d(dst.ptr, src.ptr, nbytes)
+        samples.append(be.timer_stop())
+    src.free()
+    dst.free()
+    gbs = 2 * nbytes / (float(np.median(samples)) * 1e-3) / 1e9
+    return {"copy_GBps": round(gbs, 1), "achieved_over_copy": round(achieved_gbs / gbs, 4),
+            "copy_note": "1 GiB device copy on this box, (read + write bytes) / median time"}
+
+
 def measured_traffic():
     """HBM bytes per launch of the decode split-K kernel, from the committed
     rocprofv3 FETCH_SIZE / WRITE_SIZE summary (None when absent)."""
@@ -643,6 +664,7 @@ def main():
             "merge_kernel_ms": round(merge_avg, 5),
             "merge_kernel_ms_median": round(float(np.median(merge_samples)), 5)
             if len(merge_samples) else None,
+            **copy_ceiling(be, kern_gbs),
         },
         "step_ms_median": round(step_med, 5),
         "value_at_step_median": round(nbytes / (step_med * 1e-3) / 1e9, 1),
@@ -656,12 +678,14 @@ def main():
     if not a.no_prefill:
         result["prefill_cfg3"] = prefill_cfg3(be, head_major=head_major)
     if a.copy_calibration:
-        # A plain device-to-device copy of known size, for scaling the PMC
+        # Plain device-to-device copies of known size, for scaling the PMC
         # byte counters (rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE).
         src, dst = be.alloc(1 << 30), be.alloc(1 << 30)
         for _ in range(3):
             be.memcpy_d2d(dst.ptr, src.ptr, 1 << 30)
         be.synchronize()
+        src.free()
+        dst.free()
         result["copy_calibration_bytes"] = 1 << 30
     be.close()
     if not a.no_e2e:
