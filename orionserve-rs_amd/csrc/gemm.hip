@@ -951,9 +951,17 @@ int gemm_sumsq_slots(int64_t N) {
 // their 31 us reduce launches cost, so they stay whole.)  Not for the SwiGLU
 // epilogue (its column pairs sit in one tile).  ORION_GEMM_TILED_SPLIT=n
 // forces n (measurement knob, read per call).
+// A long K (>= 256 k-steps) with fewer tiles than the resident slots (3
+// workgroups x 256 CUs) is also split, into up to 2 x slots workgroups of at
+// least 64 k-steps: config 5's down projection (K 18944, 504 tiles) went
+// 664-697 -> 585 us + a 37 us reduce with 3 splits, while shorter-K calls
+// with the same tile count (QKV, O) gained nothing.  These long-K splits are
+// preferred, not required: a caller whose scratch cannot hold them (the
+// no-allocation entry point) runs the required count.
 namespace {
 constexpr int64_t kTiledFill = 256;
-int tiled_ksplits(int64_t M, int64_t N, int64_t K) {
+constexpr int64_t kTiledSlots = 768;
+int tiled_ksplits(int64_t M, int64_t N, int64_t K, bool preferred = true) {
   const int64_t tiles = ((N + kTN - 1) / kTN) * ((M + kTM - 1) / kTM);
   const int64_t ksteps = K / kTK;
   if (const char* e = getenv("ORION_GEMM_TILED_SPLIT")) {
@@ -962,15 +970,20 @@ int tiled_ksplits(int64_t M, int64_t N, int64_t K) {
   }
   int s = 1;
   while (s < 8 && tiles * s < kTiledFill && ksteps / (2 * s) >= 16) s *= 2;
+  if (preferred && tiles < kTiledSlots && ksteps >= 256) {
+    int64_t p = std::min<int64_t>(8, 2 * kTiledSlots / tiles);
+    while (p > 1 && ksteps / p < 64) --p;
+    s = std::max<int>(s, (int)p);
+  }
   return s;
 }
 }  // namespace
 
-void gemm_scratch_need(int64_t M, int64_t N, int64_t K, size_t* ws_bytes) {
+void gemm_scratch_need(int64_t M, int64_t N, int64_t K, size_t* ws_bytes, bool preferred) {
   *ws_bytes = 0;
   if (M < 1 || K % 32 != 0) return;
   if (M > 64) {
-    const int s = tiled_ksplits(M, N, K);
+    const int s = tiled_ksplits(M, N, K, preferred);
     if (s > 1) *ws_bytes = (size_t)s * (size_t)M * (size_t)N * sizeof(float);
     return;
   }
@@ -1057,9 +1070,11 @@ hipError_t launch_gemm(hipStream_t st, const float* x, const uint16_t* w, const 
       grid = dim3((unsigned)(((total + 7) / 8) * 8), 1);
     }
     // K splits (tiled_ksplits), when the scratch holds their sums
+    const size_t avail = scratch ? scratch->ws_bytes : 0;
+    auto fits = [&](int s) { return (size_t)s * (size_t)M * (size_t)N * sizeof(float) <= avail; };
     int splits = ep == Epilogue::kSwiGLU ? 1 : tiled_ksplits(M, N, K);
-    const size_t split_bytes = (size_t)splits * (size_t)M * (size_t)N * sizeof(float);
-    if (splits > 1 && (!scratch || scratch->ws_bytes < split_bytes)) splits = 1;
+    if (splits > 1 && !fits(splits)) splits = tiled_ksplits(M, N, K, false);
+    if (splits > 1 && !fits(splits)) splits = 1;
     const int ksteps = (int)(K / kTK), kspan = (ksteps + splits - 1) / splits;
     grid.z = (unsigned)splits;
     float* partial = splits > 1 ? scratch->ws : nullptr;

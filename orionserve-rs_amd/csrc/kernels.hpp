@@ -226,7 +226,9 @@ int gemm_sumsq_slots(int64_t N);
 // Scratch a launch_gemm call of this shape uses: the decode GEMMs' K-slice
 // partials, or the LDS-tiled GEMM's K-split sums (launch_gemm leaves a tiled
 // GEMM unsplit when the scratch it is given is smaller).
-void gemm_scratch_need(int64_t M, int64_t N, int64_t K, size_t* ws_bytes);
+// preferred: include the optional long-K splits (callers that can grow
+// their scratch); false: only what the call requires.
+void gemm_scratch_need(int64_t M, int64_t N, int64_t K, size_t* ws_bytes, bool preferred = true);
 hipError_t launch_gemm(hipStream_t st, const float* x, const uint16_t* w, const float* bias,
                        int64_t M, int64_t N, int64_t K, Epilogue ep, float* out,
                        const GemmScratch* scratch = nullptr, const GemmFuse* fuse = nullptr);

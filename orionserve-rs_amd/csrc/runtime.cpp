@@ -1897,7 +1897,7 @@ ORION_EXPORT int orion_hip_gemm_noalloc(orion_hip_device* dev, const float* d_x,
   Epilogue ep;
   if (int rc = gemm_args(st, d_bias, N, K, epilogue, &ep)) return rc;
   size_t need = 0;
-  gemm_scratch_need(M, N, K, &need);
+  gemm_scratch_need(M, N, K, &need, false);
   if (need > kNoAllocScratchBytes)
     return set_err(ORION_HIP_ERR_BACKEND, st,
                    "M=%lld N=%lld K=%lld needs %zu bytes of split-K scratch; the "
