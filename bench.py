@@ -1,5 +1,5 @@
 """Headline benchmark: paged GQA decode attention at the Llama-3-8B layer shape
-on one MI355X, plus the CPU oracle timed on the same host.
+(benchmark config 2) on one MI355X, plus the CPU oracle timed on the same host.
 
 A "step" is one paged decode-attention pass over the whole batch: 64 query
 rows (one per sequence, contexts U[128, 4096]), 32 query / 8 KV heads,
@@ -65,7 +65,7 @@ def measured_traffic():
 
 
 def prefill_cfg3(be, steps=20, warmup=3, head_major=False):
-    """chunked-prefill causal attention over the paged
+    """benchmark config 3: chunked-prefill causal attention over the paged
     cache as an MFMA contraction (8 seqs x 512-token chunks on prefixes
     U[0,7680], 32q/8kv, d 128, bf16).  Timed per kernel with HIP events."""
     import orion_hip as oh
@@ -174,7 +174,7 @@ def cpu_baseline(case):
 
 
 def decode_e2e(steps=64, seqs=32, seed=20261204, cpu=True):
-    """full decode step of a random-init TinyLlama-1.1B-shape
+    """benchmark config 4: full decode step of a random-init TinyLlama-1.1B-shape
     model (bf16 weights N(0, 0.02), bf16 KV cache), 32 sequences with prompt
     lengths U[16, 1024] (random token ids), prefilled in one forward, then
     `steps` greedy decode steps (device argmax).  The greedy tokens are
@@ -385,7 +385,7 @@ QWEN2_7B_LAYER = dict(H=3584, hq=28, hkv=4, d=128, F=18944, V=1024, eps=1e-6, th
 
 
 def mixed_cfg5(steps=10, warmup=2, seed=20261205):
-    """one Qwen2-7B-shape layer (hidden 3584, 28q/4kv heads,
+    """benchmark config 5: one Qwen2-7B-shape layer (hidden 3584, 28q/4kv heads,
     d 128, ffn 18944, QKV bias; bf16 weights synthetic N(0,0.02), RoPE theta
     1e6) over a mixed continuous batch: 8 prefill chunks of 256 tokens + 192
     decode rows, half the sequences sharing a 2048-token prefix through

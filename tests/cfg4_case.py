@@ -1,4 +1,4 @@
-"""BASELINE config 4 (full decode step of a random-init TinyLlama-1.1B-shape
+"""benchmark config 4 (full decode step of a random-init TinyLlama-1.1B-shape
 model): the batch the bench decodes and the synthetic weights it runs on.
 
 * ``cfg4_case`` draws the bench's exact batch: 32 sequences with prompt

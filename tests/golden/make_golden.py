@@ -1,6 +1,6 @@
 """Writes the golden fixtures under tests/golden/ from the CPU oracle.
 
-cfg1_decode.npz: BASELINE config 1 (4 seqs, ctx U[1,512], bs 16, 8q/2kv,
+cfg1_decode.npz: benchmark config 1 (4 seqs, ctx U[1,512], bs 16, 8q/2kv,
 d 64, f32) — context lengths, block tables, a checksum of the generated
 inputs and the oracle's attention output [4, 8*64].
 tiny_model.npz: the reference's fixture model (transformer.rs:459-523) —

@@ -1,5 +1,5 @@
 """Writes tests/golden/cfg4_greedy_{f32,bf16}kv.npz: the CPU oracle's greedy
-decode of BASELINE config 4 exactly as bench.py runs it.
+decode of benchmark config 4 exactly as bench.py runs it.
 
 The TinyLlama-1.1B-shape model with the library's synthetic bf16 weights
 (seed 20261204, N(0, 0.02)), the bench's 32 sequences (prompts U[16, 1024],

@@ -1,4 +1,4 @@
-"""Seeded paged-attention workloads (BASELINE configs 1 and 2 and edge cases)
+"""Seeded paged-attention workloads (benchmark configs 1 and 2 and edge cases)
 shared by the GPU parity tests, the golden-fixture generator and bench.py."""
 import numpy as np
 
@@ -101,14 +101,14 @@ def rope_rotate(x, cos, sin):
 
 
 def cfg1(seed=20261201):
-    """4 seqs, ctx U[1,512], bs 16, 8q/2kv, d 64, f32, 256-block pool."""
+    """benchmark config 1: 4 seqs, ctx U[1,512], bs 16, 8q/2kv, d 64, f32, 256-block pool."""
     rng = np.random.default_rng(seed)
     ctxs = rng.integers(1, 513, size=4)
     return PagedCase(seed + 1, ctxs, 8, 2, 64, 16, num_blocks=256, dtype="f32")
 
 
 def cfg2(seed=20261202, num_seqs=64, head_major=False):
-    """64 seqs, ctx U[128,4096], bs 16, 32q/8kv, d 128, bf16 KV,
+    """benchmark config 2: 64 seqs, ctx U[128,4096], bs 16, 32q/8kv, d 128, bf16 KV,
     pool 1.25x the blocks needed, scattered tables; Q and cached K rotated by
     RoPE (theta 500000) at their positions before caching."""
     rng = np.random.default_rng(seed)
@@ -158,7 +158,7 @@ class PrefillCase(PagedCase):
 
 
 def cfg3(seed=20261203, head_major=False):
-    """8 seqs x 512-token chunk on a prefix U[0,7680], bs 16,
+    """benchmark config 3: 8 seqs x 512-token chunk on a prefix U[0,7680], bs 16,
     32q/8kv, d 128, bf16 inputs, scattered tables."""
     rng = np.random.default_rng(seed)
     prefixes = rng.integers(0, 7681, size=8)
@@ -168,7 +168,7 @@ def cfg3(seed=20261203, head_major=False):
 
 class MixedBatch:
     """A continuous batch mixing prefill chunks and decode rows, with prefix
-    sharing (BASELINE config 5's structure).  Sequence s has `cached[s]`
+    sharing (benchmark config 5's structure).  Sequence s has `cached[s]`
     tokens in the cache before this step and contributes `counts[s]` new rows
     at positions cached[s] .. cached[s] + counts[s] - 1.  Sharing sequences
     start with the same `prefix` tokens, stored once: their tables begin with
@@ -234,7 +234,7 @@ class MixedBatch:
 
 
 def cfg5_batch(vocab, seed=20261205):
-    """8 prefill chunks of 256 + 192 decodes; half of the
+    """benchmark config 5: 8 prefill chunks of 256 + 192 decodes; half of the
     200 sequences share a 2048-token prefix; other context lognormal (median
     1024; shape 1.0, not given by the config) capped at 16384; block 16."""
     return MixedBatch(seed, 8, 256, 192, 0.5, 2048, 1024, 1.0, 16384, 16, vocab)

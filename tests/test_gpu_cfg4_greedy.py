@@ -1,4 +1,4 @@
-"""Greedy-token parity at BASELINE config 4 exactly as the bench decodes it.
+"""Greedy-token parity at benchmark config 4 exactly as the bench decodes it.
 
 The HIP model (TinyLlama-1.1B shape, the bench's synthetic bf16 weights)
 runs the bench's batch: 32 sequences, prompts U[16, 1024], scattered block

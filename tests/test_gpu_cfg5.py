@@ -1,4 +1,4 @@
-"""BASELINE config 5 at full size: a mixed continuous batch with prefix sharing
+"""benchmark config 5 at full size: a mixed continuous batch with prefix sharing
 at the Qwen2-7B layer shape (28 query / 4 KV heads, head_dim 128, hidden
 3584, QKV bias, bf16): 8 prefill chunks of 256 tokens and 192 decode rows
 over 200 sequences, half of them sharing a 2048-token prefix through
