@@ -340,7 +340,7 @@ def validate(expected, actual, tol: Tolerance):
 class OracleTransformer:
     """TransformerModel (transformer.rs:137-443) with an f32 KV arena (the
     reference's), or with every K/V element rounded to bf16 when written
-    (kv_bf16=True: the KV dtype of BASELINE's bf16 configurations)."""
+    (kv_bf16=True: the KV dtype of the bf16 benchmark configurations)."""
 
     def __init__(self, num_layers, hidden, num_q_heads, num_kv_heads, head_dim, ffn, vocab,
                  max_positions, rms_norm_eps, rope_theta, has_qkv_bias, tied_lm_head, num_blocks,

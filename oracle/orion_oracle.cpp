@@ -656,7 +656,7 @@ struct OracleModel {
   std::vector<float> rope_cos, rope_sin;
   std::vector<float> kv;
   KvDims dims;
-  // Store K/V rounded to bf16 (nearest even), the KV dtype of BASELINE's
+  // Store K/V rounded to bf16 (nearest even), the KV dtype of the benchmark's
   // bf16 configurations; the reference's own KvStore is f32 (false).
   bool kv_bf16 = false;
 };
