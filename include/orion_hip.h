@@ -398,10 +398,12 @@ int orion_hip_gemm(orion_hip_device* dev, const float* d_x, const uint16_t* d_w,
  * graph capture or a serving loop that forbids hipMalloc).  Same arguments,
  * kernels and results as orion_hip_gemm; the split-K partial tiles of
  * decode-shaped calls (M <= 64) and the K-split sums of larger calls with
- * fewer output tiles than CUs go to a fixed 64 MiB device array that each
- * GPU holds for the life of the process, instead of the device's grown
- * scratch.  A shape whose scratch exceeds 64 MiB is refused with
- * ORION_HIP_ERR_BACKEND.  Every call on one GPU shares that GPU's array:
+ * few output tiles go to a fixed 64 MiB device array that each GPU holds
+ * for the life of the process, instead of the device's grown scratch.  A
+ * shape whose required scratch exceeds 64 MiB is refused with
+ * ORION_HIP_ERR_BACKEND.  The optional extra K splits of long-K calls (K >=
+ * 8192 with fewer than 768 output tiles) are dropped when they do not fit,
+ * so such a call can differ from orion_hip_gemm in f32 summation order.  Every call on one GPU shares that GPU's array:
  * calls that overlap on one GPU (other streams, other threads) race. */
 int orion_hip_gemm_noalloc(orion_hip_device* dev, const float* d_x, const uint16_t* d_w,
                            const float* d_bias, int64_t M, int64_t N, int64_t K, int epilogue,
