@@ -113,10 +113,14 @@ def test_rmsnorm_matches_oracle(backend, rows, cols):
     assert np.all(do.download(np.float32, (1, cols)) == 0)
 
 
-@pytest.mark.parametrize("dtype,head_major", [("f32", False), ("bf16", False), ("bf16", True)])
-def test_rope_and_cache_is_bit_exact(backend, dtype, head_major):
+@pytest.mark.parametrize("dtype,head_major,shift", [("f32", False, 0), ("bf16", False, 0),
+                                                    ("bf16", True, 0), ("f32", False, 1),
+                                                    ("bf16", False, 1)])
+def test_rope_and_cache_is_bit_exact(backend, dtype, head_major, shift):
     # RoPE + slot mapping + KV write against the oracle's apply_rope and
     # KvStore.write: the rotated Q, and every arena element, bit for bit.
+    # shift 1 moves the q/k/v inputs off 16-byte alignment, which takes the
+    # one-element-per-thread kernel instead of the vectorised one.
     rng = np.random.default_rng(17)
     L, nb, bs, hkv, hq, d = 2, 40, 16, 4, 16, 128
     layer = 1
@@ -137,11 +141,13 @@ def test_rope_and_cache_is_bit_exact(backend, dtype, head_major):
     arena_el = L * nb * 2 * bs * hkv * d
     darena = backend.alloc(arena_el * esz)
     oh._check(backend.lib.orion_hip_memset(backend.handle, darena.ptr, 0, arena_el * esz))
-    dqkv, dqo = backend.to_device(qkv), backend.alloc(n * hq * d * 4)
+    dqkv_buf = backend.to_device(np.concatenate([np.zeros(shift, np.float32), qkv.ravel()]))
+    dqo = backend.alloc(n * hq * d * 4)
+    qkv_ptr = dqkv_buf.ptr + 4 * shift  # the q/k/v base, `shift` floats into the buffer
     bufs = [backend.to_device(a) for a in (positions, row_seq, offs, ids, rope.cos, rope.sin)]
     dpos, drs, dbo, dbi, dcos, dsin = bufs
-    oh.rope_and_cache(backend, kvl, darena.ptr, layer, n, hq, dqkv.ptr, qkvd, dqo.ptr,
-                      dqkv.ptr + hq * d * 4, qkvd, dqkv.ptr + (hq + hkv) * d * 4, qkvd, dpos.ptr,
+    oh.rope_and_cache(backend, kvl, darena.ptr, layer, n, hq, qkv_ptr, qkvd, dqo.ptr,
+                      qkv_ptr + hq * d * 4, qkvd, qkv_ptr + (hq + hkv) * d * 4, qkvd, dpos.ptr,
                       drs.ptr, dbo.ptr, dbi.ptr, dcos.ptr, dsin.ptr)
     q_got = dqo.download(np.float32, (n, hq * d))
     raw = darena.download(np.uint16 if dtype == "bf16" else np.float32, (arena_el,))
