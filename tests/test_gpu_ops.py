@@ -96,7 +96,9 @@ def test_gemm_swiglu_epilogue(backend, M, F, K):
         b.free()
 
 
-@pytest.mark.parametrize("rows,cols", [(1, 64), (5, 2048), (33, 3584), (3, 100)])
+@pytest.mark.parametrize("rows,cols", [(1, 64), (5, 2048), (33, 3584), (3, 100),
+                                       # the scalar path: odd width, wider than 8192
+                                       (3, 99), (2, 10000)])
 def test_rmsnorm_matches_oracle(backend, rows, cols):
     rng = np.random.default_rng(rows * cols)
     x = (rng.standard_normal((rows, cols)) * 3).astype(np.float32)
