@@ -54,13 +54,14 @@ def test_gemm_bias_and_accumulate_epilogues(backend, M):
 
 
 @pytest.mark.parametrize("M,N,K", [(400, 272, 2048), (1100, 1024, 3584), (200, 1024, 3584),
-                                   (2048, 2048, 8192)])
+                                   (2048, 2048, 8192), (300, 8192, 4096)])
 def test_tiled_gemm_k_splits(backend, monkeypatch, M, N, K):
     # LDS-tiled shapes with few output tiles split K (sums reduced in split
     # order by a second kernel): store with bias, and accumulate, against
     # float64 and against the unsplit kernel (ORION_GEMM_TILED_SPLIT=1).
     # 200 x 1024 x 3584 is config 5's LM head on the last rows; 2048 x 2048 x
-    # 8192 (256 tiles, 256 k-steps) takes the long-K rule's 4 splits.
+    # 8192 (256 tiles, 256 k-steps) takes the long-K rule's 4 splits; 300 x
+    # 8192 x 4096 splits K with the wide 128 x 256 tiles.
     for kw in (dict(bias=True), dict(accumulate=True)):
         got, want, ref64 = gemm_case(backend, M, N, K, seed=M + K, **kw)
         monkeypatch.setenv("ORION_GEMM_TILED_SPLIT", "1")
