@@ -793,15 +793,15 @@ GemvShape gemv_shape(int64_t M, int64_t N, int64_t K, bool deferred = false) {
   }
   if (knob_nt) g.nt = knob_nt;
   if (knob_ks) g.ks = knob_ks;
-  // ORION_GEMV_GEOM="defer:NT:KS,longk:NT:KS,wide:NT:KS,other:NT:KS" (any
-  // subset): per-group override (measurement knob; NT in {1, 2, 4}, KS in
-  // {4, 8, 16}).
-  static const std::array<std::pair<int, int>, 4> geom = [] {
-    std::array<std::pair<int, int>, 4> r{};
+  // ORION_GEMV_GEOM="defer:NT:KS,longk:NT:KS,wide:NT:KS,other:NT:KS,head:NT:KS"
+  // (any subset): per-group override (measurement knob; NT in {1, 2, 4}, KS
+  // in {4, 8, 16}); "head" (N > 16384, an LM head) refines "wide".
+  static const std::array<std::pair<int, int>, 5> geom = [] {
+    std::array<std::pair<int, int>, 5> r{};
     const char* e = getenv("ORION_GEMV_GEOM");
     if (!e) return r;
-    const char* names[4] = {"defer", "longk", "wide", "other"};
-    for (int i = 0; i < 4; ++i) {
+    const char* names[5] = {"defer", "longk", "wide", "other", "head"};
+    for (int i = 0; i < 5; ++i) {
       const char* p = strstr(e, names[i]);
       int nt = 0, ks = 0;
       if (p && sscanf(p + strlen(names[i]), ":%d:%d", &nt, &ks) == 2 &&
@@ -811,7 +811,8 @@ GemvShape gemv_shape(int64_t M, int64_t N, int64_t K, bool deferred = false) {
     return r;
   }();
   {
-    const int grp = deferred ? 0 : K > 4096 ? 1 : N > 4096 ? 2 : 3;
+    int grp = deferred ? 0 : K > 4096 ? 1 : N > 4096 ? 2 : 3;
+    if (grp == 2 && N > 16384 && geom[4].first) grp = 4;
     if (geom[grp].first) g.nt = geom[grp].first, g.ks = geom[grp].second;
   }
   g.n_tiles = (int)((N + 64 * g.nt - 1) / (64 * g.nt));
