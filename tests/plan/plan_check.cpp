@@ -7,7 +7,9 @@
 //     table offset of its first block, and split indices 0 .. n-1 of the
 //     row's n = row_nsplit pieces, with n <= max_splits;
 //   * cut every row into pieces of one length, the last piece no longer;
-//   * when balanced, fit in at most four rounds of wave slots.
+//   * when balanced, fit in at most four rounds of wave slots;
+//   * flag exactly the items whose blocks another planned row (or the same
+//     row twice) also attends, and choose streaming / mixed loads to match.
 // Prints one line per failure and a summary; exit status 1 on any failure.
 #include "kernels.hpp"
 
@@ -37,11 +39,16 @@ int main(int argc, char** argv) {
     std::vector<int32_t> row_seq(rows);
     std::vector<int64_t> off(rows + 1, 0);
     std::vector<uint32_t> ids;
+    // every seventh trial: rows start with the leading blocks of row 0 (a
+    // shared prefix, as prefix caching produces)
+    const bool prefix = trial % 7 == 3;
     for (int r = 0; r < rows; ++r) {
       pos[r] = rng() % maxctx;
       row_seq[r] = r;
       const int nb = (int)pos[r] / bs + 1;
-      for (int j = 0; j < nb; ++j) ids.push_back(rng() % 100000);
+      for (int j = 0; j < nb; ++j)
+        ids.push_back(prefix && r > 0 && j < std::min<int64_t>(8, off[1]) ? ids[j]
+                                                                          : rng() % 100000);
       off[r + 1] = off[r] + nb;
     }
     std::vector<uint8_t> skip(rows, 0);
@@ -104,6 +111,26 @@ int main(int argc, char** argv) {
     }
     if (plan.balanced && (int64_t)plan.work.size() > 4 * slots)
       fail(trial, "balanced plan overfills four rounds", -1);
+    // shared blocks: attended twice over the planned rows
+    std::vector<int> uses(100000, 0);  // block ids are drawn below 100000
+    for (int r = 0; r < rows; ++r) {
+      if (use_skip && skip[r]) continue;
+      const int nb = ((int)pos[r] + bs) >> bs_log2;
+      for (int j = 0; j < nb; ++j) uses[ids[off[r] + j]]++;
+    }
+    bool any_shared = false, any_private = false;
+    for (const DecodeWork& w : plan.work) {
+      const int nblk = ((w.end - 1) >> bs_log2) - (w.start >> bs_log2) + 1;
+      bool sh = false;
+      for (int j = 0; j < nblk; ++j) sh = sh || uses[ids[w.tbl_off + j]] > 1;
+      if ((w.shared != 0) != sh) fail(trial, "shared flag", w.item / hkv);
+      any_shared = any_shared || sh;
+      any_private = any_private || !sh;
+    }
+    bool any_shared_block = false;
+    for (int u : uses) any_shared_block = any_shared_block || u > 1;
+    if (plan.stream_kv != !any_shared_block) fail(trial, "stream_kv", -1);
+    if (plan.mixed_kv != (any_shared_block && any_private)) fail(trial, "mixed_kv", -1);
   }
   printf("%d trials, %d balanced, %d failures\n", trials, balanced, fails);
   return fails ? 1 : 0;
