@@ -3,7 +3,9 @@ against orion_hip_gemm, through the C-ABI: identical kernels, so the outputs
 must be bit-identical.  Calls run back to back on one device, each later one
 smaller than the one before, so a call that read partial tiles left by the
 previous (larger) call would show.  A shape whose split-K partials exceed the
-fixed device array is refused with a Backend error before any launch."""
+fixed device array is refused with a Backend error before any launch; a
+long-K shape whose optional extra K splits do not fit runs with fewer splits
+(the same kernels, f32 sums in another order)."""
 import ctypes as C
 
 import numpy as np
@@ -60,6 +62,16 @@ def test_noalloc_gemm_twice_in_a_row_smaller_second(backend):
     for (M, N, K) in [(48, 16384, 4096), (3, 640, 2048)]:
         a, c = run_both(backend, M, N, K, oh.GEMM_STORE, False, seed=M)
         assert np.array_equal(a.view(np.uint32), c.view(np.uint32)), (M, N, K)
+
+
+def test_noalloc_gemm_runs_long_k_without_its_optional_splits(backend):
+    # config 5's down projection: 3 preferred K splits need 96 MB of sums, more
+    # than the 64 MiB array, so the no-allocation call runs it unsplit.
+    M, N, K = 2240, 3584, 18944
+    a, c = run_both(backend, M, N, K, oh.GEMM_ACCUMULATE, False, seed=5)
+    scale = float(np.abs(a).max())
+    assert np.isfinite(c).all()
+    assert float(np.abs(a - c).max()) <= 2e-5 * scale + 1e-6
 
 
 def test_noalloc_gemm_refuses_shapes_beyond_its_scratch(backend):
