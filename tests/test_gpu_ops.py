@@ -36,7 +36,9 @@ def gemm_case(be, M, N, K, bias=False, accumulate=False, seed=0):
                                    (65, 96, 256), (130, 2048, 512), (32, 32000, 2048),
                                    # LDS-tiled (prefill) kernel: M >= 256, ragged M/N edges
                                    (256, 128, 32), (300, 96, 256), (1000, 2560, 2048),
-                                   (777, 2048, 5632), (513, 32000, 2048)])
+                                   (777, 2048, 5632), (513, 32000, 2048),
+                                   # wide (128 x 256) tiles with a ragged last column tile
+                                   (300, 8200, 512)])
 def test_gemm_matches_linear(backend, M, N, K):
     got, want, ref64 = gemm_case(backend, M, N, K, seed=M + N + K)
     scale = np.abs(ref64).max()
