@@ -74,7 +74,8 @@ def test_tiled_gemm_k_splits(backend, monkeypatch, M, N, K):
         assert np.abs(got - one).max() <= 2e-5 * scale + 1e-6, kw
 
 
-@pytest.mark.parametrize("M,F,K", [(5, 48, 64), (32, 5632, 2048), (300, 176, 256), (600, 5632, 2048)])
+@pytest.mark.parametrize("M,F,K", [(5, 48, 64), (32, 5632, 2048), (300, 176, 256), (600, 5632, 2048),
+                                   (300, 4104, 256)])  # wide tiles, ragged last tile
 def test_gemm_swiglu_epilogue(backend, M, F, K):
     # Gate and up rows interleaved in groups of 8 (the model's fused W_gu
     # layout); the epilogue returns swiglu(x.Wg^T, x.Wu^T) (tensor.rs:175-189).
