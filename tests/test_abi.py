@@ -99,3 +99,13 @@ def test_prepared_batch_reuses_the_flattened_arrays():
     bad = oh.ForwardBatch([5], [0, 1], [0], [1], [1], [[3]], True)
     with pytest.raises(oh.InternalError):
         bad.prepare()
+
+
+def test_bench_measures_one_gpu_only():
+    """bench.py --gpus N with N > 1 exits with a message (this build measures
+    one GPU); the check runs before the library is loaded."""
+    import sys
+    p = subprocess.run([sys.executable, os.path.join(ROOT, "bench.py"), "--gpus", "2"],
+                       capture_output=True, text=True, timeout=120)
+    assert p.returncode == 2
+    assert "one GPU" in p.stderr
