@@ -18,6 +18,7 @@ SOURCES = [
     "attention_decode.hip",
     "decode_plan.cpp",
     "attention_prefill.hip",
+    "prefill_plan.cpp",
     "gemm.hip",
     "elementwise.hip",
     "runtime.cpp",

@@ -49,7 +49,7 @@ typedef __attribute__((address_space(3))) v4s lds_v4s;
 typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 typedef float f32x2 __attribute__((ext_vector_type(2)));
 
-constexpr int kNR = 2;                      // 16-row MFMA tiles per wave
+constexpr int kNR = kPrefillWaveRowTiles;   // 16-row MFMA tiles per wave
 constexpr int kBN = 64;                     // keys per tile
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kLazy = 8.0f;               // log2 units: weights stay <= 2^8
@@ -344,7 +344,11 @@ __global__ void __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu
         mx = fmaxf(mx, __shfl_xor(mx, 16));
         mx = fmaxf(mx, __shfl_xor(mx, 32));
         const float m_new = fmaxf(m[rt], mx);
-        const float alpha = __builtin_amdgcn_exp2f((m[rt] - m_new) * scale_log2);
+        // A query with no key yet in this part (every score so far masked)
+        // keeps m = -inf while other lanes of the wave raise theirs: its
+        // alpha must be 1 (o and lsum are still 0), not exp2(-inf + inf) = NaN.
+        const float alpha =
+            m_new == -INFINITY ? 1.f : __builtin_amdgcn_exp2f((m[rt] - m_new) * scale_log2);
         m[rt] = m_new;
         lsum[rt] *= alpha;
 #pragma unroll
@@ -465,89 +469,6 @@ __global__ void __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu
         *reinterpret_cast<float4*>(op + 16 * d) =
             make_float4(o[rt][d][0] * inv, o[rt][d][1] * inv, o[rt][d][2] * inv,
                         o[rt][d][3] * inv);
-    }
-  }
-}
-
-// Workgroup shape: 8 waves with a 3-stage K/V ring (one workgroup per CU,
-// 96 KiB of LDS at d = 128), or 4 waves with 2 stages (two per CU).
-// ORION_PREFILL_WAVES=4 selects the latter (measurement knob).
-static int prefill_waves() {
-  static const int w = [] {
-    const char* e = getenv("ORION_PREFILL_WAVES");
-    return (e && atoi(e) == 4) ? 4 : 8;
-  }();
-  return w;
-}
-
-int prefill_tile_rows() { return prefill_waves() * 16 * kNR; }
-
-// Key parts: a sequence is cut into nparts key ranges when its longest tile
-// reads more than an even share of all the tiles' key reads over the CUs
-// (and at least kMinPartTiles key tiles per part), so one long-prefix chunk
-// no longer sets the launch's length while the other CUs idle.  Every tile
-// of the sequence gets the same nparts (a row's heads can straddle two
-// tiles, and the merge counts parts per row).
-constexpr int kMinPartTiles = 16;
-
-void build_prefill_order(const int32_t* row_start, const int32_t* row_count,
-                         const uint32_t* first_pos, int64_t num_seqs, int64_t group, int64_t hkv,
-                         int64_t cus, PrefillPlan* plan) {
-  const int64_t kBM = prefill_tile_rows();
-  struct Tile {
-    int64_t seq, tile, kv_tiles;
-  };
-  std::vector<Tile> tiles;
-  int64_t total = 0;
-  for (int64_t s = 0; s < num_seqs; ++s) {
-    const int64_t packed = (int64_t)row_count[s] * group;
-    for (int64_t t = 0; t * kBM < packed; ++t) {
-      // keys the tile's last packed row attends (the kernel's kv_len)
-      const int64_t kv_len = (int64_t)first_pos[s] + (std::min(packed, (t + 1) * kBM) - 1) / group + 1;
-      const int64_t kvt = (kv_len + 63) / 64;
-      tiles.push_back({s, t, kvt});
-      total += kvt;
-    }
-  }
-  // ORION_PREFILL_SPLIT=0 keeps every sequence whole (measurement knob, read per call)
-  const char* split_env = getenv("ORION_PREFILL_SPLIT");
-  if (split_env && split_env[0] == '0') cus = 0;
-  const int64_t share = cus > 0 ? std::max<int64_t>((total * hkv + cus - 1) / cus, kMinPartTiles)
-                                : INT64_MAX;
-  std::vector<int64_t> seq_parts(num_seqs, 1);
-  for (const Tile& t : tiles)
-    if (t.kv_tiles > share)
-      seq_parts[t.seq] = std::max(seq_parts[t.seq], (t.kv_tiles + share - 1) / share);
-  std::vector<std::pair<int64_t, PrefillTile>> items;
-  for (const Tile& t : tiles) {
-    // every tile of a split sequence writes all nparts parts (a short tile's
-    // last parts may read no key: they write empty partials the merge weighs 0)
-    const int64_t np = seq_parts[t.seq];
-    const int64_t per = (t.kv_tiles + np - 1) / np;
-    const int32_t nparts = (int32_t)np;
-    for (int64_t k = 0; k < np; ++k) {
-      const int64_t a = std::min(t.kv_tiles, k * per), b = std::min(t.kv_tiles, a + per);
-      items.push_back({b - a, PrefillTile{(int32_t)t.seq, (int32_t)t.tile, (int32_t)a, (int32_t)b,
-                                          (int32_t)k, nparts}});
-    }
-  }
-  std::stable_sort(items.begin(), items.end(),
-                   [](const auto& a, const auto& b) { return a.first > b.first; });
-  plan->order.clear();
-  for (const auto& it : items) plan->order.push_back(it.second);
-  // rows whose results come in parts
-  int64_t rows = 0;
-  for (int64_t s = 0; s < num_seqs; ++s)
-    rows = std::max<int64_t>(rows, (int64_t)row_start[s] + row_count[s]);
-  plan->row_parts.assign(rows, 0);
-  plan->split_rows.clear();
-  plan->max_parts = 1;
-  for (int64_t s = 0; s < num_seqs; ++s) {
-    if (seq_parts[s] < 2) continue;
-    plan->max_parts = std::max<int>(plan->max_parts, (int)seq_parts[s]);
-    for (int64_t r = 0; r < row_count[s]; ++r) {
-      plan->row_parts[row_start[s] + r] = (int32_t)seq_parts[s];
-      plan->split_rows.push_back((int32_t)(row_start[s] + r));
     }
   }
 }

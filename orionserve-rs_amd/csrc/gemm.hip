@@ -1077,6 +1077,10 @@ hipError_t launch_gemm(hipStream_t st, const float* x, const uint16_t* w, const 
     if (splits > 1 && !fits(splits)) splits = tiled_ksplits(M, N, K, false);
     if (splits > 1 && !fits(splits)) splits = 1;
     const int ksteps = (int)(K / kTK), kspan = (ksteps + splits - 1) / splits;
+    // every split must start below K: with kspan rounded up, ceil(ksteps /
+    // kspan) splits cover K (a forced count such as 16 splits of 66 k-steps
+    // would otherwise leave splits 14 and 15 starting past the last row)
+    splits = (ksteps + kspan - 1) / kspan;
     grid.z = (unsigned)splits;
     float* partial = splits > 1 ? scratch->ws : nullptr;
     // ORION_GEMM_ACT=bf16 rounds the activations to bf16 (one MFMA per

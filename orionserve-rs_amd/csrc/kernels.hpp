@@ -120,6 +120,8 @@ struct PrefillPlan {
   std::vector<int32_t> split_rows, row_parts;
 };
 int prefill_tile_rows();  // packed rows per prefill workgroup
+int prefill_waves();      // waves per prefill workgroup (8, or 4 with ORION_PREFILL_WAVES=4)
+constexpr int kPrefillWaveRowTiles = 2;  // 16-row MFMA tiles per prefill wave
 // cus: compute units (one prefill workgroup each); hkv: KV heads (workgroups
 // per work-list entry); cus = 0 never splits.
 void build_prefill_order(const int32_t* row_start, const int32_t* row_count,

@@ -82,16 +82,33 @@ def test_shapes_against_oracle(backend, hq, hkv, d, bs, hilo, head_major):
     assert float(np.abs(got - want).max()) <= (1e-4 if hilo else 1e-2)
 
 
+# (prefixes, chunks, hq, hkv, d): the first is config 5's imbalance (one chunk
+# on a 9,000-token prefix beside short ones: parts, but no empty part and no
+# part boundary inside a row tile); the second is cut by the planner (256 CUs)
+# into 27 parts with 3 empty parts and a part whose first key lies inside the
+# positions of one 16-row MFMA tile of queries (some attend no key of the
+# part, others do).  tests/test_prefill_plan.py asserts those plan shapes on
+# the CPU, so this test cannot silently stop covering them.
+KEY_PART_CASES = [
+    ([9000, 400, 60, 0], [256, 256, 100, 1500], 28, 4, 128),
+    ([0, 0, 0, 26474], [2575, 414, 1096, 343], 2, 1, 128),
+]
+
+
+@pytest.mark.parametrize("which", [0, 1])
 @pytest.mark.parametrize("hilo", [False, True])
-def test_key_parts_for_long_prefixes(backend, monkeypatch, hilo):
+def test_key_parts_for_long_prefixes(backend, monkeypatch, hilo, which):
     # Sequences whose tiles read far more keys than an even share of the CUs
-    # are cut into key parts (partial results merged afterwards): one chunk on
-    # a 9,000-token prefix beside short ones (config 5's imbalance), and a
-    # prefix-0 chunk of 1,500 rows whose first tiles read fewer key tiles than
-    # the sequence has parts (empty parts).  Against the oracle on sampled
-    # rows and against ORION_PREFILL_SPLIT=0 (whole sequences).
-    case = PrefillCase(31, [9000, 400, 60, 0], [256, 256, 100, 1500], 28, 4, 128, 16)
+    # are cut into key parts (partial results merged afterwards).  Against the
+    # oracle on sampled rows (every row of the split sequences' chunks in the
+    # second case) and against ORION_PREFILL_SPLIT=0 (whole sequences); every
+    # output finite.
+    prefixes, chunks, hq, hkv, d = KEY_PART_CASES[which]
+    case = PrefillCase(31 + which, prefixes, chunks, hq, hkv, d, 16)
     rows = sample_rows(case, 24, seed=3)
+    if which == 1:
+        a = int(case.row_start[3])
+        rows = np.union1d(rows, np.arange(a, a + int(case.row_count[3])))
     want = case.oracle_rows(rows)
     got = run_prefill(backend, case, hilo)
     monkeypatch.setenv("ORION_PREFILL_SPLIT", "0")

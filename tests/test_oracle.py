@@ -39,25 +39,34 @@ def test_linear_rejects_mismatched_shapes():  # tensor.rs:343-355
 
 
 def test_linear_is_the_sequential_f32_dot():
-    # The reference accumulates left to right in f32 from 0.0; check the
-    # restatement bit-for-bit against an explicit numpy f32 loop, and against
-    # float64 within f32 rounding.  Sizes cover the 4-row blocking remainder.
+    # The reference accumulates left to right in f32 from 0.0 (tensor.rs:96-130).
+    # The restatement runs 16-row blocks x column pairs in vector registers;
+    # check it bit for bit against an explicit f32 loop (each product rounded,
+    # then each sum) at row counts inside one block, exactly one, and several
+    # with ragged ends (n = 17, 33, 48), odd and even out_features (a column
+    # pair cut short) and K not a multiple of 4, and against float64 within
+    # f32 rounding.
     rng = np.random.default_rng(1)
-    for n in (1, 3, 4, 7):
-        x = rng.standard_normal((n, 37)).astype(np.float32)
-        w = rng.standard_normal((5, 37)).astype(np.float32)
-        b = rng.standard_normal(5).astype(np.float32)
-        out = orc.linear(x, w, b)
-        ref = np.zeros((n, 5), np.float32)
-        for i in range(n):
-            for j in range(5):
-                acc = np.float32(0)
-                for t in range(37):
-                    acc = np.float32(acc + np.float32(x[i, t] * w[j, t]))
-                ref[i, j] = np.float32(acc + b[j])
-        assert np.array_equal(out, ref)
-        np.testing.assert_allclose(out, x.astype(np.float64) @ w.T.astype(np.float64) + b,
-                                   rtol=1e-5, atol=1e-5)
+    for n in (1, 3, 4, 7, 16, 17, 33, 48):
+        for out_f, k in ((5, 37), (6, 38), (1, 3)):
+            x = rng.standard_normal((n, k)).astype(np.float32)
+            w = rng.standard_normal((out_f, k)).astype(np.float32)
+            b = rng.standard_normal(out_f).astype(np.float32)
+            out = orc.linear(x, w, b)
+            acc = np.zeros((n, out_f), np.float32)
+            for t in range(k):  # vectorised over (i, j); sequential over t
+                acc = (acc + (x[:, t, None] * w[None, :, t]).astype(np.float32)).astype(np.float32)
+            ref = (acc + b[None, :]).astype(np.float32)
+            assert np.array_equal(out, ref), (n, out_f, k)
+            np.testing.assert_allclose(out, x.astype(np.float64) @ w.T.astype(np.float64) + b,
+                                       rtol=1e-5, atol=1e-5)
+    # a slip in the block index (rows of block 2 taken from block 1) shows
+    # as a swapped row: rows must depend on their own inputs only
+    x = rng.standard_normal((48, 8)).astype(np.float32)
+    w = rng.standard_normal((3, 8)).astype(np.float32)
+    full = orc.linear(x, w)
+    for i in (0, 15, 16, 31, 32, 47):
+        assert np.array_equal(full[i], orc.linear(x[i:i + 1], w)[0])
 
 
 def test_rms_norm_normalizes_to_unit_rms():  # tensor.rs:357-373
