@@ -83,7 +83,12 @@ def prefill_cfg3(be, steps=20, warmup=3, head_major=False):
     res = {"workload": "chunked-prefill attention, config 3: 8 seqs x 512-token chunks, prefix "
                        "U[0,7680], 32q/8kv, head_dim 128, bf16, block 16",
            "flops_per_call": flops}
-    for hilo in (False, True):
+    rng = np.random.default_rng(3)
+    rows = np.array(sorted({r for c in range(case.S)
+                            for r in [512 * c, 512 * c + 511] + list(512 * c + rng.integers(
+                                0, 512, size=30))}))
+    want = case.oracle_rows(rows)
+    for hilo, key in ((0, "bf16"), (1, "hilo"), (2, "q_hilo"), (3, "p_hilo")):
         def call():
             oh.paged_attention_prefill(be, kv, arena.ptr, 0, dq.ptr, case.hq, case.S, drs.ptr,
                                        drc.ptr, dfp.ptr, dbo.ptr, dbi.ptr, 512,
@@ -97,19 +102,17 @@ def prefill_cfg3(be, steps=20, warmup=3, head_major=False):
         be.kernel_timing(False)
         ms = float(np.median(samples))
         tf = flops / (ms * 1e-3) / 1e12
-        key = "hilo" if hilo else "bf16"
         res[key] = {"ms": round(ms, 4), "ms_mean": round(float(samples.mean()), 4),
                     "launches": int(len(samples)), "tflops": round(tf, 1),
                     "frac_of_bf16_peak": round(tf / BF16_PEAK_TFLOPS, 4)}
-        # spot check of the timed output: the first and last row of every
-        # chunk (all 32 heads); the full-size parity test checks ~200 rows
+        # check of the timed output: the first, the last and 30 random rows
+        # of every chunk (all 32 heads) against the oracle
         got = dout.download(np.float32, (n, case.hq * case.d))
-        rows = np.array(sorted({r for c in range(case.S) for r in (512 * c, 512 * c + 511)}))
-        res[key]["max_abs_err_vs_oracle"] = float(
-            np.abs(got[rows] - case.oracle_rows(rows)).max())
+        res[key]["max_abs_err_vs_oracle"] = float(np.abs(got[rows] - want).max())
         res[key]["rows_checked"] = f"{len(rows)} of {n}"
-    res["operands"] = ("bf16: Q and softmax weights rounded to bf16 (MFMA rate); hilo: each as "
-                       "a hi+lo bf16 pair (2x MFMA work)")
+    res["operands"] = ("bf16: Q and softmax weights P rounded to bf16 (MFMA rate); hilo: each as "
+                       "a hi+lo bf16 pair (2x MFMA work); q_hilo: Q as a pair, P rounded; "
+                       "p_hilo: Q rounded, P as a pair")
     for b in bufs:
         b.free()
     return res
@@ -179,7 +182,8 @@ def decode_e2e(steps=64, seqs=32, seed=20261204, cpu=True):
     lengths U[16, 1024] (random token ids), prefilled in one forward, then
     `steps` greedy decode steps (device argmax).  The greedy tokens are
     compared with the CPU oracle's greedy decode of the same batch
-    (tests/golden/cfg4_greedy.npz).  Returns a dict of results."""
+    (tests/golden/cfg4_greedy_bf16kv.npz), and an untimed f32-KV run with the
+    reference-exact oracle (cfg4_greedy_f32kv.npz).  Returns a dict of results."""
     import orion_hip as oh
     from cfg4_case import TINYLLAMA, cfg4_case
 
@@ -263,7 +267,19 @@ def decode_e2e(steps=64, seqs=32, seed=20261204, cpu=True):
     res["hbm_bytes_per_step"] = int(res["weight_bytes_per_step"] + (kv_read + kv_write) / n_steps)
     res["frac_of_hbm_roofline"] = round(
         res["hbm_bytes_per_step"] / (res["decode_ms_per_step"] * 1e-3) / HBM_PEAK_GBS / 1e9, 4)
-    res["greedy_vs_oracle"] = greedy_vs_golden(generated, steps, seqs)
+    res["greedy_vs_oracle"] = greedy_vs_golden(generated, steps, seqs, "bf16")
+    model.close()
+    # The same free-running greedy decode (untimed) on an f32 arena, the
+    # reference's KV dtype, against the reference-exact oracle's decode.
+    model = oh.HipTransformerModel(meta, num_blocks, bs, be, oh.F32)
+    model.init_synthetic(seed, 0.02)
+    out = model.forward(pf_batch, want_logits=False, want_argmax=True)
+    last = out.argmax.tolist()
+    ctx = [int(n) for n in lens]
+    generated = [last]
+    for _ in range(steps):
+        step()
+    res["greedy_vs_oracle_f32kv"] = greedy_vs_golden(generated, steps, seqs, "f32")
     model.close()
     be.close()
     if cpu:
@@ -272,28 +288,44 @@ def decode_e2e(steps=64, seqs=32, seed=20261204, cpu=True):
     return res
 
 
-def greedy_vs_golden(generated, steps, seqs):
+def greedy_vs_golden(generated, steps, seqs, kv):
     """The bench's free-running greedy tokens against the CPU oracle's greedy
     decode of the same batch with the same KV dtype
-    (tests/golden/cfg4_greedy_bf16kv.npz: K/V rounded to bf16 when written):
-    per sequence, the tokens that agree up to the first difference (after
-    one, the two sequences continue from different inputs)."""
-    path = os.path.join(ROOT, "tests", "golden", "cfg4_greedy_bf16kv.npz")
+    (tests/golden/cfg4_greedy_{kv}kv.npz; for bf16 the oracle rounds each K/V
+    element to bf16 when written): per sequence, the tokens that agree up to
+    the first difference (after one, the two sequences continue from
+    different inputs), and at each first difference the oracle's margin
+    between its own token and the device's (from the golden's 8 largest
+    logits; None when the device's token is not among them)."""
+    path = os.path.join(ROOT, "tests", "golden", f"cfg4_greedy_{kv}kv.npz")
     if not os.path.exists(path):
         return None
-    gold = np.load(path)["tokens"]
+    g = np.load(path)
+    gold = g["tokens"]
     got = np.asarray(generated, np.int64)
     if got.shape != gold.shape:
         return {"error": f"shape {got.shape} against golden {gold.shape}"}
     agree = got == gold
     prefix = [int(np.argmin(agree[:, s])) if not agree[:, s].all() else steps + 1
               for s in range(seqs)]
+    margins = []
+    for s, p in enumerate(prefix):
+        if p > steps:
+            continue
+        idx = list(g["top_idx"][p, s])
+        tok = int(got[p, s])
+        margins.append(float(g["top_val"][p, s, 0] - g["top_val"][p, s, idx.index(tok)])
+                       if tok in idx else None)
+    known = [m for m in margins if m is not None]
     return {"tokens_compared": int(gold.size), "tokens_matched": int(sum(prefix)),
             "sequences_identical": int(sum(p == steps + 1 for p in prefix)),
             "first_difference_steps": [p for p in prefix if p <= steps],
-            "note": "bf16 KV on both sides (the oracle rounds each K/V element to bf16 "
-                    "when written); matched = tokens up to each sequence's first "
-                    "difference"}
+            "oracle_margin_at_first_differences": [None if m is None else round(m, 6)
+                                                   for m in margins],
+            "smallest_margin": round(min(known), 6) if known else None,
+            "note": f"{kv} KV on both sides; matched = tokens up to each sequence's first "
+                    "difference; margin = oracle top-1 logit minus the oracle's logit of "
+                    "the device's token"}
 
 
 def gemm_shapes(reps=10):

@@ -345,9 +345,11 @@ int orion_hip_paged_attention_decode(orion_hip_device* dev, const orion_hip_kv_l
  * consecutive from d_first_pos[s]; row i attends 0..=d_first_pos[s] + i.  Same
  * result per row as orion_hip_paged_attention_decode.  `max_rows` bounds every
  * d_row_count (it sizes the grid), `max_position` every position.  bf16 KV
- * only (an f32 arena returns a Backend error).  hilo = 0 rounds Q and the
- * softmax weights to bf16 (the MFMA-rate path for bf16 inputs); hilo = 1
- * carries each as a hi + lo bf16 pair (~16-bit products, twice the MFMA work).
+ * only (an f32 arena returns a Backend error).  Operand precision `hilo`:
+ * 0 rounds Q and the softmax weights P to bf16 (the MFMA-rate path for bf16
+ * inputs); 1 carries each as a hi + lo bf16 pair (~16-bit products, twice the
+ * MFMA work); 2 carries Q as a pair and rounds P; 3 rounds Q and carries P as
+ * a pair.  Other values are an Internal error.
  * Table lengths and block ids are the caller's guarantee, as for decode. */
 int orion_hip_paged_attention_prefill(orion_hip_device* dev, const orion_hip_kv_layout* kv,
                                       const void* d_arena, int64_t layer, const float* d_q,
@@ -403,8 +405,11 @@ int orion_hip_gemm(orion_hip_device* dev, const float* d_x, const uint16_t* d_w,
  * shape whose required scratch exceeds 64 MiB is refused with
  * ORION_HIP_ERR_BACKEND.  The optional extra K splits of long-K calls (K >=
  * 8192 with fewer than 768 output tiles) are dropped when they do not fit,
- * so such a call can differ from orion_hip_gemm in f32 summation order.  Every call on one GPU shares that GPU's array:
- * calls that overlap on one GPU (other streams, other threads) race. */
+ * so such a call can differ from orion_hip_gemm in f32 summation order.  Every call on one GPU shares that GPU's array;
+ * the library orders the calls made through it on one GPU (any device
+ * handle, any thread): each call's stream waits for an event recorded after
+ * the previous call's launches.  Work that bypasses that order races on the
+ * array: a captured graph of such a call replayed while another call runs. */
 int orion_hip_gemm_noalloc(orion_hip_device* dev, const float* d_x, const uint16_t* d_w,
                            const float* d_bias, int64_t M, int64_t N, int64_t K, int epilogue,
                            float* d_out);

@@ -26,10 +26,12 @@
 // K/V tiles are double-buffered in LDS; the global loads of tile t+1 and the
 // block-table lookups of tile t+2 are in flight while tile t computes.
 //
-// Operand precision: with HILO = false Q and P are rounded to bf16 (RNE,
-// the MFMA-rate path for bf16 inputs); with HILO = true each is carried as a
-// hi + lo bf16 pair (two MFMAs), so products keep ~16 mantissa bits, matching
-// the decode kernels' precision.
+// Operand precision, per operand (OPS = kPrefillQHiLo | kPrefillPHiLo bits):
+// an operand without its bit is rounded to bf16 (RNE, the MFMA-rate path for
+// bf16 inputs); with it, it is carried as a hi + lo bf16 pair (two MFMAs), so
+// its products keep ~16 mantissa bits, matching the decode kernels'
+// precision.  Q's rounding moves every score (the softmax amplifies it); P's
+// only the weights' last bits.
 #include "common.hpp"
 #include "kernels.hpp"
 
@@ -92,7 +94,7 @@ __device__ inline int swz_v(int r) {
 
 // WAVES waves per workgroup (16 * kNR packed rows each); STAGES K/V tiles
 // resident in LDS, STAGES - 1 of them in flight.
-template <int D, bool HILO, bool BIG, int WAVES, int STAGES>
+template <int D, int OPS, bool BIG, int WAVES, int STAGES>
 __global__ void __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu(2)))
     paged_prefill_kernel(const uint16_t* __restrict__ kv_layer, uint32_t blk_stride,
                          uint32_t v_off, uint32_t slot_stride, uint32_t head_stride,
@@ -107,6 +109,7 @@ __global__ void __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu
                          float* __restrict__ out, PrefillSplitOut split) {
   constexpr int kWaves = WAVES;
   constexpr int kBM = kWaves * 16 * kNR;  // packed rows per workgroup
+  constexpr bool QHL = (OPS & kPrefillQHiLo) != 0, PHL = (OPS & kPrefillPHiLo) != 0;
   constexpr int kStages = STAGES;
   static_assert(kStages >= 2 && kStages <= 3, "LDS stages");
   constexpr int KCH = D / 32;           // S^T k-steps
@@ -162,7 +165,7 @@ __global__ void __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu
       const float4 x0 = *reinterpret_cast<const float4*>(qp + 32 * c);
       const float4 x1 = *reinterpret_cast<const float4*>(qp + 32 * c + 4);
       uint4 h, l;
-      if constexpr (HILO) {
+      if constexpr (QHL) {
         split2_trunc(x0.x, x0.y, h.x, l.x);
         split2_trunc(x0.z, x0.w, h.y, l.y);
         split2_trunc(x1.x, x1.y, h.z, l.z);
@@ -313,7 +316,7 @@ __global__ void __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu
         for (int rt = 0; rt < kNR; ++rt) {
           s[rt][kt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
               ka, qhi[rt][c], c == 0 ? f32x4{0.f, 0.f, 0.f, 0.f} : s[rt][kt], 0, 0, 0);
-          if constexpr (HILO)
+          if constexpr (QHL)
             s[rt][kt] =
                 __builtin_amdgcn_mfma_f32_16x16x32_bf16(ka, qlo[rt][c], s[rt][kt], 0, 0, 0);
         }
@@ -367,7 +370,7 @@ __global__ void __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu
               __builtin_amdgcn_exp2f(__builtin_fmaf(s[rt][2 * kp + 1][i], scale_log2, nm));
         }
         uint4 h, l;
-        if constexpr (HILO) {
+        if constexpr (PHL) {
           split2_trunc(pv[0], pv[1], h.x, l.x);
           split2_trunc(pv[2], pv[3], h.y, l.y);
           split2_trunc(pv[4], pv[5], h.z, l.z);
@@ -392,7 +395,7 @@ __global__ void __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu
 #pragma unroll
       for (int rt = 0; rt < kNR; ++rt) {
         lsum[rt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ones, phi[rt][kp], lsum[rt], 0, 0, 0);
-        if constexpr (HILO)
+        if constexpr (PHL)
           lsum[rt] =
               __builtin_amdgcn_mfma_f32_16x16x32_bf16(ones, plo[rt][kp], lsum[rt], 0, 0, 0);
       }
@@ -421,7 +424,7 @@ __global__ void __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu
 #pragma unroll
         for (int rt = 0; rt < kNR; ++rt) {
           o[rt][d] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(va, phi[rt][kp], o[rt][d], 0, 0, 0);
-          if constexpr (HILO)
+          if constexpr (PHL)
             o[rt][d] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(va, plo[rt][kp], o[rt][d], 0, 0, 0);
         }
       }
@@ -478,7 +481,7 @@ hipError_t launch_paged_prefill(hipStream_t st, const KvGeom& kv, const void* ar
                                 const PrefillTile* order, int64_t num_tiles,
                                 const int32_t* row_start, const int32_t* row_count,
                                 const uint32_t* first_pos, const int64_t* bt_offsets,
-                                const uint32_t* bt_ids, bool hilo, float* out,
+                                const uint32_t* bt_ids, int operands, float* out,
                                 const PrefillSplitOut& split) {
   if (num_tiles == 0) return hipSuccess;
   if (!kv.dtype_bf16) return hipErrorNotSupported;
@@ -518,11 +521,19 @@ hipError_t launch_paged_prefill(hipStream_t st, const KvGeom& kv, const void* ar
       ORION_PREFILL_B(DD, HH, false);\
   } while (0)
   const bool big = kv.block_size >= 16;
-  if (D == 128) {
-    if (hilo) ORION_PREFILL(128, true); else ORION_PREFILL(128, false);
-  } else {
-    if (hilo) ORION_PREFILL(64, true); else ORION_PREFILL(64, false);
-  }
+  const int ops = operands & (kPrefillQHiLo | kPrefillPHiLo);
+#define ORION_PREFILL_D(DD)                                          \
+  do {                                                               \
+    if (ops == (kPrefillQHiLo | kPrefillPHiLo)) ORION_PREFILL(DD, 3); \
+    else if (ops == kPrefillQHiLo) ORION_PREFILL(DD, 1);              \
+    else if (ops == kPrefillPHiLo) ORION_PREFILL(DD, 2);              \
+    else ORION_PREFILL(DD, 0);                                        \
+  } while (0)
+  if (D == 128)
+    ORION_PREFILL_D(128);
+  else
+    ORION_PREFILL_D(64);
+#undef ORION_PREFILL_D
 #undef ORION_PREFILL
 #undef ORION_PREFILL_B
 #undef ORION_PREFILL_W

@@ -122,6 +122,10 @@ struct PrefillPlan {
 int prefill_tile_rows();  // packed rows per prefill workgroup
 int prefill_waves();      // waves per prefill workgroup (8, or 4 with ORION_PREFILL_WAVES=4)
 constexpr int kPrefillWaveRowTiles = 2;  // 16-row MFMA tiles per prefill wave
+// Prefill operand precision bits (launch_paged_prefill `operands`): each set
+// bit carries that operand as a hi + lo bf16 pair, each clear one rounds it
+// to bf16.
+constexpr int kPrefillQHiLo = 1, kPrefillPHiLo = 2;
 // cus: compute units (one prefill workgroup each); hkv: KV heads (workgroups
 // per work-list entry); cus = 0 never splits.
 void build_prefill_order(const int32_t* row_start, const int32_t* row_count,
@@ -139,7 +143,7 @@ hipError_t launch_paged_prefill(hipStream_t st, const KvGeom& kv, const void* ar
                                 const PrefillTile* order, int64_t num_tiles,
                                 const int32_t* row_start, const int32_t* row_count,
                                 const uint32_t* first_pos, const int64_t* bt_off,
-                                const uint32_t* bt_ids, bool hilo, float* out,
+                                const uint32_t* bt_ids, int operands, float* out,
                                 const PrefillSplitOut& split = PrefillSplitOut{});
 // Packed (row, query head) rows per prefill workgroup tile.
 

@@ -318,6 +318,12 @@ static __device__ __align__(256) char scratch[kNoAllocScratchBytes];
 
 static std::mutex g_noalloc_mu;
 static void* g_noalloc_scratch[256] = {};
+// Per GPU: an event recorded after the last orion_hip_gemm_noalloc launch on
+// that GPU (from any device handle, each with its own stream).  The next call
+// makes its stream wait for it, so calls through different handles of one GPU
+// run one after another on the shared array instead of racing on it.
+static hipEvent_t g_noalloc_done[256] = {};
+static bool g_noalloc_recorded[256] = {};
 
 // Resolves this device's address of `scratch` (the device must be current).
 static hipError_t resolve_noalloc_scratch(int ordinal, void** out) {
@@ -329,6 +335,8 @@ static hipError_t resolve_noalloc_scratch(int ordinal, void** out) {
     if (e != hipSuccess) return e;
     if (!p) return hipErrorInvalidSymbol;
     g_noalloc_scratch[ordinal] = p;
+    e = hipEventCreateWithFlags(&g_noalloc_done[ordinal], hipEventDisableTiming);
+    if (e != hipSuccess) return e;
   }
   *out = g_noalloc_scratch[ordinal];
   return hipSuccess;
@@ -1408,6 +1416,14 @@ ORION_EXPORT int orion_hip_model_forward(orion_hip_model* m, const orion_hip_bat
   std::vector<int32_t> pf_start, pf_count;
   std::vector<uint32_t> pf_pos;
   std::vector<int64_t> pf_btoff;
+  // Prefill attention operands: Q and P as hi + lo bf16 pairs (default);
+  // ORION_PREFILL_OPERANDS=bf16 rounds both to bf16, =q keeps only Q as a
+  // pair, =p only P (measurement knob, read per call).
+  const char* pf_env = getenv("ORION_PREFILL_OPERANDS");
+  int pf_ops = kPrefillQHiLo | kPrefillPHiLo;
+  if (pf_env && std::strcmp(pf_env, "bf16") == 0) pf_ops = 0;
+  if (pf_env && std::strcmp(pf_env, "q") == 0) pf_ops = kPrefillQHiLo;
+  if (pf_env && std::strcmp(pf_env, "p") == 0) pf_ops = kPrefillPHiLo;
   // ORION_PREFILL_ROUTE=0 sends every row to the decode kernel (read per
   // call; lets tests compare the two routes on one batch).
   const char* route = getenv("ORION_PREFILL_ROUTE");
@@ -1586,7 +1602,7 @@ ORION_EXPORT int orion_hip_model_forward(orion_hip_model* m, const orion_hip_bat
     if (npf) {
       HIP_TRY(st, launch_paged_prefill(stream, m->kv, m->arena, l, qrot, Hq, d_pforder,
                                        (int64_t)pf_order.size(), d_pfstart, d_pfcount, d_pfpos,
-                                       d_pfoff, d_btids, /*hilo=*/true, attn, pf_out));
+                                       d_pfoff, d_btids, pf_ops, attn, pf_out));
       if (pf_split)
         HIP_TRY(st, launch_split_merge(stream, d.head_dim, n, Hq, pf_merge, attn));
     }
@@ -1756,6 +1772,9 @@ ORION_EXPORT int orion_hip_paged_attention_prefill(
     const uint32_t* d_bt_ids, int64_t max_rows, int64_t max_position, int32_t hilo,
     float* d_out) {
   const char* st = "paged_attention_prefill";
+  if (hilo < 0 || hilo > 3) return internal(st, "operand mode %d is not 0..3", (int)hilo);
+  // 0: bf16 Q and P; 1: hi/lo both; 2: hi/lo Q, bf16 P; 3: bf16 Q, hi/lo P
+  static const int kOps[4] = {0, kPrefillQHiLo | kPrefillPHiLo, kPrefillQHiLo, kPrefillPHiLo};
   KvGeom g;
   if (int rc = kv_geom_from(kv, &g, st)) return rc;
   if (g.num_kv_heads <= 0 || num_q_heads % g.num_kv_heads)
@@ -1825,7 +1844,7 @@ ORION_EXPORT int orion_hip_paged_attention_prefill(
             hipError_t e = launch_paged_prefill(dev->stream, g, d_arena, layer, d_q, num_q_heads,
                                                 dev->prefill_order.as<const PrefillTile>(),
                                                 (int64_t)order.size(), d_row_start, d_row_count,
-                                                d_first_pos, d_bt_offsets, d_bt_ids, hilo != 0,
+                                                d_first_pos, d_bt_offsets, d_bt_ids, kOps[hilo],
                                                 d_out, out_parts);
             if (e == hipSuccess && split)
               e = launch_split_merge(dev->stream, g.head_dim, rows, num_q_heads, merge, d_out);
@@ -1911,7 +1930,14 @@ ORION_EXPORT int orion_hip_gemm_noalloc(orion_hip_device* dev, const float* d_x,
   GemmScratch sc;
   sc.ws = static_cast<float*>(dev->noalloc_scratch);
   sc.ws_bytes = kNoAllocScratchBytes;
+  // Order against the previous call on this GPU (any handle, any host
+  // thread): wait for its event, launch, record ours, all under the lock.
+  std::lock_guard<std::mutex> lk(g_noalloc_mu);
+  const int o = dev->ordinal;
+  if (g_noalloc_recorded[o]) HIP_TRY(st, hipStreamWaitEvent(dev->stream, g_noalloc_done[o], 0));
   HIP_TRY(st, launch_gemm(dev->stream, d_x, d_w, d_bias, M, N, K, ep, d_out, &sc, nullptr));
+  HIP_TRY(st, hipEventRecord(g_noalloc_done[o], dev->stream));
+  g_noalloc_recorded[o] = true;
   return ORION_HIP_OK;
 }
 

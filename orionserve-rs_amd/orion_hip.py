@@ -756,11 +756,14 @@ def paged_attention_prefill(be: HipBackend, kv: KvLayout, arena_ptr: int, layer:
                             num_q_heads: int, num_seqs: int, row_start_ptr: int,
                             row_count_ptr: int, first_pos_ptr: int, bt_off_ptr: int,
                             bt_ids_ptr: int, max_rows: int, max_position: int,
-                            out_ptr: int, hilo: bool = False) -> None:
+                            out_ptr: int, hilo=False) -> None:
+    """hilo: False / True (bf16 / hi+lo Q and P), or the C mode 0..3
+    (2: hi/lo Q only, 3: hi/lo P only)."""
+    mode = int(hilo) if not isinstance(hilo, bool) else (1 if hilo else 0)
     _check(be.lib.orion_hip_paged_attention_prefill(
         be.handle, C.byref(kv), arena_ptr, layer, q_ptr, num_q_heads, num_seqs, row_start_ptr,
         row_count_ptr, first_pos_ptr, bt_off_ptr, bt_ids_ptr, max_rows, max_position,
-        1 if hilo else 0, out_ptr))
+        mode, out_ptr))
 
 
 def rope_and_cache(be: HipBackend, kv: KvLayout, arena_ptr: int, layer: int, num_rows: int,

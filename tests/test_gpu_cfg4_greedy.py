@@ -21,10 +21,11 @@ runtime/src/sampling.rs:196-207 argmax, lowest index on ties):
   * the device argmax equals the oracle's token, except at near-ties: the
     device's token is then among the oracle's 8 best, and the oracle's margin
     between the two tokens is within twice that sequence's measured logit
-    error.  Measured on the MI355X: 2 such tokens of 2,080 with f32 KV (logit
-    error 6.7e-5 of max |logit|), 6 with bf16 KV (1.0e-3: a K/V element
-    whose f32 value differs in its last bits between the two sides can round
-    to the neighbouring bf16 value).  The caps are 4 and 12.
+    error.  Measured on the MI355X: 2 or 3 such tokens of 2,080 with f32 KV
+    (two runs; logit error 6.7e-5 and 7.6e-5 of max |logit|), 6 with bf16 KV
+    (two runs; 1.0e-3: a K/V element whose f32 value differs in its last bits
+    between the two sides can round to the neighbouring bf16 value).  The
+    caps are the largest measured count + 1: 4 (f32) and 7 (bf16).
 """
 import os
 
@@ -39,7 +40,7 @@ pytestmark = pytest.mark.gpu
 GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
 
 
-@pytest.mark.parametrize("kv,bound,cap", [("bf16", 2e-3, 12), ("f32", 1e-4, 4)])
+@pytest.mark.parametrize("kv,bound,cap", [("bf16", 2e-3, 7), ("f32", 1e-4, 4)])
 def test_cfg4_bench_batch_greedy_tokens_match_oracle(backend, kv, bound, cap):
     g = np.load(os.path.join(GOLDEN, f"cfg4_greedy_{kv}kv.npz"))
     case = cfg4_case()
@@ -62,6 +63,7 @@ def test_cfg4_bench_batch_greedy_tokens_match_oracle(backend, kv, bound, cap):
     ctx = list(case.lens)
     compared = mismatches = 0
     worst = 0.0
+    margins = []
     for step in range(steps + 1):
         lg, am = out.logits, out.argmax
         top_idx, top_val = g["top_idx"][step], g["top_val"][step]
@@ -77,6 +79,7 @@ def test_cfg4_bench_batch_greedy_tokens_match_oracle(backend, kv, bound, cap):
                 assert k > 0, (step, s, int(am[s]))
                 gap = float(top_val[s, 0] - top_val[s, k])
                 assert gap <= 2 * float(err_s[s]), (step, s, gap, float(err_s[s]))
+                margins.append(gap)
                 mismatches += 1
         if step == steps:
             break
@@ -86,6 +89,7 @@ def test_cfg4_bench_batch_greedy_tokens_match_oracle(backend, kv, bound, cap):
                         want_argmax=True)
         ctx = [c + 1 for c in ctx]
     print(f"[cfg4 greedy] {compared} tokens compared, {mismatches} near-tie mismatches, "
-          f"worst logit error {worst:.2e} of max |logit|", flush=True)
+          f"worst logit error {worst:.2e} of max |logit|, oracle margins at the mismatches "
+          f"{sorted(round(x, 6) for x in margins)}", flush=True)
     assert mismatches <= cap
     m.close()

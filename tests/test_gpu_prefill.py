@@ -172,3 +172,19 @@ def test_uncovered_prefill_shapes_are_backend_errors(backend, hq, hkv, d):
     case = PrefillCase(4, [20], [8], hq, hkv, d, 16)
     with pytest.raises(oh.BackendError):
         run_prefill(backend, case, False)
+
+
+@pytest.mark.parametrize("mode", [2, 3])
+@pytest.mark.parametrize("hq,hkv,d", [(32, 8, 128), (32, 4, 64), (28, 4, 128)])
+def test_single_operand_hilo_modes(backend, mode, hq, hkv, d):
+    # Mode 2 carries Q as a hi/lo pair and rounds the softmax weights P to
+    # bf16; mode 3 the reverse.  Each sits between the bf16 and the hi/lo
+    # modes: within the north-star 1e-2 of the oracle, and its error is
+    # printed beside the two full modes' for the record.
+    case = PrefillCase(500 + mode + d, [0, 37, 700, 3000], [64, 200, 129, 300], hq, hkv, d, 16)
+    want = case.oracle()
+    errs = {m: float(np.abs(run_prefill(backend, case, m) - want).max()) for m in (0, mode, 1)}
+    print(f"[prefill operands] hq={hq} hkv={hkv} d={d} max abs err bf16 {errs[0]:.2e} "
+          f"mode{mode} {errs[mode]:.2e} hilo {errs[1]:.2e}", flush=True)
+    assert errs[mode] <= 1e-2
+    assert errs[1] <= 1e-4

@@ -80,3 +80,45 @@ def test_noalloc_gemm_refuses_shapes_beyond_its_scratch(backend):
         oh._check(backend.lib.orion_hip_gemm_noalloc(backend.handle, C.c_void_p(16),
                                                      C.c_void_p(16), None, 64, 200000, 4096,
                                                      oh.GEMM_STORE, C.c_void_p(16)))
+
+
+def test_noalloc_gemm_ordered_across_device_handles(backend):
+    # Two handles on GPU 0 each have their own stream, and both use the GPU's
+    # one scratch array.  Calls alternate between the handles with no host
+    # synchronisation between them; each must still be bit-identical to
+    # orion_hip_gemm (the library orders them with a per-GPU event).
+    be2 = oh.HipBackend(backend.ordinal)
+    cases = []
+    try:
+        shapes = [(32, 32000, 2048, oh.GEMM_STORE), (48, 11264, 2048, oh.GEMM_SWIGLU),
+                  (64, 2048, 5632, oh.GEMM_STORE), (8, 2560, 2048, oh.GEMM_STORE)]
+        rng = np.random.default_rng(77)
+        for (M, N, K, ep) in shapes:
+            x = rng.standard_normal((M, K), dtype=np.float32)
+            w = bf16_round(rng.standard_normal((N, K), dtype=np.float32) * 0.05)
+            n_out = N // 2 if ep == oh.GEMM_SWIGLU else N
+            dx, dw = backend.to_device(x), backend.to_device(oh.f32_to_bf16_bits(w))
+            ref = backend.alloc(M * n_out * 4)
+            oh._check(backend.lib.orion_hip_gemm(backend.handle, dx.ptr, dw.ptr, None, M, N, K,
+                                                 ep, ref.ptr))
+            outs = [backend.alloc(M * n_out * 4) for _ in range(2)]
+            cases.append((M, N, K, ep, n_out, dx, dw, ref, outs))
+        backend.synchronize()
+        print("[gemm_noalloc] two handles, alternating calls", flush=True)
+        for rnd in range(2):
+            for i, (M, N, K, ep, n_out, dx, dw, ref, outs) in enumerate(cases):
+                be = backend if (i + rnd) % 2 == 0 else be2
+                oh._check(be.lib.orion_hip_gemm_noalloc(be.handle, dx.ptr, dw.ptr, None, M, N, K,
+                                                        ep, outs[rnd].ptr))
+        backend.synchronize()
+        be2.synchronize()
+        for (M, N, K, ep, n_out, dx, dw, ref, outs) in cases:
+            want = ref.download(np.float32, (M, n_out))
+            for o in outs:
+                got = o.download(np.float32, (M, n_out))
+                assert np.array_equal(want.view(np.uint32), got.view(np.uint32)), (M, N, K, ep)
+    finally:
+        be2.close()
+        for (M, N, K, ep, n_out, dx, dw, ref, outs) in cases:
+            for b in (dx, dw, ref, *outs):
+                b.free()
