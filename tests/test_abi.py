@@ -109,3 +109,19 @@ def test_bench_measures_one_gpu_only():
                        capture_output=True, text=True, timeout=120)
     assert p.returncode == 2
     assert "one GPU" in p.stderr
+
+
+def test_serve_backend_patch_applies_to_the_reference():
+    # crates/orion-hip/serve-backend.patch (the `orion serve --backend hip`
+    # selection) must apply cleanly to the reference sources it targets; run
+    # only where the reference tree is present (a dry run, nothing written).
+    import shutil
+    import subprocess
+    ref = "/root/reference"
+    patch = os.path.join(ROOT, "crates", "orion-hip", "serve-backend.patch")
+    if not os.path.isdir(ref) or not shutil.which("patch"):
+        pytest.skip("reference tree or patch(1) not present")
+    p = subprocess.run(["patch", "-p1", "--dry-run", "-d", ref, "-i", patch],
+                       capture_output=True, text=True)
+    assert p.returncode == 0, p.stdout + p.stderr
+    assert "FAILED" not in p.stdout
