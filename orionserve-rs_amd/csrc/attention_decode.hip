@@ -622,13 +622,14 @@ __global__ void __launch_bounds__(256)
 
 // paged_attention (attention.rs:219-295) accepts any even head_dim and any
 // grouping of query heads over KV heads.  This wave covers what the MFMA and
-// per-dtype VALU waves do not: head_dim even and at most 256, any group size.
-// One wave per work item (row, KV head, chunk).  Lane l holds dimensions
-// {2l, 2l+1} and {128+2l, 128+2l+1} of every vector; a 16-token step loads
-// the 16 keys, reduces each score over the wave, and updates the online
-// softmax (max, sum, output) of one query head.  The G query heads of the
-// item run one after another over the same chunk, so heads after the first
-// re-read its K/V from the caches.  Partial results use the same split
+// per-dtype VALU waves do not: any even head_dim up to kMaxHeadDim, any group
+// size.  One wave per work item (row, KV head, chunk).  Lane l holds
+// dimensions {128c + 2l, 128c + 2l + 1} of every vector, for c < NC (NC
+// 128-dimension chunks, the smallest template width covering D); a 16-token
+// step loads the 16 keys, reduces each score over the wave, and updates the
+// online softmax (max, sum, output) of one query head.  The G query heads of
+// the item run one after another over the same chunk, so heads after the
+// first re-read its K/V from the caches.  Partial results use the same split
 // layout as the other waves.
 template <typename T>
 __device__ inline float2 load_pair(const T* p, bool valid);
@@ -642,7 +643,7 @@ __device__ inline float2 load_pair<uint16_t>(const uint16_t* p, bool valid) {
   return make_float2(bf16lo(v), bf16hi(v));
 }
 
-template <typename T>
+template <typename T, int NC>
 __global__ void __launch_bounds__(256)
     paged_decode_any_kernel(const T* __restrict__ kv_layer, int64_t blk_stride, int64_t v_off,
                             int64_t slot_stride, int64_t head_stride, int bs_log2,
@@ -657,8 +658,9 @@ __global__ void __launch_bounds__(256)
   const int row = wk.item / num_kv_heads, kvh = wk.item - row * num_kv_heads;
   const int G = num_q_heads / num_kv_heads;
   const int lane = threadIdx.x & 63;
-  const int d0 = 2 * lane, d1 = 128 + 2 * lane;
-  const bool has0 = d0 < D, has1 = d1 < D;
+  bool has[NC];
+#pragma unroll
+  for (int c = 0; c < NC; ++c) has[c] = 128 * c + 2 * lane < D;
   const int start = wk.start, end = wk.end;
   const int split = wk.split;
   const int bs_mask = (1 << bs_log2) - 1;
@@ -666,14 +668,18 @@ __global__ void __launch_bounds__(256)
   const int nblk = ((end - 1) >> bs_log2) - first_blk + 1;
   const uint32_t* tbl = bt_ids + wk.tbl_off;
   const int my_blk = lane < nblk ? (int)tbl[lane] : 0;
-  const T* kbase = kv_layer + (int64_t)kvh * head_stride;
+  const T* kbase = kv_layer + (int64_t)kvh * head_stride + 2 * lane;
   for (int g = 0; g < G; ++g) {
     const int64_t head = (int64_t)row * num_q_heads + (int64_t)kvh * G + g;
-    const float* qp = q + head * D;
-    const float2 q0 = has0 ? *reinterpret_cast<const float2*>(qp + d0) : make_float2(0.f, 0.f);
-    const float2 q1 = has1 ? *reinterpret_cast<const float2*>(qp + d1) : make_float2(0.f, 0.f);
+    const float* qp = q + head * D + 2 * lane;
+    float2 qv[NC];
+#pragma unroll
+    for (int c = 0; c < NC; ++c)
+      qv[c] = has[c] ? *reinterpret_cast<const float2*>(qp + 128 * c) : make_float2(0.f, 0.f);
     float m = -INFINITY, l = 0.f;
-    float o[4] = {0.f, 0.f, 0.f, 0.f};
+    float o[2 * NC];
+#pragma unroll
+    for (int e = 0; e < 2 * NC; ++e) o[e] = 0.f;
     for (int base = start; base < end; base += 16) {
       float s[16];
       int64_t off[16];
@@ -683,9 +689,12 @@ __global__ void __launch_bounds__(256)
         const bool valid = j < end;
         const int blk = __shfl(my_blk, valid ? (j >> bs_log2) - first_blk : 0);
         off[r] = (int64_t)blk * blk_stride + (int64_t)(j & bs_mask) * slot_stride;
-        const float2 k0 = load_pair<T>(kbase + off[r] + d0, valid && has0);
-        const float2 k1 = load_pair<T>(kbase + off[r] + d1, valid && has1);
-        const float part = q0.x * k0.x + q0.y * k0.y + q1.x * k1.x + q1.y * k1.y;
+        float part = 0.f;
+#pragma unroll
+        for (int c = 0; c < NC; ++c) {
+          const float2 kk = load_pair<T>(kbase + off[r] + 128 * c, valid && has[c]);
+          part += qv[c].x * kk.x + qv[c].y * kk.y;
+        }
         const float dot = wave_sum(part);
         s[r] = valid ? dot * scale : -INFINITY;
       }
@@ -695,41 +704,45 @@ __global__ void __launch_bounds__(256)
       const float m_new = fmaxf(m, mx);
       const float alpha = __expf(m - m_new);
       float psum = 0.f;
-      float acc[4] = {o[0] * alpha, o[1] * alpha, o[2] * alpha, o[3] * alpha};
+#pragma unroll
+      for (int e = 0; e < 2 * NC; ++e) o[e] *= alpha;
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
         const bool valid = base + r < end;
         const float p = valid ? __expf(s[r] - m_new) : 0.f;
         psum += p;
-        const float2 v0 = load_pair<T>(kbase + off[r] + v_off + d0, valid && has0);
-        const float2 v1 = load_pair<T>(kbase + off[r] + v_off + d1, valid && has1);
-        acc[0] += p * v0.x;
-        acc[1] += p * v0.y;
-        acc[2] += p * v1.x;
-        acc[3] += p * v1.y;
+#pragma unroll
+        for (int c = 0; c < NC; ++c) {
+          const float2 vv = load_pair<T>(kbase + off[r] + v_off + 128 * c, valid && has[c]);
+          o[2 * c] += p * vv.x;
+          o[2 * c + 1] += p * vv.y;
+        }
       }
       l = l * alpha + psum;
       m = m_new;
-#pragma unroll
-      for (int e = 0; e < 4; ++e) o[e] = acc[e];
     }
     if (wk.nsplit == 1) {
       const float inv = 1.f / l;
-      float* op = out + head * D;
-      if (has0) *reinterpret_cast<float2*>(op + d0) = make_float2(o[0] * inv, o[1] * inv);
-      if (has1) *reinterpret_cast<float2*>(op + d1) = make_float2(o[2] * inv, o[3] * inv);
+      float* op = out + head * D + 2 * lane;
+#pragma unroll
+      for (int c = 0; c < NC; ++c)
+        if (has[c])
+          *reinterpret_cast<float2*>(op + 128 * c) = make_float2(o[2 * c] * inv, o[2 * c + 1] * inv);
     } else {
       const int64_t slot = head * max_splits + split;
-      float* op = ws_o + slot * D;
-      if (has0) *reinterpret_cast<float2*>(op + d0) = make_float2(o[0], o[1]);
-      if (has1) *reinterpret_cast<float2*>(op + d1) = make_float2(o[2], o[3]);
+      float* op = ws_o + slot * D + 2 * lane;
+#pragma unroll
+      for (int c = 0; c < NC; ++c)
+        if (has[c]) *reinterpret_cast<float2*>(op + 128 * c) = make_float2(o[2 * c], o[2 * c + 1]);
       if (lane == 0) *reinterpret_cast<float2*>(ws_ml + slot * 2) = make_float2(m, l);
     }
   }
 }
 
-// Merges the split partials for any head_dim (even, <= 256): one wave per
-// (row, query head), splits in order, lane l holding dimensions l + 64 i.
+// Merges the split partials for any even head_dim up to kMaxHeadDim: one wave
+// per (row, query head), splits in order, lane l holding dimensions l + 64 i
+// for i < NI.
+template <int NI>
 __global__ void __launch_bounds__(256)
     paged_decode_combine_any_kernel(int num_rows, int num_q_heads, int D,
                                     const int32_t* __restrict__ row_nsplit,
@@ -752,15 +765,17 @@ __global__ void __launch_bounds__(256)
   float ls = 0.f;
   for (int s = lane; s < nsplit; s += 64) ls += __expf(ml[2 * s] - mx) * ml[2 * s + 1];
   const float inv = 1.f / wave_sum(ls);
-  float acc[4] = {0.f, 0.f, 0.f, 0.f};
+  float acc[NI];
+#pragma unroll
+  for (int i = 0; i < NI; ++i) acc[i] = 0.f;
   for (int s = 0; s < nsplit; ++s) {
     const float wj = __expf(ml[2 * s] - mx);
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
+    for (int i = 0; i < NI; ++i)
       if (lane + 64 * i < D) acc[i] += wj * ob[(int64_t)s * D + lane + 64 * i];
   }
 #pragma unroll
-  for (int i = 0; i < 4; ++i)
+  for (int i = 0; i < NI; ++i)
     if (lane + 64 * i < D) out[item * D + lane + 64 * i] = acc[i] * inv;
 }
 
@@ -834,10 +849,21 @@ static hipError_t launch_combine(hipStream_t st, int64_t D, int64_t rows, int64_
   const int64_t nr = plan.rows ? plan.num_rows : rows;
   if (nr == 0) return hipSuccess;
   dim3 cgrid((unsigned)((nr * hq + 3) / 4));
-  if (D != 64 && D != 128)
-    hipLaunchKernelGGL(paged_decode_combine_any_kernel, cgrid, dim3(256), 0, st, (int)nr,
-                       (int)hq, (int)D, plan.row_nsplit, plan.rows, ms, ws_o, ws_ml, out);
-  else if (D == 128)
+  if (D != 64 && D != 128) {
+    if (D > kMaxHeadDim) return hipErrorInvalidValue;
+#define ORION_COMBINE_ANY(NI)                                                                  \
+  hipLaunchKernelGGL(paged_decode_combine_any_kernel<NI>, cgrid, dim3(256), 0, st, (int)nr,  \
+                     (int)hq, (int)D, plan.row_nsplit, plan.rows, ms, ws_o, ws_ml, out)
+    if (D <= 256)
+      ORION_COMBINE_ANY(4);
+    else if (D <= 512)
+      ORION_COMBINE_ANY(8);
+    else if (D <= 1024)
+      ORION_COMBINE_ANY(16);
+    else
+      ORION_COMBINE_ANY(32);
+#undef ORION_COMBINE_ANY
+  } else if (D == 128)
     hipLaunchKernelGGL(paged_decode_combine_kernel<128>, cgrid, dim3(256), 0, st, (int)nr,
                        (int)hq, plan.row_nsplit, plan.rows, ms, ws_o, ws_ml, out);
   else
@@ -882,17 +908,29 @@ hipError_t launch_paged_decode(hipStream_t st, const KvGeom& kv, const void* are
   const dim3 grid((unsigned)((plan.num_work + 3) / 4));
   hipError_t e;
   if ((D != 64 && D != 128) || G > 8) {
-    if (D > 256 || (D & 1)) return hipErrorInvalidValue;
+    if (D > kMaxHeadDim || (D & 1)) return hipErrorInvalidValue;
+#define ORION_ANY(TT, NC)                                                                      \
+  hipLaunchKernelGGL((paged_decode_any_kernel<TT, NC>), grid, dim3(256), 0, st,                \
+                     static_cast<const TT*>(arena) + layer * a.layer, a.blk, a.v_off, a.slot,  \
+                     a.head, bs_log2, (int)hkv, (int)hq, (int)D, plan.work, plan.num_work, q,  \
+                     bt_ids, ms, scale, out, ws_o, ws_ml)
+#define ORION_ANY_D(TT)            \
+  do {                             \
+    if (D <= 256)                  \
+      ORION_ANY(TT, 2);            \
+    else if (D <= 512)             \
+      ORION_ANY(TT, 4);            \
+    else if (D <= 1024)            \
+      ORION_ANY(TT, 8);            \
+    else                           \
+      ORION_ANY(TT, 16);           \
+  } while (0)
     if (kv.dtype_bf16)
-      hipLaunchKernelGGL(paged_decode_any_kernel<uint16_t>, grid, dim3(256), 0, st,
-                         static_cast<const uint16_t*>(arena) + layer * a.layer, a.blk, a.v_off,
-                         a.slot, a.head, bs_log2, (int)hkv, (int)hq, (int)D, plan.work,
-                         plan.num_work, q, bt_ids, ms, scale, out, ws_o, ws_ml);
+      ORION_ANY_D(uint16_t);
     else
-      hipLaunchKernelGGL(paged_decode_any_kernel<float>, grid, dim3(256), 0, st,
-                         static_cast<const float*>(arena) + layer * a.layer, a.blk, a.v_off,
-                         a.slot, a.head, bs_log2, (int)hkv, (int)hq, (int)D, plan.work,
-                         plan.num_work, q, bt_ids, ms, scale, out, ws_o, ws_ml);
+      ORION_ANY_D(float);
+#undef ORION_ANY_D
+#undef ORION_ANY
     e = hipGetLastError();
   } else if (kv.dtype_bf16) {
     // in-block strides travel as 32-bit values; block offsets are 64-bit

@@ -130,8 +130,9 @@ __device__ inline void store_kv<uint16_t>(uint16_t* p, float v) { *p = f32_to_bf
 
 // One workgroup per (row, head): heads [0, hq) are Q, [hq, hq + hkv) K and
 // the rest V, which are also the column ranges of the fused QKV output, so
-// head u covers columns [u * D, (u + 1) * D).  Thread i holds element i and
-// takes its rotate-half partner (i +- D/2) from LDS.
+// head u covers columns [u * D, (u + 1) * D).  Thread i holds elements i,
+// i + blockDim, ... and takes each one's rotate-half partner (e +- D/2) from
+// LDS (D floats of dynamic shared memory).
 template <typename T>
 __global__ void __launch_bounds__(256)
     rope_cache_kernel(T* __restrict__ kv_layer, int64_t blk_stride, int64_t v_off,
@@ -144,10 +145,9 @@ __global__ void __launch_bounds__(256)
                       const uint32_t* __restrict__ bt_ids, const float* __restrict__ cos_t,
                       const float* __restrict__ sin_t, GemmPartials qkv) {
 #pragma clang fp contract(off)
-  __shared__ float xs[256];
+  extern __shared__ float xs[];
   const int64_t row = blockIdx.x;
   const int unit = blockIdx.y;
-  const int i = threadIdx.x;
   const bool is_q = unit < hq, is_k = !is_q && unit < hq + hkv;
   const int h = is_q ? unit : is_k ? unit - hq : unit - hq - hkv;
   const uint32_t pos = positions[row];
@@ -158,31 +158,30 @@ __global__ void __launch_bounds__(256)
 
   // Inputs come from the q/k/v buffers, or straight from the QKV GEMM's
   // unreduced partials.
-  float x = 0.f;
-  if (i < D) {
-    if (qkv.ws)
-      x = partial_sum(qkv, row, (int64_t)unit * D + i);
-    else
-      x = is_q ? q_in[row * q_stride + h * D + i]
-          : is_k ? k[row * k_stride + h * D + i]
-                 : v[row * v_stride + h * D + i];
-  }
+  auto input = [&](int e) {
+    if (qkv.ws) return partial_sum(qkv, row, (int64_t)unit * D + e);
+    return is_q ? q_in[row * q_stride + h * D + e]
+         : is_k ? k[row * k_stride + h * D + e]
+                : v[row * v_stride + h * D + e];
+  };
   if (!is_q && !is_k) {  // uniform over the workgroup
-    if (i < D) store_kv<T>(kdst + v_off + i, x);
+    for (int e = threadIdx.x; e < D; e += blockDim.x) store_kv<T>(kdst + v_off + e, input(e));
     return;
   }
-  xs[i] = x;
+  for (int e = threadIdx.x; e < D; e += blockDim.x) xs[e] = input(e);
   __syncthreads();
-  if (i >= D) return;
   const int half = D >> 1;
-  const int j = i < half ? i : i - half;
-  const float c = cos_t[(int64_t)pos * half + j], sn = sin_t[(int64_t)pos * half + j];
-  // out[j] = x0 cos - x1 sin, out[j + half] = x0 sin + x1 cos (x0 = x[j], x1 = x[j + half])
-  const float y = i < half ? x * c - xs[i + half] * sn : xs[j] * sn + x * c;
-  if (is_q)
-    q_out[row * (int64_t)hq * D + h * D + i] = y;
-  else
-    store_kv<T>(kdst + i, y);
+  for (int i = threadIdx.x; i < D; i += blockDim.x) {
+    const float x = xs[i];
+    const int j = i < half ? i : i - half;
+    const float c = cos_t[(int64_t)pos * half + j], sn = sin_t[(int64_t)pos * half + j];
+    // out[j] = x0 cos - x1 sin, out[j + half] = x0 sin + x1 cos (x0 = x[j], x1 = x[j + half])
+    const float y = i < half ? x * c - xs[i + half] * sn : xs[j] * sn + x * c;
+    if (is_q)
+      q_out[row * (int64_t)hq * D + h * D + i] = y;
+    else
+      store_kv<T>(kdst + i, y);
+  }
 }
 
 // The same RoPE + KV write for inputs in the q/k/v buffers (the prefill
@@ -269,7 +268,7 @@ hipError_t launch_rope_and_cache(hipStream_t st, const KvGeom& kv, void* arena, 
   int bs_log2 = 0;
   while ((1 << bs_log2) < kv.block_size) ++bs_log2;
   const ArenaStrides a = arena_strides(kv);
-  if (kv.head_dim > 256 || kv.head_dim % 2 || hq + 2 * kv.num_kv_heads > 65535 ||
+  if (kv.head_dim > kMaxHeadDim || kv.head_dim % 2 || hq + 2 * kv.num_kv_heads > 65535 ||
       rows > INT32_MAX)
     return hipErrorInvalidValue;
   // Inputs in the q/k/v buffers with 16-byte aligned rows: the vectorised
@@ -297,16 +296,17 @@ hipError_t launch_rope_and_cache(hipStream_t st, const KvGeom& kv, void* arena, 
     return hipGetLastError();
   }
   const dim3 grid((unsigned)rows, (unsigned)(hq + 2 * kv.num_kv_heads));
-  const dim3 block((unsigned)((kv.head_dim + 63) & ~63));
+  const dim3 block((unsigned)std::min<int64_t>((kv.head_dim + 63) & ~63, 256));
+  const size_t lds = (size_t)kv.head_dim * sizeof(float);
   if (kv.dtype_bf16) {
     uint16_t* base = static_cast<uint16_t*>(arena) + layer * a.layer;
-    hipLaunchKernelGGL(rope_cache_kernel<uint16_t>, grid, block, 0, st, base,
+    hipLaunchKernelGGL(rope_cache_kernel<uint16_t>, grid, block, lds, st, base,
                        a.blk, a.v_off, a.slot, a.head, bs_log2, (int)hq, (int)kv.num_kv_heads,
                        (int)kv.head_dim, q_in, q_stride, q_out, k, k_stride, v, v_stride,
                        positions, row_seq, bt_off, bt_ids, cos_t, sin_t, qp);
   } else {
     float* base = static_cast<float*>(arena) + layer * a.layer;
-    hipLaunchKernelGGL(rope_cache_kernel<float>, grid, block, 0, st, base,
+    hipLaunchKernelGGL(rope_cache_kernel<float>, grid, block, lds, st, base,
                        a.blk, a.v_off, a.slot, a.head, bs_log2, (int)hq, (int)kv.num_kv_heads,
                        (int)kv.head_dim, q_in, q_stride, q_out, k, k_stride, v, v_stride,
                        positions, row_seq, bt_off, bt_ids, cos_t, sin_t, qp);

@@ -121,6 +121,9 @@ struct PrefillPlan {
 };
 int prefill_tile_rows();  // packed rows per prefill workgroup
 int prefill_waves();      // waves per prefill workgroup (8, or 4 with ORION_PREFILL_WAVES=4)
+// Largest head_dim the attention and RoPE kernels take (any even value up to
+// it; the reference accepts any even head_dim).
+constexpr int kMaxHeadDim = 2048;
 constexpr int kPrefillWaveRowTiles = 2;  // 16-row MFMA tiles per prefill wave
 // Prefill operand precision bits (launch_paged_prefill `operands`): each set
 // bit carries that operand as a hi + lo bf16 pair, each clear one rounds it

@@ -557,11 +557,12 @@ static int check_desc(const orion_hip_model_desc* d) {
   if (d->block_size < 4 || d->block_size > 256 || (d->block_size & (d->block_size - 1)))
     return internal(st, "block_size must be a power of two in [4, 256], got %d", d->block_size);
   // RoPE rotates halves (tensor.rs:283-298), so head_dim is even; the
-  // attention kernels cover every even head_dim up to 256 and any grouping
-  // (MFMA for 64 and 128 with groups up to 8, a general wave otherwise).
-  if (d->head_dim % 2 || d->head_dim > 256)
-    return set_err(ORION_HIP_ERR_BACKEND, st, "head_dim %d unsupported (even, at most 256)",
-                   d->head_dim);
+  // attention kernels cover every even head_dim up to kMaxHeadDim and any
+  // grouping (MFMA for 64 and 128 with groups up to 8, a general wave
+  // otherwise).
+  if (d->head_dim % 2 || d->head_dim > kMaxHeadDim)
+    return set_err(ORION_HIP_ERR_BACKEND, st, "head_dim %d unsupported (even, at most %d)",
+                   d->head_dim, kMaxHeadDim);
   if (d->hidden_size % 32 || d->intermediate_size % 32 ||
       (d->num_attention_heads * d->head_dim) % 32)
     return set_err(ORION_HIP_ERR_BACKEND, st,
@@ -1656,9 +1657,9 @@ static int kv_geom_from(const orion_hip_kv_layout* kv, KvGeom* g, const char* st
     return set_err(ORION_HIP_ERR_BACKEND, st, "kv dtype must be F32 or BF16");
   if (kv->block_size < 1 || (kv->block_size & (kv->block_size - 1)) || kv->block_size > 256)
     return internal(st, "block_size must be a power of two <= 256");
-  if (kv->head_dim <= 0 || kv->head_dim % 2 || kv->head_dim > 256)
-    return set_err(ORION_HIP_ERR_BACKEND, st, "head_dim %lld unsupported (even, at most 256)",
-                   (long long)kv->head_dim);
+  if (kv->head_dim <= 0 || kv->head_dim % 2 || kv->head_dim > kMaxHeadDim)
+    return set_err(ORION_HIP_ERR_BACKEND, st, "head_dim %lld unsupported (even, at most %d)",
+                   (long long)kv->head_dim, kMaxHeadDim);
   *g = KvGeom{kv->num_layers, kv->num_blocks, kv->block_size, kv->num_kv_heads, kv->head_dim,
               kv->dtype == ORION_DTYPE_BF16, kv->head_major != 0};
   return ORION_HIP_OK;

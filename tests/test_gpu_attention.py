@@ -103,6 +103,10 @@ def test_shapes_groups_and_block_sizes(backend, hq, hkv, d, bs, dtype, head_majo
     (8, 1, 80, 16, "bf16"), (16, 1, 96, 16, "f32"), (32, 2, 256, 16, "bf16"),
     (32, 1, 64, 16, "bf16"), (24, 2, 128, 8, "f32"), (4, 2, 2, 16, "f32"),
     (6, 3, 160, 32, "bf16"), (12, 1, 48, 4, "bf16"),
+    # head_dim above 256, up to the kernels' 2048: 2, 4, 8 and 16
+    # 128-dimension chunks per lane (and a partial last chunk)
+    (4, 2, 258, 16, "f32"), (8, 2, 512, 16, "bf16"), (4, 1, 1000, 16, "bf16"),
+    (2, 1, 2048, 16, "f32"), (6, 2, 1538, 8, "bf16"),
 ])
 def test_any_head_dim_and_group(backend, hq, hkv, d, bs, dtype):
     ctxs = [1, 2, 17, 64, 65, 300, 513, 1000, 2049]

@@ -457,10 +457,11 @@ def test_fused_decode_layer_matches_oracle_and_unfused(backend, monkeypatch, H, 
 
 
 @pytest.mark.parametrize("H,hq,hkv,d,kv", [(320, 4, 2, 80, oh.F32), (320, 4, 2, 80, oh.BF16),
-                                           (256, 16, 1, 48, oh.F32), (384, 24, 2, 96, oh.BF16)])
+                                           (256, 16, 1, 48, oh.F32), (384, 24, 2, 96, oh.BF16),
+                                           (512, 2, 1, 384, oh.F32), (1024, 2, 2, 1024, oh.F32)])
 def test_any_head_dim_and_group_forward(backend, H, hq, hkv, d, kv):
-    # head_dim 80 / 48 / 96 and groups of 2, 16 and 12 query heads per KV
-    # head: RoPE + cache write, the general decode wave for every row and the
+    # head_dim 80 / 48 / 96 / 384 / 1024 and groups of 1, 2, 16 and 12 query
+    # heads per KV head: RoPE + cache write, the general decode wave for every row and the
     # general merge, through prefill and decode forwards.  A bf16 arena is
     # compared with the oracle rounding K/V to bf16 when written.
     rng = np.random.default_rng(H + hq + d)
@@ -497,9 +498,9 @@ def test_any_head_dim_and_group_forward(backend, H, hq, hkv, d, kv):
     gm.close()
 
 
-@pytest.mark.parametrize("d", [63, 258])
+@pytest.mark.parametrize("d", [63, 2050])
 def test_uncovered_head_dims_are_backend_errors(backend, d):
-    # odd head_dim (RoPE rotates halves) and head_dim above 256
+    # odd head_dim (RoPE rotates halves) and head_dim above the kernels' 2048
     spec = Spec(1, 256, 2, 1, d, 512, 100, num_blocks=8, block_size=16)
     with pytest.raises(oh.BackendError):
         oh.HipTransformerModel(meta_of(spec), 8, 16, backend, oh.F32)

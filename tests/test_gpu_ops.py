@@ -119,16 +119,18 @@ def test_rmsnorm_matches_oracle(backend, rows, cols):
     assert np.all(do.download(np.float32, (1, cols)) == 0)
 
 
-@pytest.mark.parametrize("dtype,head_major,shift", [("f32", False, 0), ("bf16", False, 0),
-                                                    ("bf16", True, 0), ("f32", False, 1),
-                                                    ("bf16", False, 1)])
-def test_rope_and_cache_is_bit_exact(backend, dtype, head_major, shift):
+@pytest.mark.parametrize("dtype,head_major,shift,d", [
+    ("f32", False, 0, 128), ("bf16", False, 0, 128), ("bf16", True, 0, 128),
+    ("f32", False, 1, 128), ("bf16", False, 1, 128),
+    # head_dim above 256: several elements per thread in the scalar kernel
+    ("f32", False, 1, 1000), ("bf16", False, 1, 2048), ("bf16", False, 0, 512)])
+def test_rope_and_cache_is_bit_exact(backend, dtype, head_major, shift, d):
     # RoPE + slot mapping + KV write against the oracle's apply_rope and
     # KvStore.write: the rotated Q, and every arena element, bit for bit.
     # shift 1 moves the q/k/v inputs off 16-byte alignment, which takes the
     # one-element-per-thread kernel instead of the vectorised one.
     rng = np.random.default_rng(17)
-    L, nb, bs, hkv, hq, d = 2, 40, 16, 4, 16, 128
+    L, nb, bs, hkv, hq = 2, 40, 16, 4, 16
     layer = 1
     n = 37
     S = 3
