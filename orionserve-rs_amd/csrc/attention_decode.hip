@@ -502,9 +502,12 @@ __device__ __forceinline__ void decode_wave_mfma2(
 }
 
 // KV: 0 cached K/V loads, 1 streaming, 2 per item (streaming unless the item
-// reads a shared block, DecodeWork::shared).
+// reads a shared block, DecodeWork::shared).  Three waves per SIMD (three
+// workgroups per CU); groups above 8 at head_dim 128 hold too much query
+// tile in LDS for three, and take two.
 template <int D, int G, int KV, bool BIG_BLOCKS>
-__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3)))
+__global__ void __launch_bounds__(256)
+__attribute__((amdgpu_waves_per_eu((D == 128 && G > 8) ? 2 : 3)))
     paged_decode_mfma2_kernel(const uint16_t* __restrict__ kv_layer, uint32_t blk_stride,
                               uint32_t v_off, uint32_t slot_stride,
                               uint32_t head_stride, int bs_log2, int num_kv_heads,
@@ -835,6 +838,14 @@ static hipError_t launch_mfma2(int G, dim3 grid, hipStream_t st, const uint16_t*
     ORION_MFMA2_CASE(6)
     ORION_MFMA2_CASE(7)
     ORION_MFMA2_CASE(8)
+    ORION_MFMA2_CASE(9)
+    ORION_MFMA2_CASE(10)
+    ORION_MFMA2_CASE(11)
+    ORION_MFMA2_CASE(12)
+    ORION_MFMA2_CASE(13)
+    ORION_MFMA2_CASE(14)
+    ORION_MFMA2_CASE(15)
+    ORION_MFMA2_CASE(16)
     default:
       return hipErrorInvalidValue;
   }
@@ -907,7 +918,10 @@ hipError_t launch_paged_decode(hipStream_t st, const KvGeom& kv, const void* are
   const float scale = 1.0f / sqrtf((float)D);
   const dim3 grid((unsigned)((plan.num_work + 3) / 4));
   hipError_t e;
-  if ((D != 64 && D != 128) || G > 8) {
+  // bf16 arenas at head_dim 64/128 with up to 16 query heads per KV head (the
+  // MFMA B operand's 16 columns) take the MFMA wave; f32 arenas take the VALU
+  // wave up to 8; everything else the general wave.
+  if ((D != 64 && D != 128) || G > (kv.dtype_bf16 ? 16 : 8)) {
     if (D > kMaxHeadDim || (D & 1)) return hipErrorInvalidValue;
 #define ORION_ANY(TT, NC)                                                                      \
   hipLaunchKernelGGL((paged_decode_any_kernel<TT, NC>), grid, dim3(256), 0, st,                \

@@ -558,7 +558,7 @@ static int check_desc(const orion_hip_model_desc* d) {
     return internal(st, "block_size must be a power of two in [4, 256], got %d", d->block_size);
   // RoPE rotates halves (tensor.rs:283-298), so head_dim is even; the
   // attention kernels cover every even head_dim up to kMaxHeadDim and any
-  // grouping (MFMA for 64 and 128 with groups up to 8, a general wave
+  // grouping (MFMA for 64 and 128 with groups up to 16 on bf16 arenas, a general wave
   // otherwise).
   if (d->head_dim % 2 || d->head_dim > kMaxHeadDim)
     return set_err(ORION_HIP_ERR_BACKEND, st, "head_dim %d unsupported (even, at most %d)",
@@ -1429,7 +1429,7 @@ ORION_EXPORT int orion_hip_model_forward(orion_hip_model* m, const orion_hip_bat
   // call; lets tests compare the two routes on one batch).
   const char* route = getenv("ORION_PREFILL_ROUTE");
   const bool route_pf = !(route && route[0] == '0');
-  if (route_pf && m->kv.dtype_bf16 && (d.head_dim == 64 || d.head_dim == 128) && G <= 8) {
+  if (route_pf && m->kv.dtype_bf16 && (d.head_dim == 64 || d.head_dim == 128)) {
     int64_t r0 = 0;
     for (int64_t s = 0; s < S; ++s) {
       const int64_t c = b->slot_token_counts[s];
@@ -1784,11 +1784,6 @@ ORION_EXPORT int orion_hip_paged_attention_prefill(
     return set_err(ORION_HIP_ERR_BACKEND, st,
                    "prefill attention covers head_dim 64 and 128 (got %lld); other shapes take "
                    "the decode entry point row by row", (long long)g.head_dim);
-  if (num_q_heads / g.num_kv_heads > 8)
-    return set_err(ORION_HIP_ERR_BACKEND, st,
-                   "prefill attention covers groups of up to 8 query heads per kv head (got "
-                   "%lld); larger groups take the decode entry point",
-                   (long long)(num_q_heads / g.num_kv_heads));
   HIP_TRY(st, hipSetDevice(dev->ordinal));
   (void)max_rows;
   (void)max_position;

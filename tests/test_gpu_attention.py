@@ -107,6 +107,9 @@ def test_shapes_groups_and_block_sizes(backend, hq, hkv, d, bs, dtype, head_majo
     # 128-dimension chunks per lane (and a partial last chunk)
     (4, 2, 258, 16, "f32"), (8, 2, 512, 16, "bf16"), (4, 1, 1000, 16, "bf16"),
     (2, 1, 2048, 16, "f32"), (6, 2, 1538, 8, "bf16"),
+    # groups of 9 to 16 on bf16 arenas at head_dim 64/128: the MFMA wave
+    (16, 1, 128, 16, "bf16"), (24, 2, 128, 16, "bf16"), (18, 2, 64, 16, "bf16"),
+    (64, 4, 64, 16, "bf16"), (20, 2, 128, 8, "bf16"),
 ])
 def test_any_head_dim_and_group(backend, hq, hkv, d, bs, dtype):
     ctxs = [1, 2, 17, 64, 65, 300, 513, 1000, 2049]

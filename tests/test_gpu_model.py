@@ -458,10 +458,12 @@ def test_fused_decode_layer_matches_oracle_and_unfused(backend, monkeypatch, H, 
 
 @pytest.mark.parametrize("H,hq,hkv,d,kv", [(320, 4, 2, 80, oh.F32), (320, 4, 2, 80, oh.BF16),
                                            (256, 16, 1, 48, oh.F32), (384, 24, 2, 96, oh.BF16),
-                                           (512, 2, 1, 384, oh.F32), (1024, 2, 2, 1024, oh.F32)])
+                                           (512, 2, 1, 384, oh.F32), (1024, 2, 2, 1024, oh.F32),
+                                           (1024, 16, 1, 64, oh.BF16)])
 def test_any_head_dim_and_group_forward(backend, H, hq, hkv, d, kv):
     # head_dim 80 / 48 / 96 / 384 / 1024 and groups of 1, 2, 16 and 12 query
-    # heads per KV head: RoPE + cache write, the general decode wave for every row and the
+    # heads per KV head (and head_dim 64 with 16, whose prompts take the MFMA
+    # prefill kernel): RoPE + cache write, the general decode wave for every row and the
     # general merge, through prefill and decode forwards.  A bf16 arena is
     # compared with the oracle rounding K/V to bf16 when written.
     rng = np.random.default_rng(H + hq + d)
@@ -483,7 +485,13 @@ def test_any_head_dim_and_group_forward(backend, H, hq, hkv, d, kv):
     tables = [list(range(16 * s, 16 * s + 16)) for s in range(3)]
     toks = rng.integers(0, spec.V, sum(lens))
     pos = np.concatenate([np.arange(n) for n in lens])
-    bound = 1e-4 if kv == oh.F32 else 1e-3
+    # bf16 KV: the oracle rounds K/V to bf16 as well, but an element whose f32
+    # value differs in its last bits between the two sides can round to the
+    # other neighbour.  Measured on the MI355X at hidden 1024 with one or two
+    # KV heads (every query head reads the same rounded K/V): 1.2e-3 to 2.4e-3
+    # relative, equal through the prefill and the decode kernels, against
+    # 4e-5 on f32 arenas of the same shapes; 6.5e-4 at hidden 384.
+    bound = 1e-4 if kv == oh.F32 else (1e-3 if H < 1024 else 3e-3)
     print(f"[any head_dim] H={H} hq={hq} hkv={hkv} d={d} kv={kv}", flush=True)
     g = gm.forward(batch(toks, pos, lens, tables)).logits
     o = om.forward(toks, pos, lens, lens, tables)

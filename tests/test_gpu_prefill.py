@@ -64,6 +64,8 @@ def test_cfg3_full_size_sampled_rows(backend, hilo, head_major):
 @pytest.mark.parametrize("hq,hkv,d,bs", [
     (32, 8, 128, 16), (28, 4, 128, 16), (32, 4, 64, 16), (8, 2, 64, 16), (8, 8, 64, 8),
     (12, 4, 128, 32), (6, 1, 64, 1), (16, 16, 128, 64),
+    # groups above 8 (Llama-3.1-405B has 16 query heads per KV head; MQA)
+    (32, 2, 128, 16), (12, 1, 128, 16), (32, 1, 64, 16),
 ])
 @pytest.mark.parametrize("hilo", [False, True])
 @pytest.mark.parametrize("head_major", [False, True])
@@ -163,9 +165,9 @@ def test_f32_arena_is_a_backend_error(backend):
         run_prefill(backend, case, False)
 
 
-@pytest.mark.parametrize("hq,hkv,d", [(8, 2, 80), (16, 1, 64), (4, 2, 256)])
+@pytest.mark.parametrize("hq,hkv,d", [(8, 2, 80), (4, 2, 256), (8, 1, 96)])
 def test_uncovered_prefill_shapes_are_backend_errors(backend, hq, hkv, d):
-    # The MFMA prefill kernel covers head_dim 64/128 with groups up to 8; the
+    # The MFMA prefill kernel covers head_dim 64/128 with any grouping; the
     # model forward sends other shapes' rows to the decode kernel (which
     # covers every even head_dim up to 256 and any group), and the op-level
     # entry point refuses them with a Backend error before any launch.
