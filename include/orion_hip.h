@@ -312,7 +312,12 @@ int orion_hip_model_kv_layout(orion_hip_model* model, orion_hip_kv_layout* out);
  * evenly loaded on ragged batches; each item carries its table offset and first
  * block id.  A plan depends only on the batch, so one plan serves every layer
  * of a forward pass.  The plan also owns the split-K workspace.  Rows whose
- * position has no block in their table are rejected (EngineError::Internal). */
+ * position has no block in their table are rejected (EngineError::Internal).
+ * Rows whose tables start with the same block ids (a shared prefix, as
+ * prefix caching leaves them) attend that prefix together on bf16 arenas at
+ * head_dim 64/128: the query heads of up to 16 / (query heads per KV head)
+ * such rows share one work item per prefix piece ("packed" items), so each
+ * prefix block is read once per pack rather than once per row. */
 typedef struct orion_hip_decode_plan orion_hip_decode_plan;
 int orion_hip_decode_plan_create(orion_hip_device* dev, const uint32_t* positions,
                                  const int32_t* row_seq, const int64_t* block_table_offsets,
@@ -323,6 +328,11 @@ void orion_hip_decode_plan_destroy(orion_hip_decode_plan* plan);
 /* Chunk length in tokens, number of work items, chunks of the longest row. */
 int orion_hip_decode_plan_info(const orion_hip_decode_plan* plan, int64_t* chunk,
                                int64_t* num_work, int64_t* max_splits);
+/* Packed prefix items among num_work (as planned for a bf16 arena) and the
+ * rows each packs (0 when nothing is packed).  No counterpart in the
+ * reference: a planning statistic for tests and measurement. */
+int orion_hip_decode_plan_packed(const orion_hip_decode_plan* plan, int64_t* packed_items,
+                                 int64_t* rows_per_pack);
 
 /* paged_attention (attention.rs:219-295) for `num_rows` independent query
  * rows: row r attends positions 0..=d_positions[r] of the sequence

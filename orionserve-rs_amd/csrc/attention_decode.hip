@@ -270,21 +270,25 @@ __device__ __forceinline__ uint4 kv_load16(const uint16_t* p) {
   }
 }
 
-template <int D, int G, bool STREAM, bool BIG_BLOCKS>
+// PR > 1: a packed item -- the query columns hold the G heads of each of up
+// to PR rows (prow[0 .. PR), -1 unused) that share this piece's blocks;
+// column c is head c % G of row prow[c / G].
+template <int D, int G, bool STREAM, bool BIG_BLOCKS, int PR = 1>
 __device__ __forceinline__ void decode_wave_mfma2(
     const uint16_t* __restrict__ kv_layer, uint32_t blk_stride, uint32_t v_off,
     uint32_t slot_stride, uint32_t head_stride, int bs_log2, int num_q_heads, const float* __restrict__ q,
     const uint32_t* __restrict__ tbl, int blk0, int max_splits, float scale,
     float* __restrict__ out, float* __restrict__ ws_o, float* __restrict__ ws_ml, uint16_t* VL,
     uint16_t* QL, uint16_t* KL, int row, int kvh,
-    int start, int end, int split, int nsplit) {
+    int start, int end, int split, int nsplit, const int32_t* __restrict__ prow = nullptr) {
+  constexpr int QC = G * PR;      // query columns in use
   constexpr int KCH = D / 32;     // K . Q^T MFMA k-steps
   constexpr int DT = D / 16;      // output dim tiles of the P.V MFMA
   constexpr int CH = D / 8;       // lanes per V row (16 bytes each)
   constexpr int TPW = 64 / CH;    // V rows per wave load
   constexpr int RV = 16 / TPW;    // V loads per lane per step
   constexpr int VROW = D + 8;     // padded LDS row, in bf16 elements
-  static_assert(G <= 16 && TPW <= 16 && (16 % TPW) == 0, "unsupported shape");
+  static_assert(QC <= 16 && TPW <= 16 && (16 % TPW) == 0, "unsupported shape");
 
   const int lane = threadIdx.x & 63;
   const int bs_mask = (1 << bs_log2) - 1;
@@ -297,8 +301,17 @@ __device__ __forceinline__ void decode_wave_mfma2(
   constexpr int KCH_ = D / 32;
   const int kd_ = grp * 8;
   float4 qr[2 * KCH_];
+  // this lane's query column: head qhead of row qrow (columns past QC repeat
+  // column QC - 1; their scores are never used)
+  int qrow = row, qhead = min(l16, G - 1);
+  if constexpr (PR > 1) {
+    const int col = min(l16, QC - 1);
+    const int pr = prow[col / G];
+    qrow = pr >= 0 ? pr : prow[0];
+    qhead = col % G;
+  }
   {
-    const float* qp = q + ((int64_t)row * num_q_heads + (int64_t)kvh * G + min(l16, G - 1)) * D + kd_;
+    const float* qp = q + ((int64_t)qrow * num_q_heads + (int64_t)kvh * G + qhead) * D + kd_;
 #pragma unroll
     for (int j = 0; j < KCH_; ++j) {
       qr[2 * j] = *reinterpret_cast<const float4*>(qp + 32 * j);
@@ -354,7 +367,7 @@ __device__ __forceinline__ void decode_wave_mfma2(
   // VGPRs.  B-operand column l16 >= G reads head l16 % G: those columns of S
   // are never used, and duplicating a real head keeps them finite.
   constexpr int QROW = D + 8;
-  const int qh = l16 % G;
+  const int qh = l16 % QC;
   {
 #pragma unroll
     for (int j = 0; j < KCH; ++j) {
@@ -363,16 +376,16 @@ __device__ __forceinline__ void decode_wave_mfma2(
       split2_trunc(qr[2 * j].z, qr[2 * j].w, hv.y, lv.y);
       split2_trunc(qr[2 * j + 1].x, qr[2 * j + 1].y, hv.z, lv.z);
       split2_trunc(qr[2 * j + 1].z, qr[2 * j + 1].w, hv.w, lv.w);
-      if (l16 < G) {
+      if (l16 < QC) {
         *reinterpret_cast<uint4*>(&QL[l16 * QROW + 32 * j + kd]) = hv;
-        *reinterpret_cast<uint4*>(&QL[(G + l16) * QROW + 32 * j + kd]) = lv;
+        *reinterpret_cast<uint4*>(&QL[(QC + l16) * QROW + 32 * j + kd]) = lv;
       }
     }
   }
   wave_lds_sync();
   auto qb = [&](int j, int lo) -> bf16x8 {
     uint4 v;
-    __builtin_memcpy(&v, (const void*)&QL[(lo * G + qh) * QROW + 32 * j + kd], 16);
+    __builtin_memcpy(&v, (const void*)&QL[(lo * QC + qh) * QROW + 32 * j + kd], 16);
     return __builtin_bit_cast(bf16x8, v);
   };
 
@@ -482,8 +495,14 @@ __device__ __forceinline__ void decode_wave_mfma2(
 
   lsum += __shfl_xor(lsum, 16);
   lsum += __shfl_xor(lsum, 32);
-  if (l16 >= G) return;
-  const int64_t hidx = (int64_t)row * num_q_heads + (int64_t)kvh * G + l16;
+  if (l16 >= QC) return;
+  int orow = row, ohead = l16;
+  if constexpr (PR > 1) {
+    orow = prow[l16 / G];
+    ohead = l16 % G;
+    if (orow < 0) return;
+  }
+  const int64_t hidx = (int64_t)orow * num_q_heads + (int64_t)kvh * G + ohead;
   if (nsplit == 1) {
     const float inv = 1.f / lsum;
     float* op = out + hidx * D + 4 * grp;
@@ -505,9 +524,11 @@ __device__ __forceinline__ void decode_wave_mfma2(
 // reads a shared block, DecodeWork::shared).  Three waves per SIMD (three
 // workgroups per CU); groups above 8 at head_dim 128 hold too much query
 // tile in LDS for three, and take two.
-template <int D, int G, int KV, bool BIG_BLOCKS>
+// PR > 1: the plan holds packed prefix items (DecodeWork::shared == 2), PR
+// rows each, whose rows are pack_rows[pack * PR ..]; they take cached loads.
+template <int D, int G, int KV, bool BIG_BLOCKS, int PR = 1>
 __global__ void __launch_bounds__(256)
-__attribute__((amdgpu_waves_per_eu((D == 128 && G > 8) ? 2 : 3)))
+__attribute__((amdgpu_waves_per_eu((D == 128 && G * PR > 8) ? 2 : 3)))
     paged_decode_mfma2_kernel(const uint16_t* __restrict__ kv_layer, uint32_t blk_stride,
                               uint32_t v_off, uint32_t slot_stride,
                               uint32_t head_stride, int bs_log2, int num_kv_heads,
@@ -517,15 +538,25 @@ __attribute__((amdgpu_waves_per_eu((D == 128 && G > 8) ? 2 : 3)))
                               const int64_t* __restrict__ bt_off,
                               const uint32_t* __restrict__ bt_ids, int max_splits,
                               float scale, float* __restrict__ out, float* __restrict__ ws_o,
-                              float* __restrict__ ws_ml) {
+                              float* __restrict__ ws_ml, const int32_t* __restrict__ pack_rows) {
   __shared__ __attribute__((aligned(16))) uint16_t lds_v[4][16 * (D + 8)];
-  __shared__ __attribute__((aligned(16))) uint16_t lds_q[4][2 * G * (D + 8)];
+  __shared__ __attribute__((aligned(16))) uint16_t lds_q[4][2 * G * PR * (D + 8)];
   __shared__ __attribute__((aligned(16))) uint16_t lds_k[4][16 * D];
   const int wv = threadIdx.x >> 6;
   const int w = blockIdx.x * 4 + wv;
   if (w >= num_work) return;
   const DecodeWork wk = work[w];
   const int row = wk.item / num_kv_heads, kvh = wk.item - row * num_kv_heads;
+  if constexpr (PR > 1) {
+    if (__builtin_amdgcn_readfirstlane(wk.shared) == 2) {  // row = the pack index
+      decode_wave_mfma2<D, G, false, BIG_BLOCKS, PR>(
+          kv_layer, blk_stride, v_off, slot_stride, head_stride, bs_log2, num_q_heads, q,
+          bt_ids + wk.tbl_off, wk.blk0, max_splits, scale, out, ws_o, ws_ml, lds_v[wv],
+          lds_q[wv], lds_k[wv], -1, kvh, wk.start, wk.end, wk.split, wk.nsplit,
+          pack_rows + (int64_t)row * PR);
+      return;
+    }
+  }
   auto run = [&](auto stream_tag) {
     decode_wave_mfma2<D, G, decltype(stream_tag)::value, BIG_BLOCKS>(
         kv_layer, blk_stride, v_off, slot_stride, head_stride, bs_log2, num_q_heads, q,
@@ -533,7 +564,7 @@ __attribute__((amdgpu_waves_per_eu((D == 128 && G > 8) ? 2 : 3)))
         lds_k[wv], row, kvh, wk.start, wk.end, wk.split, wk.nsplit);
   };
   if constexpr (KV == 2) {
-    if (__builtin_amdgcn_readfirstlane(wk.shared))
+    if (__builtin_amdgcn_readfirstlane(wk.shared) == 1)
       run(std::false_type{});
     else
       run(std::true_type{});
@@ -820,14 +851,19 @@ static hipError_t launch_mfma2(int G, dim3 grid, hipStream_t st, const uint16_t*
                                const DecodeWork* work, int nwork, const float* q,
                                const uint32_t* pos, const int32_t* rs, const int64_t* bo,
                                const uint32_t* bi, int ms, float scale, float* out,
-                               float* wo, float* wml) {
+                               float* wo, float* wml, const int32_t* pack_rows) {
 #define ORION_MFMA2_CASE(GG)                                                                   \
   case GG:                                                                                     \
-    hipLaunchKernelGGL((paged_decode_mfma2_kernel<D, GG, KV, BIG>), grid, dim3(256), 0, st,     \
-                       kv,                                                                     \
-                       (uint32_t)a.blk, (uint32_t)a.v_off, (uint32_t)a.slot, (uint32_t)a.head, \
-                       bsl, hkv, hq, work, nwork, q, pos, rs, bo, bi, ms, scale, out, wo,      \
-                       wml);                                                                   \
+    if (pack_rows && 16 / GG >= 2)                                                             \
+      hipLaunchKernelGGL((paged_decode_mfma2_kernel<D, GG, KV, BIG, (16 / GG >= 2 ? 16 / GG : 1)>), \
+                         grid, dim3(256), 0, st, kv, (uint32_t)a.blk, (uint32_t)a.v_off,       \
+                         (uint32_t)a.slot, (uint32_t)a.head, bsl, hkv, hq, work, nwork, q, pos, \
+                         rs, bo, bi, ms, scale, out, wo, wml, pack_rows);                     \
+    else                                                                                       \
+      hipLaunchKernelGGL((paged_decode_mfma2_kernel<D, GG, KV, BIG>), grid, dim3(256), 0, st,   \
+                         kv, (uint32_t)a.blk, (uint32_t)a.v_off, (uint32_t)a.slot,             \
+                         (uint32_t)a.head, bsl, hkv, hq, work, nwork, q, pos, rs, bo, bi, ms,  \
+                         scale, out, wo, wml, nullptr);                                        \
     break;
   switch (G) {
     ORION_MFMA2_CASE(1)
@@ -921,6 +957,10 @@ hipError_t launch_paged_decode(hipStream_t st, const KvGeom& kv, const void* are
   // bf16 arenas at head_dim 64/128 with up to 16 query heads per KV head (the
   // MFMA B operand's 16 columns) take the MFMA wave; f32 arenas take the VALU
   // wave up to 8; everything else the general wave.
+  // packed prefix items exist only for the MFMA wave, pack_r = 16 / G rows
+  const bool mfma = kv.dtype_bf16 && (D == 64 || D == 128) && G <= 16;
+  if (plan.num_packed && (!mfma || G > 8 || plan.pack_r != 16 / G || !plan.pack_rows))
+    return hipErrorInvalidValue;
   if ((D != 64 && D != 128) || G > (kv.dtype_bf16 ? 16 : 8)) {
     if (D > kMaxHeadDim || (D & 1)) return hipErrorInvalidValue;
 #define ORION_ANY(TT, NC)                                                                      \
@@ -954,7 +994,7 @@ hipError_t launch_paged_decode(hipStream_t st, const KvGeom& kv, const void* are
 #define ORION_MFMA2(DD, SS, BB)                                                                      \
   launch_mfma2<DD, SS, BB>(G, grid, st, base, a, bs_log2, (int)hkv, (int)hq, plan.work,          \
                        plan.num_work, q, positions, row_seq, bt_off, bt_ids, ms, scale, out,    \
-                       ws_o, ws_ml)
+                       ws_o, ws_ml, plan.num_packed ? plan.pack_rows : nullptr)
     // per-item load flavour only with whole-block steps (blocks of >= 16 slots)
     const int kvm = plan.stream_kv ? 1 : (plan.mixed_kv && big) ? 2 : 0;
     if (D == 128)

@@ -6,6 +6,8 @@
 #include <algorithm>
 #include <cstdint>
 #include <cstdlib>
+#include <unordered_map>
+#include <utility>
 #include <vector>
 
 namespace orion {
@@ -53,28 +55,95 @@ static int64_t estimate_split_time(const std::vector<int>& lens, int64_t hkv, in
   return std::max(fluid, largest + kItemOverhead);
 }
 
+// Shortest shared prefix worth a packed item (tokens).
+constexpr int kMinPackPrefix = 256;
+
 void build_decode_plan(const uint32_t* positions, const int32_t* row_seq,
                        const int64_t* bt_offsets, const uint32_t* bt_ids, int64_t rows,
                        int64_t hkv, int64_t block_size, int64_t wave_slots,
-                       const uint8_t* skip_rows, DecodePlanHost* plan) {
+                       const uint8_t* skip_rows, DecodePlanHost* plan, int pack_r) {
   int bs_log2 = 0;
   while ((1 << bs_log2) < block_size) ++bs_log2;
+  const int unit = (int)std::max<int64_t>(16, block_size);
   // Rows flagged in skip_rows get no work (another kernel covers them);
   // their length counts as 0 for the chunk choice and the split bound.
   std::vector<int> lens(rows);
-  int max_len = 0;
   plan->rows.clear();
   for (int64_t r = 0; r < rows; ++r) {
     const bool skip = skip_rows && skip_rows[r];
     lens[r] = skip ? 0 : (int)positions[r] + 1;
-    max_len = std::max(max_len, lens[r]);
     if (skip_rows && !skip) plan->rows.push_back((int32_t)r);
   }
+
+  // ---- packs: rows whose tables start with the same block ids (a shared
+  // prefix) attend that prefix together, pack_r rows per item.  Rows are
+  // grouped by their first block id and ordered by how many leading blocks
+  // they share with the group's first row; each pack's prefix is the part
+  // all its rows share, in whole units, short of every row's last position
+  // (so each row keeps a private piece). ORION_DECODE_PACK=0 disables
+  // packing (measurement knob, read per call). ----
+  const char* pack_env = getenv("ORION_DECODE_PACK");
+  if (pack_env && pack_env[0] == '0') pack_r = 0;
+  std::vector<int> prefix(rows, 0), pack_of(rows, -1);
+  std::vector<int> pack_len;  // shared prefix tokens of each pack
+  plan->pack_rows.clear();
+  plan->pack_r = pack_r >= 2 ? pack_r : 0;
+  if (pack_r >= 2) {
+    std::unordered_map<uint32_t, std::vector<int64_t>> by_first;
+    for (int64_t r = 0; r < rows; ++r)
+      if (lens[r] > kMinPackPrefix) by_first[bt_ids[bt_offsets[row_seq[r]]]].push_back(r);
+    std::vector<uint32_t> keys;
+    for (const auto& kv : by_first)
+      if (kv.second.size() >= 2) keys.push_back(kv.first);
+    std::sort(keys.begin(), keys.end());  // deterministic pack order
+    for (uint32_t key : keys) {
+      std::vector<int64_t>& grp = by_first[key];
+      const int64_t r0 = grp[0];
+      const uint32_t* t0 = bt_ids + bt_offsets[row_seq[r0]];
+      const int64_t nb0 = ((int64_t)lens[r0] + block_size - 1) >> bs_log2;
+      std::vector<std::pair<int64_t, int64_t>> lcp;  // (shared blocks with r0, row)
+      for (int64_t r : grp) {
+        const uint32_t* t = bt_ids + bt_offsets[row_seq[r]];
+        const int64_t nb = std::min<int64_t>(nb0, ((int64_t)lens[r] + block_size - 1) >> bs_log2);
+        int64_t k = 0;
+        while (k < nb && t[k] == t0[k]) ++k;
+        lcp.push_back({k, r});
+      }
+      std::stable_sort(lcp.begin(), lcp.end(),
+                       [](const auto& a, const auto& b) { return a.first > b.first; });
+      for (size_t i = 0; i + 2 <= lcp.size(); i += pack_r) {
+        const size_t e = std::min(lcp.size(), i + (size_t)pack_r);
+        int64_t L = INT64_MAX;
+        for (size_t j = i; j < e; ++j)
+          L = std::min<int64_t>(L, std::min<int64_t>(lcp[j].first * block_size,
+                                                     lens[lcp[j].second] - 1));
+        L = L / unit * unit;
+        if (L < kMinPackPrefix) continue;
+        const int pk = (int)pack_len.size();
+        pack_len.push_back((int)L);
+        for (size_t j = i; j < i + (size_t)pack_r; ++j) {
+          const int64_t r = j < e ? lcp[j].second : -1;
+          plan->pack_rows.push_back((int32_t)r);
+          if (r >= 0) prefix[r] = (int)L, pack_of[r] = pk;
+        }
+      }
+    }
+  }
+  const int npacks = (int)pack_len.size();
+
+  // The segments the pieces are cut from: each row's private part [prefix,
+  // len) and each pack's prefix [0, L).
+  std::vector<int> seg;
+  int max_len = 0;
+  for (int64_t r = 0; r < rows; ++r) seg.push_back(lens[r] - prefix[r]);
+  for (int L : pack_len) seg.push_back(L);
+  for (int L : seg) max_len = std::max(max_len, L);
+
   int best_c = 0;
   int64_t best_t = 0;
   for (int C = 64; C <= 2048; C <<= 1) {
     if (C < block_size || C / block_size > 64) continue;
-    const int64_t t = estimate_split_time(lens, hkv, C, wave_slots);
+    const int64_t t = estimate_split_time(seg, hkv, C, wave_slots);
     if (best_c == 0 || t < best_t) {
       best_c = C;
       best_t = t;
@@ -90,8 +159,8 @@ void build_decode_plan(const uint32_t* positions, const int32_t* row_seq,
       forced / block_size <= 64)
     best_c = forced;
   const int C = best_c;
-  // Balanced pieces: row r is cut into n_r = ceil(L_r / P) pieces of equal
-  // length (rounded up to whole blocks of at least 16 tokens), with the
+  // Balanced pieces: segment s is cut into n_s = ceil(L_s / P) pieces of
+  // equal length (rounded up to whole blocks of at least 16 tokens), with the
   // bound P the smallest for which every item fits in one round of the
   // resident wave slots, so no wave starts after the first round and the
   // pieces of a row end together.  ORION_DECODE_BALANCE=0 keeps fixed chunks.
@@ -99,7 +168,6 @@ void build_decode_plan(const uint32_t* positions, const int32_t* row_seq,
   // one per lane.)
   const char* balance_env = getenv("ORION_DECODE_BALANCE");
   const bool balance_knob = !(balance_env && balance_env[0] == '0');
-  const int unit = (int)std::max<int64_t>(16, block_size);
   const int max_piece = (int)std::max<int64_t>(unit, 64 * block_size / unit * unit);
   auto pieces_of = [&](int L, int P, int* piece) {
     const int n = (L + P - 1) / P;
@@ -108,7 +176,7 @@ void build_decode_plan(const uint32_t* positions, const int32_t* row_seq,
   };
   auto items_at = [&](int P) {
     int64_t items = 0;
-    for (int L : lens) {
+    for (int L : seg) {
       int piece;
       if (L) items += hkv * pieces_of(L, P, &piece);
     }
@@ -136,7 +204,7 @@ void build_decode_plan(const uint32_t* positions, const int32_t* row_seq,
       // fixed chunks.
       if (bal_p) {
         int64_t items = 0, total = 0, largest = 0;
-        for (int L : lens) {
+        for (int L : seg) {
           if (!L) continue;
           int piece;
           const int n = pieces_of(L, bal_p, &piece);
@@ -156,42 +224,65 @@ void build_decode_plan(const uint32_t* positions, const int32_t* row_seq,
   plan->row_nsplit.assign(rows, 0);
   plan->chunk = 0;
   plan->max_splits = 0;
-  // (start, length, row) of every piece, then ordered longest first (stable:
-  // a row's pieces stay in order, full chunks before tails)
-  struct Piece {
-    int start, len;
-    int64_t row;
-  };
-  std::vector<Piece> pcs;
-  std::vector<int> row_piece(rows, 1);
-  for (int64_t r = 0; r < rows; ++r) {
-    const int L = lens[r];
-    if (!L) continue;
+  auto piece_len = [&](int L) {
     int piece = C;
     if (bal_p) pieces_of(L, bal_p, &piece);
-    const int n = (L + piece - 1) / piece;
-    row_piece[r] = piece;
-    plan->row_nsplit[r] = n;
-    plan->max_splits = std::max(plan->max_splits, n);
-    plan->chunk = std::max(plan->chunk, std::min(piece, L));
-    for (int s = 0; s < n; ++s) pcs.push_back({s * piece, std::min(L - s * piece, piece), r});
+    return piece;
+  };
+  // pack prefixes: np pieces each, splits 0 .. np-1 of every row of the pack
+  std::vector<int> pack_np(npacks), pack_piece(npacks);
+  for (int pk = 0; pk < npacks; ++pk) {
+    pack_piece[pk] = piece_len(pack_len[pk]);
+    pack_np[pk] = (pack_len[pk] + pack_piece[pk] - 1) / pack_piece[pk];
+    plan->chunk = std::max(plan->chunk, std::min(pack_piece[pk], pack_len[pk]));
   }
+  // (start, length, row or pack, split) of every piece, then ordered longest
+  // first (stable: a row's pieces stay in order, full chunks before tails)
+  struct Piece {
+    int start, len;
+    int64_t row;  // pack index for packed pieces
+    int split;
+    bool packed;
+  };
+  std::vector<Piece> pcs;
+  for (int64_t r = 0; r < rows; ++r) {
+    const int L = lens[r] - prefix[r];
+    if (!lens[r]) continue;
+    const int piece = piece_len(L);
+    const int n = (L + piece - 1) / piece;
+    const int np = pack_of[r] >= 0 ? pack_np[pack_of[r]] : 0;
+    plan->row_nsplit[r] = np + n;
+    plan->max_splits = std::max(plan->max_splits, np + n);
+    plan->chunk = std::max(plan->chunk, std::min(piece, L));
+    for (int s = 0; s < n; ++s)
+      pcs.push_back({prefix[r] + s * piece, std::min(L - s * piece, piece), r, np + s, false});
+  }
+  for (int pk = 0; pk < npacks; ++pk)
+    for (int s = 0; s < pack_np[pk]; ++s)
+      pcs.push_back({s * pack_piece[pk], std::min(pack_len[pk] - s * pack_piece[pk],
+                                                  pack_piece[pk]), pk, s, true});
   std::stable_sort(pcs.begin(), pcs.end(),
                    [](const Piece& a, const Piece& b) { return a.len > b.len; });
   plan->work.reserve(pcs.size() * hkv);
+  plan->num_packed = 0;
   for (const Piece& pc : pcs) {
-    const int64_t tbl_off = bt_offsets[row_seq[pc.row]] + (pc.start >> bs_log2);
-    const int32_t n = plan->row_nsplit[pc.row];
-    const int32_t split = pc.start / row_piece[pc.row];
+    const int64_t r0 = pc.packed ? plan->pack_rows[pc.row * pack_r] : pc.row;
+    const int64_t tbl_off = bt_offsets[row_seq[r0]] + (pc.start >> bs_log2);
+    // a packed item always writes partials (nsplit 2: every row of the pack
+    // has a private piece too) and is flagged shared = 2
+    const int32_t n = pc.packed ? 2 : plan->row_nsplit[pc.row];
     for (int64_t h = 0; h < hkv; ++h)
       plan->work.push_back({(int32_t)(pc.row * hkv + h), pc.start, pc.start + pc.len, n,
-                            (int32_t)tbl_off, (int32_t)bt_ids[tbl_off], 0, split});
+                            (int32_t)tbl_off, (int32_t)bt_ids[tbl_off], pc.packed ? 2 : 0,
+                            pc.split});
+    if (pc.packed) plan->num_packed += (int)hkv;
   }
+  const int64_t num_plain = (int64_t)plan->work.size() - plan->num_packed;
   // Shared blocks: a block id attended by two planned rows (two rows of one
   // sequence share their prefix blocks too).  One pass over the attended
   // ids with two bitmaps (seen, seen again) that are cleared afterwards;
-  // then each work item is flagged when its token range reads a shared
-  // block.
+  // then each plain work item is flagged when its token range reads a
+  // shared block (packed items, shared = 2, keep cached loads).
   static thread_local std::vector<uint64_t> seen, again;
   bool shared = false;
   size_t w_lo = SIZE_MAX, w_hi = 0;  // words touched (cleared afterwards)
@@ -220,6 +311,7 @@ void build_decode_plan(const uint32_t* positions, const int32_t* row_seq,
     // the hkv items of a piece are adjacent and read the same blocks
     for (size_t i = 0; i < plan->work.size(); i += hkv) {
       const DecodeWork& wk = plan->work[i];
+      if (wk.shared == 2) continue;
       const int nb = ((wk.end - 1) >> bs_log2) - (wk.start >> bs_log2) + 1;
       bool s = false;
       for (int j = 0; j < nb && !s; ++j) {
@@ -235,7 +327,14 @@ void build_decode_plan(const uint32_t* positions, const int32_t* row_seq,
     std::fill(again.begin() + w_lo, again.begin() + w_hi + 1, 0);
   }
   plan->stream_kv = !shared;
-  plan->mixed_kv = shared && shared_items < (int64_t)plan->work.size();
+  plan->mixed_kv = shared && shared_items < num_plain;
+}
+
+int decode_pack_rows(const KvGeom& kv, int64_t hq) {
+  if (!kv.dtype_bf16 || (kv.head_dim != 64 && kv.head_dim != 128) || kv.num_kv_heads <= 0)
+    return 0;
+  const int64_t G = hq / kv.num_kv_heads;
+  return G >= 1 && G <= 8 ? (int)(16 / G) : 0;
 }
 
 size_t decode_workspace_bytes(int64_t rows, int64_t hq, int64_t D, int64_t max_splits) {

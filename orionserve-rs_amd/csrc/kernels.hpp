@@ -47,7 +47,8 @@ inline ArenaStrides arena_strides(const KvGeom& kv) {
 // first entry, so the first step's loads can be issued before the slice
 // arrives.
 struct DecodeWork {
-  // shared: the item reads a block that another planned row also reads
+  // shared: 1 when the item reads a block that another planned row also
+  // reads, 2 for a packed prefix item (DecodePlanHost::num_packed)
   int32_t item, start, end, nsplit, tbl_off, blk0, shared, split;
 };
 // Decode work plan: items in longest-first order; built on the host from the
@@ -65,6 +66,17 @@ struct DecodePlanHost {
   // Some blocks are shared but some work items read none of them: those
   // items stream, the others keep cached loads (DecodeWork::shared).
   bool mixed_kv = false;
+  // Packed items (DecodeWork::shared == 2, num_packed of them): a piece of a
+  // prefix that up to pack_r rows share (identical leading block ids),
+  // attended for all of them at once -- their query heads fill the query
+  // columns of one MFMA wave, so the prefix is read once per pack instead of
+  // once per row.  Entry item = pack * hkv + kv_head; the pack's rows are
+  // pack_rows[pack * pack_r .. + pack_r) (-1: unused).  Their prefix pieces
+  // are splits 0 .. np-1 of each of those rows; the rows' remaining context
+  // follows as ordinary items with splits np ...
+  int num_packed = 0;
+  int pack_r = 0;
+  std::vector<int32_t> pack_rows;
 };
 struct DecodePlanDev {
   const DecodeWork* work = nullptr;
@@ -78,12 +90,22 @@ struct DecodePlanDev {
   int num_rows = 0;
   bool stream_kv = true;  // DecodePlanHost::stream_kv
   bool mixed_kv = false;  // DecodePlanHost::mixed_kv
+  // packed prefix items (DecodePlanHost::num_packed, counted in num_work),
+  // DecodePlanHost::pack_rows on the device, and rows per pack
+  int num_packed = 0;
+  const int32_t* pack_rows = nullptr;
+  int pack_r = 0;
 };
+// pack_r: rows per packed prefix item; 0 packs nothing.  The decode kernels
+// take packed items only on bf16 arenas at head_dim 64/128 with
+// pack_r = 16 / (query heads per KV head) >= 2 (decode_pack_rows).
 void build_decode_plan(const uint32_t* positions, const int32_t* row_seq,
                        const int64_t* bt_offsets, const uint32_t* bt_ids, int64_t rows,
                        int64_t hkv, int64_t block_size, int64_t wave_slots,
-                       const uint8_t* skip_rows, DecodePlanHost* plan);
+                       const uint8_t* skip_rows, DecodePlanHost* plan, int pack_r = 0);
 size_t decode_workspace_bytes(int64_t rows, int64_t hq, int64_t D, int64_t max_splits);
+// Rows per packed prefix item for this arena and grouping (0: no packing).
+int decode_pack_rows(const KvGeom& kv, int64_t hq);
 // Which launches of a decode pass to issue (the merge only runs when the
 // plan splits some row).
 enum class DecodePhase { kBoth, kSplit, kMerge };

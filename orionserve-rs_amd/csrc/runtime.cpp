@@ -181,24 +181,37 @@ struct orion_hip_device {
 struct orion_hip_decode_plan {
   orion_hip_device* dev = nullptr;
   int64_t rows = 0, hq = 0, hkv = 0, head_dim = 0, block_size = 0;
-  DecodePlanHost host;
-  DevBuf work, ws;
+  // host: the plan as built for a bf16 arena (shared prefixes packed where
+  // the MFMA wave takes them); plain: the same rows without packing, built
+  // only when host packs something (an f32 arena takes it).  Each device
+  // buffer holds the work items, the pieces per row, then the pack rows.
+  DecodePlanHost host, plain;
+  DevBuf work, work_plain, ws;
   ~orion_hip_decode_plan() {
     work.release();
+    work_plain.release();
     ws.release();
   }
-  DecodePlanDev view() const {
+  static DecodePlanDev view_of(const DecodePlanHost& h, const DevBuf& b) {
     DecodePlanDev d;
-    d.work = work.as<const DecodeWork>();
-    d.row_nsplit = reinterpret_cast<const int32_t*>(
-        work.as<const char>() + host.work.size() * sizeof(DecodeWork));
-    d.num_work = (int)host.work.size();
-    d.chunk = host.chunk;
-    d.max_splits = host.max_splits;
+    d.work = b.as<const DecodeWork>();
+    const char* base = b.as<const char>();
+    d.row_nsplit = reinterpret_cast<const int32_t*>(base + h.work.size() * sizeof(DecodeWork));
+    d.num_work = (int)h.work.size();
+    d.chunk = h.chunk;
+    d.max_splits = h.max_splits;
+    d.stream_kv = h.stream_kv;
+    d.mixed_kv = h.mixed_kv;
+    d.num_packed = h.num_packed;
+    d.pack_rows = reinterpret_cast<const int32_t*>(base + h.work.size() * sizeof(DecodeWork) +
+                                                   h.row_nsplit.size() * sizeof(int32_t));
+    d.pack_r = h.pack_r;
+    return d;
+  }
+  DecodePlanDev view(bool bf16) const {
+    DecodePlanDev d = (!bf16 && host.num_packed) ? view_of(plain, work_plain) : view_of(host, work);
     d.ws = ws.as<float>();
     d.ws_bytes = ws.bytes;
-    d.stream_kv = host.stream_kv;
-    d.mixed_kv = host.mixed_kv;
     return d;
   }
 };
@@ -1457,7 +1470,7 @@ ORION_EXPORT int orion_hip_model_forward(orion_hip_model* m, const orion_hip_bat
   DecodePlanHost plan;
   build_decode_plan(b->positions, hb.row_seq.data(), b->block_table_offsets, b->block_table_ids, n,
                     d.num_kv_heads, d.block_size, m->dev->wave_slots,
-                    npf ? skip.data() : nullptr, &plan);
+                    npf ? skip.data() : nullptr, &plan, decode_pack_rows(m->kv, Hq));
   // One workspace for the decode splits and the prefill key parts (their
   // launches are ordered on the stream: the decode merge has read the splits
   // before the prefill kernel writes its parts).
@@ -1481,7 +1494,8 @@ ORION_EXPORT int orion_hip_model_forward(orion_hip_model* m, const orion_hip_bat
   const size_t o_pforder = (o_drows + plan.rows.size() * 4 + 7) & ~(size_t)7;
   const size_t o_pfsplit = o_pforder + pf_order.size() * sizeof(PrefillTile);
   const size_t o_pfparts = o_pfsplit + (pf_split ? pfp.split_rows.size() * 4 : 0);
-  const size_t total = o_pfparts + (pf_split ? pfp.row_parts.size() * 4 : 0);
+  const size_t o_packrows = o_pfparts + (pf_split ? pfp.row_parts.size() * 4 : 0);
+  const size_t total = o_packrows + plan.pack_rows.size() * 4;
   if (total > m->pinned_bytes) {
     if (m->pinned) {
       HIP_TRY(st, hipStreamSynchronize(stream));
@@ -1513,6 +1527,7 @@ ORION_EXPORT int orion_hip_model_forward(orion_hip_model* m, const orion_hip_bat
     std::memcpy(hp + o_pfsplit, pfp.split_rows.data(), pfp.split_rows.size() * 4);
     std::memcpy(hp + o_pfparts, pfp.row_parts.data(), pfp.row_parts.size() * 4);
   }
+  std::memcpy(hp + o_packrows, plan.pack_rows.data(), plan.pack_rows.size() * 4);
   char* dp = m->b_tokens.as<char>();
   HIP_TRY(st, hipMemcpyAsync(dp, hp, total, hipMemcpyHostToDevice, stream));
   const uint32_t* d_tok = reinterpret_cast<const uint32_t*>(dp + o_tok);
@@ -1531,6 +1546,9 @@ ORION_EXPORT int orion_hip_model_forward(orion_hip_model* m, const orion_hip_bat
   dplan.ws_bytes = m->ws.bytes;
   dplan.stream_kv = plan.stream_kv;
   dplan.mixed_kv = plan.mixed_kv;
+  dplan.num_packed = plan.num_packed;
+  dplan.pack_rows = reinterpret_cast<const int32_t*>(dp + o_packrows);
+  dplan.pack_r = plan.pack_r;
   if (npf) {
     dplan.rows = reinterpret_cast<const int32_t*>(dp + o_drows);
     dplan.num_rows = (int)plan.rows.size();
@@ -1692,20 +1710,36 @@ ORION_EXPORT int orion_hip_decode_plan_create(orion_hip_device* dev, const uint3
       return internal(st, "row %lld: position %u has no block in its table", (long long)i,
                       positions[i]);
   }
+  // packing applies to bf16 arenas at head_dim 64/128 (the plan does not know
+  // the arena's dtype yet: an f32 arena takes the unpacked copy)
+  const KvGeom bf16_geom{1, 1, block_size, num_kv_heads, head_dim, true};
+  const int pack_r = decode_pack_rows(bf16_geom, num_q_heads);
   build_decode_plan(positions, row_seq, block_table_offsets, block_table_ids, num_rows,
-                    num_kv_heads, block_size, dev->wave_slots, nullptr, &p->host);
-  // work items, then the pieces per row, in one buffer
-  const size_t wbytes = p->host.work.size() * sizeof(DecodeWork);
-  const size_t nbytes = p->host.row_nsplit.size() * sizeof(int32_t);
-  HIP_TRY(st, p->work.reserve(wbytes + nbytes));
-  std::vector<char> staged(wbytes + nbytes);
-  std::memcpy(staged.data(), p->host.work.data(), wbytes);
-  std::memcpy(staged.data() + wbytes, p->host.row_nsplit.data(), nbytes);
-  if (!staged.empty())
-    HIP_TRY(st, hipMemcpyAsync(p->work.ptr, staged.data(), staged.size(), hipMemcpyHostToDevice,
-                               dev->stream));
-  HIP_TRY(st, p->ws.reserve(
-                  decode_workspace_bytes(num_rows, num_q_heads, head_dim, p->host.max_splits)));
+                    num_kv_heads, block_size, dev->wave_slots, nullptr, &p->host, pack_r);
+  if (p->host.num_packed)
+    build_decode_plan(positions, row_seq, block_table_offsets, block_table_ids, num_rows,
+                      num_kv_heads, block_size, dev->wave_slots, nullptr, &p->plain, 0);
+  // work items, then the pieces per row, then the pack rows, in one buffer
+  auto upload = [&](const DecodePlanHost& h, DevBuf& buf) -> hipError_t {
+    const size_t wbytes = h.work.size() * sizeof(DecodeWork);
+    const size_t nbytes = h.row_nsplit.size() * sizeof(int32_t);
+    const size_t pbytes = h.pack_rows.size() * sizeof(int32_t);
+    hipError_t e = buf.reserve(wbytes + nbytes + pbytes);
+    if (e != hipSuccess) return e;
+    std::vector<char> staged(wbytes + nbytes + pbytes);
+    std::memcpy(staged.data(), h.work.data(), wbytes);
+    std::memcpy(staged.data() + wbytes, h.row_nsplit.data(), nbytes);
+    std::memcpy(staged.data() + wbytes + nbytes, h.pack_rows.data(), pbytes);
+    if (staged.empty()) return hipSuccess;
+    e = hipMemcpyAsync(buf.ptr, staged.data(), staged.size(), hipMemcpyHostToDevice, dev->stream);
+    if (e != hipSuccess) return e;
+    return hipStreamSynchronize(dev->stream);  // staged is freed on return
+  };
+  HIP_TRY(st, upload(p->host, p->work));
+  if (p->host.num_packed) HIP_TRY(st, upload(p->plain, p->work_plain));
+  HIP_TRY(st, p->ws.reserve(decode_workspace_bytes(
+                  num_rows, num_q_heads, head_dim,
+                  std::max(p->host.max_splits, p->plain.max_splits))));
   HIP_TRY(st, hipStreamSynchronize(dev->stream));
   *out = p.release();
   return ORION_HIP_OK;
@@ -1716,6 +1750,13 @@ ORION_EXPORT void orion_hip_decode_plan_destroy(orion_hip_decode_plan* plan) {
   (void)hipSetDevice(plan->dev->ordinal);
   (void)hipStreamSynchronize(plan->dev->stream);
   delete plan;
+}
+
+ORION_EXPORT int orion_hip_decode_plan_packed(const orion_hip_decode_plan* plan,
+                                              int64_t* packed_items, int64_t* rows_per_pack) {
+  *packed_items = plan->host.num_packed;
+  *rows_per_pack = plan->host.num_packed ? plan->host.pack_r : 0;
+  return ORION_HIP_OK;
 }
 
 ORION_EXPORT int orion_hip_decode_plan_info(const orion_hip_decode_plan* plan, int64_t* chunk,
@@ -1747,12 +1788,12 @@ ORION_EXPORT int orion_hip_paged_attention_decode(
   HIP_TRY(st, hipSetDevice(dev->ordinal));
   if (!dev->ktiming) {
     HIP_TRY(st, launch_paged_decode(dev->stream, g, d_arena, layer, d_q, num_rows, num_q_heads,
-                                    d_positions, d_row_seq, d_bt_offsets, d_bt_ids, plan->view(),
+                                    d_positions, d_row_seq, d_bt_offsets, d_bt_ids, plan->view(g.dtype_bf16),
                                     d_out));
     return ORION_HIP_OK;
   }
   // Timed: the split-K kernel and the merge kernel as separate launches.
-  DecodePlanDev pv = plan->view();
+  DecodePlanDev pv = plan->view(g.dtype_bf16);
   HIP_TRY(st, timed_launch(dev, 0, [&] {
             return launch_paged_decode(dev->stream, g, d_arena, layer, d_q, num_rows, num_q_heads,
                                        d_positions, d_row_seq, d_bt_offsets, d_bt_ids, pv, d_out,

@@ -49,7 +49,8 @@ EXPORTED = [
     "orion_hip_model_load_checkpoint", "orion_hip_sample", "orion_hip_model_sample",
     "orion_hip_model_download_weight", "orion_hip_model_forward", "orion_hip_model_kv_read",
     "orion_hip_model_kv_write", "orion_hip_model_kv_arena", "orion_hip_model_kv_layout", "orion_hip_decode_plan_create",
-    "orion_hip_decode_plan_destroy", "orion_hip_decode_plan_info", "orion_hip_paged_attention_decode",
+    "orion_hip_decode_plan_destroy", "orion_hip_decode_plan_info",
+    "orion_hip_decode_plan_packed", "orion_hip_paged_attention_decode",
     "orion_hip_paged_attention_prefill", "orion_hip_rope_and_cache", "orion_hip_rmsnorm",
     "orion_hip_gemm", "orion_hip_gemm_noalloc", "orion_hip_silu_mul", "orion_hip_argmax",
 ]
@@ -174,6 +175,7 @@ def load_library(path: str = LIB_PATH) -> C.CDLL:
                                          C.c_int),
         "orion_hip_decode_plan_destroy": ([vp], None),
         "orion_hip_decode_plan_info": ([vp, P(i64), P(i64), P(i64)], C.c_int),
+        "orion_hip_decode_plan_packed": ([vp, P(i64), P(i64)], C.c_int),
         "orion_hip_paged_attention_decode": (
             [vp, P(KvLayout), vp, i64, vp, i64, i64, vp, vp, vp, vp, vp, vp], C.c_int),
         "orion_hip_paged_attention_prefill": (
@@ -735,7 +737,10 @@ class DecodePlan:
         c, n, m = C.c_int64(), C.c_int64(), C.c_int64()
         _check(self.be.lib.orion_hip_decode_plan_info(self.handle, C.byref(c), C.byref(n),
                                                       C.byref(m)))
-        return {"chunk": c.value, "num_work": n.value, "max_splits": m.value}
+        p, r = C.c_int64(), C.c_int64()
+        _check(self.be.lib.orion_hip_decode_plan_packed(self.handle, C.byref(p), C.byref(r)))
+        return {"chunk": c.value, "num_work": n.value, "max_splits": m.value,
+                "packed_items": p.value, "rows_per_pack": r.value}
 
     def close(self) -> None:
         if self.handle:

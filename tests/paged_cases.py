@@ -56,6 +56,19 @@ class PagedCase:
         self.arena_f32 = arena  # exact values the device holds, widened to f32
         self.row_seq = np.arange(self.S, dtype=np.int32)
 
+    def share_prefixes(self, groups):
+        """Prefix sharing: for each (rows, nblocks) in `groups`, the first
+        `nblocks` table entries of every listed row become those of the
+        group's first row (identical leading block ids, as prefix caching
+        produces).  Each row must hold at least that many blocks."""
+        for rows, nb in groups:
+            lead = self.tables[rows[0]][:nb].copy()
+            for r in rows[1:]:
+                assert len(self.tables[r]) >= nb
+                self.tables[r] = np.concatenate([lead, self.tables[r][nb:]]).astype(np.uint32)
+        self.bt_ids = np.concatenate(self.tables)
+        return self
+
     def dims(self):
         return (1, self.num_blocks, self.bs, self.hkv, self.d)
 

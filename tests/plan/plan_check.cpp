@@ -26,6 +26,7 @@ int main(int argc, char** argv) {
   const int trials = argc > 1 ? atoi(argv[1]) : 2000;
   std::mt19937 rng(20261202);
   int fails = 0, balanced = 0;
+  long packed_items = 0;
   auto fail = [&](int trial, const char* what, int row) {
     if (fails++ < 20) printf("trial %d: %s (row %d)\n", trial, what, row);
   };
@@ -41,35 +42,70 @@ int main(int argc, char** argv) {
     std::vector<uint32_t> ids;
     // every seventh trial: rows start with the leading blocks of row 0 (a
     // shared prefix, as prefix caching produces)
-    const bool prefix = trial % 7 == 3;
+    // (every third trial of those: deep prefixes of up to 64 blocks, which
+    // the packing planner groups)
+    const bool prefix = trial % 7 == 3 || trial % 11 == 5;
+    const int64_t share = trial % 11 == 5 ? 1 + rng() % 64 : 8;
     for (int r = 0; r < rows; ++r) {
       pos[r] = rng() % maxctx;
       row_seq[r] = r;
       const int nb = (int)pos[r] / bs + 1;
       for (int j = 0; j < nb; ++j)
-        ids.push_back(prefix && r > 0 && j < std::min<int64_t>(8, off[1]) ? ids[j]
-                                                                          : rng() % 100000);
+        ids.push_back(prefix && r > 0 && j < std::min<int64_t>(share, off[1]) ? ids[j]
+                                                                              : rng() % 100000);
       off[r + 1] = off[r] + nb;
     }
+    const int G = 1 + rng() % 8;
+    const int pack_r = (trial % 2) ? 16 / G : 0;
     std::vector<uint8_t> skip(rows, 0);
     const bool use_skip = trial % 5 == 0;
     if (use_skip)
       for (int r = 0; r < rows; ++r) skip[r] = rng() % 3 == 0;
     DecodePlanHost plan;
     orion::build_decode_plan(pos.data(), row_seq.data(), off.data(), ids.data(), rows, hkv, bs,
-                             slots, use_skip ? skip.data() : nullptr, &plan);
+                             slots, use_skip ? skip.data() : nullptr, &plan, pack_r);
     balanced += plan.balanced;
+    packed_items += plan.num_packed;
     int bs_log2 = 0;
     while ((1 << bs_log2) < bs) ++bs_log2;
     std::map<int, std::vector<std::pair<int, int>>> cover;  // item -> [start, end)
     std::map<std::pair<int, int>, int> seen_split;
+    std::vector<int> in_pack(rows, 0);
+    int counted_packed = 0;
     for (const DecodeWork& w : plan.work) {
+      const int nblk = ((w.end - 1) >> bs_log2) - (w.start >> bs_log2) + 1;
+      if (w.shared == 2) {  // packed: one piece of every row of the pack
+        ++counted_packed;
+        const int pk = w.item / hkv, h = w.item % hkv;
+        if (pack_r < 2 || pk < 0 || (size_t)(pk + 1) * pack_r > plan.pack_rows.size()) {
+          fail(trial, "packed item without a pack", pk);
+          continue;
+        }
+        if (w.start % 16 || w.end <= w.start || nblk > 64) fail(trial, "bad packed bounds", pk);
+        if (w.nsplit < 2) fail(trial, "packed item finishes in place", pk);
+        int members = 0;
+        for (int j = 0; j < pack_r; ++j) {
+          const int r = plan.pack_rows[pk * pack_r + j];
+          if (r < 0) continue;
+          ++members;
+          in_pack[r] = 1;
+          if ((int)w.end > (int)pos[r]) fail(trial, "packed piece reaches a row's position", r);
+          for (int b = 0; b < nblk; ++b)
+            if (ids[w.tbl_off + b] != ids[off[r] + (w.start >> bs_log2) + b])
+              fail(trial, "packed row does not share the piece's blocks", r);
+          if (w.split < 0 || w.split >= plan.row_nsplit[r]) fail(trial, "bad packed split", r);
+          if (seen_split[{r * hkv + h, w.split}]++) fail(trial, "split index repeated", r);
+          cover[r * hkv + h].push_back({w.start, w.end});
+        }
+        if (members < 2) fail(trial, "pack of fewer than two rows", pk);
+        if ((uint32_t)w.blk0 != ids[w.tbl_off]) fail(trial, "bad packed blk0", pk);
+        continue;
+      }
       const int row = w.item / hkv;
       if (row < 0 || row >= rows) {
         fail(trial, "row out of range", row);
         continue;
       }
-      const int nblk = ((w.end - 1) >> bs_log2) - (w.start >> bs_log2) + 1;
       if (w.start % 16 || w.end <= w.start || nblk > 64) fail(trial, "bad piece bounds", row);
       if (w.tbl_off != off[row] + (w.start >> bs_log2) || (uint32_t)w.blk0 != ids[w.tbl_off])
         fail(trial, "bad table slice", row);
@@ -79,6 +115,8 @@ int main(int argc, char** argv) {
       if (seen_split[{w.item, w.split}]++) fail(trial, "split index repeated", row);
       cover[w.item].push_back({w.start, w.end});
     }
+    if (counted_packed != plan.num_packed) fail(trial, "num_packed", counted_packed);
+    if (pack_r < 2 && plan.num_packed) fail(trial, "packed without pack_r", -1);
     for (int r = 0; r < rows; ++r) {
       const bool planned = !(use_skip && skip[r]);
       if (!planned && plan.row_nsplit[r] != 0) fail(trial, "skipped row has pieces", r);
@@ -105,7 +143,7 @@ int main(int argc, char** argv) {
         }
         if (at != (int)pos[r] + 1) fail(trial, "context not covered", r);
         if ((int)v.size() != plan.row_nsplit[r]) fail(trial, "row_nsplit mismatch", r);
-        if (v.size() > 1 && (lo != hi || v.back().second - v.back().first > hi))
+        if (!in_pack[r] && v.size() > 1 && (lo != hi || v.back().second - v.back().first > hi))
           fail(trial, "uneven pieces", r);
       }
     }
@@ -120,6 +158,7 @@ int main(int argc, char** argv) {
     }
     bool any_shared = false, any_private = false;
     for (const DecodeWork& w : plan.work) {
+      if (w.shared == 2) continue;
       const int nblk = ((w.end - 1) >> bs_log2) - (w.start >> bs_log2) + 1;
       bool sh = false;
       for (int j = 0; j < nblk; ++j) sh = sh || uses[ids[w.tbl_off + j]] > 1;
@@ -132,6 +171,7 @@ int main(int argc, char** argv) {
     if (plan.stream_kv != !any_shared_block) fail(trial, "stream_kv", -1);
     if (plan.mixed_kv != (any_shared_block && any_private)) fail(trial, "mixed_kv", -1);
   }
-  printf("%d trials, %d balanced, %d failures\n", trials, balanced, fails);
+  printf("%d trials, %d balanced, %ld packed items, %d failures\n", trials, balanced,
+         packed_items, fails);
   return fails ? 1 : 0;
 }

@@ -32,3 +32,4 @@ def test_decode_plans_cover_every_context_once(plan_check, balance):
     trials, nbal = p.stdout.split()[0], int(p.stdout.split()[2])
     assert trials == "2000"
     assert (nbal > 0) == (balance == "1")
+    assert int(p.stdout.split()[4]) > 0  # packed prefix items were planned and checked

@@ -121,6 +121,60 @@ def test_any_head_dim_and_group(backend, hq, hkv, d, bs, dtype):
     assert mm == 0, (ma, mr, wi)
 
 
+def shared_prefix_case(seed, hq, hkv, d, bs):
+    # 40 rows: rows 0-19 share 1,024 tokens; rows 20-26 share 320; rows
+    # 30-35 share 640 with row 30 except row 33, which shares 288 (a pack's
+    # prefix is what all its rows share); rows 36-39 share 2 blocks (too
+    # short to pack); the rest are private.
+    rng = np.random.default_rng(seed)
+    ctxs = rng.integers(1100, 3000, 40)
+    case = PagedCase(seed, ctxs, hq, hkv, d, bs, dtype="bf16")
+    tok = lambda n: -(-n // bs)
+    return case.share_prefixes([(list(range(20)), tok(1024)), (list(range(20, 27)), tok(320)),
+                                ([30, 31, 32, 34, 35], tok(640)), ([30, 33], tok(288)),
+                                ([36, 37, 38, 39], 2)])
+
+
+@pytest.mark.parametrize("hq,hkv,d,bs", [(28, 4, 128, 16), (32, 8, 128, 16), (8, 8, 64, 16),
+                                         (16, 4, 64, 16), (16, 2, 128, 32), (12, 4, 64, 8)])
+def test_packed_shared_prefixes(backend, monkeypatch, hq, hkv, d, bs):
+    # Rows whose tables start with the same block ids attend that prefix
+    # together: up to 16 / G rows' query heads fill one MFMA wave's query
+    # columns, and the prefix pieces are splits of every row of the pack.
+    # Against the oracle, and against the same plan without packing
+    # (ORION_DECODE_PACK=0), which plans no packed item.
+    case = shared_prefix_case(hq + d + bs, hq, hkv, d, bs)
+    args = (case.positions, case.row_seq, case.bt_offsets, case.bt_ids, hq, hkv, d, bs)
+    items = oh.DecodePlan(backend, *args)
+    info = items.info()
+    items.close()
+    got = run_decode(backend, case)
+    monkeypatch.setenv("ORION_DECODE_PACK", "0")
+    items = oh.DecodePlan(backend, *args)
+    info_plain = items.info()
+    items.close()
+    plain = run_decode(backend, case)
+    monkeypatch.delenv("ORION_DECODE_PACK")
+    want = case.oracle()
+    err, diff = float(np.abs(got - want).max()), float(np.abs(got - plain).max())
+    print(f"[packed prefixes] G={hq // hkv} {info['packed_items']} packed items of "
+          f"{info['num_work']} ({info['rows_per_pack']} rows each), unpacked plan "
+          f"{info_plain['num_work']} items; err {err:.2e}, vs unpacked {diff:.2e}", flush=True)
+    assert info["packed_items"] > 0 and info["rows_per_pack"] == 16 // (hq // hkv)
+    assert info_plain["packed_items"] == 0
+    assert err <= 1e-4 and float(np.abs(plain - want).max()) <= 1e-4
+    assert diff <= 2e-5
+
+
+def test_packed_plan_on_an_f32_arena_takes_the_unpacked_copy(backend):
+    # The plan is built before the arena's dtype is known; an f32 arena (VALU
+    # waves, no packed items) runs the unpacked copy of the same plan.
+    case = shared_prefix_case(3, 28, 4, 128, 16)
+    case.dtype = "f32"
+    got = run_decode(backend, case)
+    assert float(np.abs(got - case.oracle()).max()) <= 1e-4
+
+
 def test_ragged_positions_and_shared_sequences(backend):
     # Several query rows per sequence at arbitrary positions (what a chunked
     # prefill batch looks like to the decode kernel) and sequences sharing
