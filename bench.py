@@ -584,6 +584,9 @@ def main():
     ap.add_argument("--no-mixed", action="store_true", help="skip the config-5 mixed batch")
     ap.add_argument("--no-gemm", action="store_true", help="skip the GEMM shape timings")
     ap.add_argument("--no-sampling", action="store_true", help="skip the device sampler timing")
+    ap.add_argument("--e2e-steps", type=int, default=64,
+                    help="greedy decode steps of the config-4 run (64 as benchmarked; fewer for "
+                         "profiling its prefill forward; the golden comparison needs 64)")
     ap.add_argument("--kv-layout", choices=["head-major", "reference"], default="reference",
                     help="block-internal order of the KV arena (reference = attention.rs order)")
     ap.add_argument("--copy-calibration", action="store_true",
@@ -721,7 +724,7 @@ def main():
         result["copy_calibration_bytes"] = 1 << 30
     be.close()
     if not a.no_e2e:
-        result["decode_e2e"] = decode_e2e(cpu=not a.no_cpu)
+        result["decode_e2e"] = decode_e2e(steps=a.e2e_steps, cpu=not a.no_cpu)
     if not a.no_mixed:
         result["mixed_cfg5"] = mixed_cfg5()
     if not a.no_gemm:

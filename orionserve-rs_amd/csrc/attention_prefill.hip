@@ -466,12 +466,28 @@ __global__ void __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu
     } else if (p < P) {
       const int r = p / G;
       const float inv = 1.0f / lsum[rt][0];
-      float* op = out + ((rs + r) * num_q_heads + (int64_t)kvh * G + (p - r * G)) * D + 4 * grp;
+      const int64_t head = (rs + r) * num_q_heads + (int64_t)kvh * G + (p - r * G);
+      if (split.out_hilo) {
+        // the O GEMM's split operand layout: per 8 dims [8 hi bf16 | 8 lo bf16];
+        // this lane's 4 dims are half grp & 1 of group 2d + grp / 2
+        uint2* hb = reinterpret_cast<uint2*>(out + head * D) + (grp >> 1) * 4 + (grp & 1);
 #pragma unroll
-      for (int d = 0; d < DT; ++d)
-        *reinterpret_cast<float4*>(op + 16 * d) =
-            make_float4(o[rt][d][0] * inv, o[rt][d][1] * inv, o[rt][d][2] * inv,
-                        o[rt][d][3] * inv);
+        for (int d = 0; d < DT; ++d) {
+          uint16_t h[4], l[4];
+#pragma unroll
+          for (int i = 0; i < 4; ++i) split1_trunc(o[rt][d][i] * inv, h[i], l[i]);
+          hb[8 * d] = make_uint2(h[0] | ((uint32_t)h[1] << 16), h[2] | ((uint32_t)h[3] << 16));
+          hb[8 * d + 2] =
+              make_uint2(l[0] | ((uint32_t)l[1] << 16), l[2] | ((uint32_t)l[3] << 16));
+        }
+      } else {
+        float* op = out + head * D + 4 * grp;
+#pragma unroll
+        for (int d = 0; d < DT; ++d)
+          *reinterpret_cast<float4*>(op + 16 * d) =
+              make_float4(o[rt][d][0] * inv, o[rt][d][1] * inv, o[rt][d][2] * inv,
+                          o[rt][d][3] * inv);
+      }
     }
   }
 }

@@ -101,6 +101,17 @@ __device__ inline void split2_trunc(float x0, float x1, uint32_t& hi, uint32_t& 
   lo = __builtin_amdgcn_perm(__float_as_uint(r1), __float_as_uint(r0), 0x07060302u);
 }
 
+// split2_trunc for one value: hi = the top 16 bits of x, lo = the top 16
+// bits of x - hi (exact in f32).  The subtraction must not contract with a
+// product that computed x (fma(a, b, -hi) gives the remainder of the exact
+// product, not of the rounded value an f32 store holds), hence the pragma.
+__device__ inline void split1_trunc(float x, uint16_t& hi, uint16_t& lo) {
+#pragma clang fp contract(off)
+  const uint32_t b = __float_as_uint(x);
+  hi = (uint16_t)(b >> 16);
+  lo = (uint16_t)(__float_as_uint(x - __uint_as_float(b & 0xffff0000u)) >> 16);
+}
+
 // Split an f32 into hi + lo bf16 terms: hi = rne(x), lo = rne(x - hi).
 // x - hi is exact in f32, so hi + lo carries ~16 significant bits of x.
 __device__ inline void split_bf16(float x, uint16_t& hi, uint16_t& lo) {

@@ -51,7 +51,7 @@ hipError_t launch_embed(hipStream_t st, const uint32_t* tokens, int64_t n, const
 __global__ void __launch_bounds__(256)
     rmsnorm_kernel(const float* __restrict__ x, const int32_t* __restrict__ row_index,
                    const float* __restrict__ weight, int64_t cols, float eps,
-                   float* __restrict__ out) {
+                   float* __restrict__ out, bool hilo) {
 #pragma clang fp contract(off)
   __shared__ double part[4];
   const int64_t orow = blockIdx.x;
@@ -89,8 +89,21 @@ __global__ void __launch_bounds__(256)
       const int i = (int)threadIdx.x + 256 * j;
       if (i < n4) {
         const float4 w = w4[i];
-        o4[i] = make_float4(v[j].x * scale * w.x, v[j].y * scale * w.y, v[j].z * scale * w.z,
-                            v[j].w * scale * w.w);
+        const float4 y = make_float4(v[j].x * scale * w.x, v[j].y * scale * w.y,
+                                     v[j].z * scale * w.z, v[j].w * scale * w.w);
+        if (hilo) {
+          // float4 i is half i & 1 of group i >> 1: its 4 hi and 4 lo values
+          uint16_t h[4], l[4];
+          split1_trunc(y.x, h[0], l[0]);
+          split1_trunc(y.y, h[1], l[1]);
+          split1_trunc(y.z, h[2], l[2]);
+          split1_trunc(y.w, h[3], l[3]);
+          uint2* g = reinterpret_cast<uint2*>(orow_p) + (i >> 1) * 4 + (i & 1);
+          g[0] = make_uint2(h[0] | ((uint32_t)h[1] << 16), h[2] | ((uint32_t)h[3] << 16));
+          g[2] = make_uint2(l[0] | ((uint32_t)l[1] << 16), l[2] | ((uint32_t)l[3] << 16));
+        } else {
+          o4[i] = y;
+        }
       }
     }
     return;
@@ -105,14 +118,26 @@ __global__ void __launch_bounds__(256)
   __syncthreads();
   const double total = part[0] + part[1] + part[2] + part[3];
   const float scale = (float)(1.0 / sqrt(total / (double)cols + (double)eps));
+  if (hilo) {
+    uint16_t* o16 = reinterpret_cast<uint16_t*>(orow_p);
+    for (int64_t i = threadIdx.x; i < cols; i += 256) {
+      uint16_t h, l;
+      split1_trunc(xr[i] * scale * weight[i], h, l);
+      o16[(i >> 3) * 16 + (i & 7)] = h;
+      o16[(i >> 3) * 16 + 8 + (i & 7)] = l;
+    }
+    return;
+  }
   for (int64_t i = threadIdx.x; i < cols; i += 256) orow_p[i] = xr[i] * scale * weight[i];
 }
 
 hipError_t launch_rmsnorm(hipStream_t st, const float* x, const int32_t* row_index,
-                          const float* weight, int64_t rows, int64_t cols, float eps, float* out) {
+                          const float* weight, int64_t rows, int64_t cols, float eps, float* out,
+                          bool hilo) {
   if (rows == 0) return hipSuccess;
+  if (hilo && cols % 8) return hipErrorInvalidValue;
   hipLaunchKernelGGL(rmsnorm_kernel, dim3((unsigned)rows), dim3(256), 0, st, x, row_index, weight,
-                     cols, eps, out);
+                     cols, eps, out, hilo);
   return hipGetLastError();
 }
 

@@ -215,13 +215,17 @@ struct PackedGeom {
 
 // HILO: x carried as a truncated hi + lo bf16 pair (two MFMAs, ~16 bits of
 // x per product); otherwise rounded to bf16 (nearest even, one MFMA).
+// XS (with HILO): x is already in that split layout (GemmFuse::x_hilo), so a
+// fragment's two 16-byte LDS chunks are its hi and lo bf16x8 as they are.
 // NTW: 16-column tiles per wave (4: 128-column workgroup tiles; 8: 256).
-template <bool HILO, int NTW>
+// out_hilo: the SwiGLU epilogue writes its output in the split layout.
+template <bool HILO, int NTW, bool XS = false>
 __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(NTW == 8 ? 2 : 1)))
     gemm_tiled_kernel(const float* __restrict__ x, const uint16_t* __restrict__ w,
                       const float* __restrict__ bias, int M, int N, int K, int ep,
                       float* __restrict__ out, PackedGeom pk, int gm, int kspan,
-                      float* __restrict__ partial) {
+                      float* __restrict__ partial, bool out_hilo) {
+  static_assert(HILO || !XS, "a pre-split x needs the hi/lo MFMAs");
   constexpr int TN = 32 * NTW;   // workgroup columns
   constexpr int BJ = NTW / 2;    // B copies (1 KiB each) per wave per k-step
   __shared__ __attribute__((aligned(1024))) float As[2][kTM * kTK];
@@ -347,7 +351,11 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(NTW ==
                           __uint_as_float(hi4.x), __uint_as_float(hi4.y),
                           __uint_as_float(hi4.z), __uint_as_float(hi4.w)};
       bf16x8 ahi, alo;
-      if constexpr (HILO) {
+      if constexpr (XS) {
+        ahi = __builtin_bit_cast(bf16x8, lo4);
+        alo = __builtin_bit_cast(bf16x8, hi4);
+        (void)a;
+      } else if constexpr (HILO) {
         split8(a, ahi, alo);
       } else {
         typedef __bf16 bf16x8v __attribute__((ext_vector_type(8)));
@@ -398,7 +406,16 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(NTW ==
           const float u = __shfl_xor(v, 8);
           if (l16 < 8 && row < M && col < N) {
             const float act = v / (1.0f + __expf(-v)) * u;
-            out[(int64_t)row * (N >> 1) + ((n0 + wn * 16 * NTW + nt * 16) >> 1) + l16] = act;
+            const int c8 = (n0 + wn * 16 * NTW + nt * 16) >> 1;  // a multiple of 8
+            if (out_hilo) {
+              uint16_t h, lo;
+              split1_trunc(act, h, lo);
+              uint16_t* o16 = reinterpret_cast<uint16_t*>(out) + (int64_t)row * N + c8 * 2;
+              o16[l16] = h;
+              o16[8 + l16] = lo;
+            } else {
+              out[(int64_t)row * (N >> 1) + c8 + l16] = act;
+            }
           }
         } else if (row < M && col < N) {
           float* op = out + (int64_t)row * N + col;
@@ -1009,6 +1026,9 @@ hipError_t launch_gemm(hipStream_t st, const float* x, const uint16_t* w, const 
     const char* e = getenv("ORION_GEMM_TILED_MIN_M");
     return e ? (int64_t)atoll(e) : (int64_t)256;
   }();
+  // split-layout activations exist only for the LDS-tiled kernel
+  if ((f.x_hilo || f.out_hilo) && (M <= 64 || (M < tiled_min_m && !f.w_packed)))
+    return hipErrorInvalidValue;
   // Decode-shaped M: split-K weight streaming (needs the scratch when K spans
   // several slices).
   if (M <= 64 && N <= INT32_MAX && K <= INT32_MAX) {
@@ -1087,10 +1107,13 @@ hipError_t launch_gemm(hipStream_t st, const float* x, const uint16_t* w, const 
     // fragment) instead of the hi/lo pair (measurement knob, read per call).
     const char* act = getenv("ORION_GEMM_ACT");
     const bool hilo = !(act && act[0] == 'b');
-    auto kern = wide ? (hilo ? gemm_tiled_kernel<true, 8> : gemm_tiled_kernel<false, 8>)
-                     : (hilo ? gemm_tiled_kernel<true, 4> : gemm_tiled_kernel<false, 4>);
+    if (f.x_hilo && !hilo) return hipErrorInvalidValue;
+    auto kern = f.x_hilo ? (wide ? gemm_tiled_kernel<true, 8, true> : gemm_tiled_kernel<true, 4, true>)
+                : wide   ? (hilo ? gemm_tiled_kernel<true, 8> : gemm_tiled_kernel<false, 8>)
+                         : (hilo ? gemm_tiled_kernel<true, 4> : gemm_tiled_kernel<false, 4>);
     hipLaunchKernelGGL(kern, grid, dim3(256), 0, st, x, f.w_packed ? f.w_packed : w, bias,
-                       (int)M, (int)N, (int)K, (int)ep, out, pk, gm, kspan, partial);
+                       (int)M, (int)N, (int)K, (int)ep, out, pk, gm, kspan, partial,
+                       f.out_hilo && ep == Epilogue::kSwiGLU);
     if (splits > 1) {
       const int64_t total = M * N;
       const unsigned blocks = (unsigned)std::min<int64_t>((total + 255) / 256, 8192);

@@ -162,6 +162,9 @@ struct PrefillSplitOut {
   float* ws_o = nullptr;
   float* ws_ml = nullptr;
   int max_parts = 1;
+  // finished rows are written in the split operand layout of GemmFuse::x_hilo
+  // (only when no row comes in parts)
+  int out_hilo = 0;
 };
 hipError_t launch_paged_prefill(hipStream_t st, const KvGeom& kv, const void* arena,
                                 int64_t layer, const float* q, int64_t hq,
@@ -239,6 +242,12 @@ struct GemmFuse {
   // (64, 256)).  w may be null when w_packed is given.
   const uint16_t* w_packed = nullptr;
   bool w_packed_deferred = false;
+  // The LDS-tiled kernel only (M > 64): x arrives already split into its
+  // bf16 hi/lo pair (the layout launch_rmsnorm and the SwiGLU epilogue write
+  // with `hilo`: per row, K/8 groups of [8 hi bf16 | 8 lo bf16], the same
+  // bytes as f32), and a SwiGLU output is written that way.
+  bool x_hilo = false;
+  bool out_hilo = false;
 };
 // Bytes of W [N, K] in the decode kernel's packed order (0: K not a multiple
 // of 32), and the kernel that writes it from row-major W.  `deferred` must be
@@ -286,8 +295,12 @@ hipError_t launch_sample(hipStream_t st, float* logits, int64_t rows, int64_t vo
 hipError_t launch_embed(hipStream_t st, const uint32_t* tokens, int64_t n, const uint16_t* table,
                         int64_t hidden, float* out, double* sumsq = nullptr);
 // rows selected by `row_index` (nullptr = identity)
+// hilo: out holds each row as cols/8 groups of [8 hi bf16 | 8 lo bf16] (hi =
+// the f32 value truncated to bf16, lo = the remainder truncated), the input
+// layout of GemmFuse::x_hilo; needs cols % 8 == 0.
 hipError_t launch_rmsnorm(hipStream_t st, const float* x, const int32_t* row_index,
-                          const float* weight, int64_t rows, int64_t cols, float eps, float* out);
+                          const float* weight, int64_t rows, int64_t cols, float eps, float* out,
+                          bool hilo = false);
 // hidden[r] += (deferred GEMM output)[r], then out = rms_norm(hidden[r]) (the
 // residual add of transformer.rs:328-345 fused with the next norm).  With
 // row_index, only the gathered rows are computed and hidden is not written.

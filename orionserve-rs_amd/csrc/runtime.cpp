@@ -1595,6 +1595,22 @@ ORION_EXPORT int orion_hip_model_forward(orion_hip_model* m, const orion_hip_bat
   GemmFuse accumulate;  // residual-add GEMMs: out += x W^T (+ row sums of squares)
   accumulate.sumsq_out = sumsq;
   GemmPartials part{};
+  // Prefill-shaped batches (every layer GEMM on the LDS-tiled kernel): the
+  // two RMSNorms and the SwiGLU epilogue write their outputs already split
+  // into the GEMM's bf16 hi/lo operands, so the QKV, gate/up and down GEMMs
+  // load their activation fragments as they are.  The same truncated split,
+  // so the results are bit-identical; ORION_GEMM_PRESPLIT=0 keeps f32
+  // activations (measurement knob, read per call).
+  const char* presplit_env = getenv("ORION_GEMM_PRESPLIT");
+  const char* act_env = getenv("ORION_GEMM_ACT");
+  const bool presplit = !fused && n > 64 && pack_layers && H % 8 == 0 && F % 8 == 0 &&
+                        !(presplit_env && presplit_env[0] == '0') &&
+                        !(act_env && act_env[0] == 'b');
+  // The O GEMM's input too, when the prefill kernel writes every attention
+  // row itself (no decode rows, no key parts).
+  const bool o_presplit = presplit && plan.work.empty() && npf > 0 && !pf_split &&
+                          !(presplit_env && presplit_env[0] == '2');
+  pf_out.out_hilo = o_presplit ? 1 : 0;
   // (the fused route's embed also leaves the row sums of squares, so layer
   // 0's QKV GEMM applies its RMSNorm like every later layer's)
   HIP_TRY(st, launch_embed(stream, d_tok, n, m->w_embed, H, hidden, sumsq));
@@ -1606,8 +1622,10 @@ ORION_EXPORT int orion_hip_model_forward(orion_hip_model* m, const orion_hip_bat
     GemmFuse qkv_f = norm_in(L.input_norm);
     const float* qkv_x = hidden;
     if (!qkv_f.norm_sumsq) {
-      HIP_TRY(st, launch_rmsnorm(stream, hidden, nullptr, L.input_norm, n, H, d.rms_norm_eps, xn));
+      HIP_TRY(st, launch_rmsnorm(stream, hidden, nullptr, L.input_norm, n, H, d.rms_norm_eps, xn,
+                                 presplit));
       qkv_x = xn;
+      qkv_f.x_hilo = presplit;
     }
     qkv_f.defer = &part;
     if (pack_layers) qkv_f.w_packed = L.p_qkv, qkv_f.w_packed_deferred = true;
@@ -1626,16 +1644,20 @@ ORION_EXPORT int orion_hip_model_forward(orion_hip_model* m, const orion_hip_bat
         HIP_TRY(st, launch_split_merge(stream, d.head_dim, n, Hq, pf_merge, attn));
     }
     GemmFuse o_f = accumulate;
+    o_f.x_hilo = o_presplit;
     if (pack_layers) o_f.w_packed = L.p_o;
     HIP_TRY(st, gemm_on(m->dev, attn, L.w_o, nullptr, n, H, m->qd, Epilogue::kAccumulate,
                         hidden, &o_f));
     GemmFuse gu_f = norm_in(L.post_norm);
     if (pack_layers) gu_f.w_packed = L.p_gu;
     if (!fused)
-      HIP_TRY(st, launch_rmsnorm(stream, hidden, nullptr, L.post_norm, n, H, d.rms_norm_eps, xn));
+      HIP_TRY(st, launch_rmsnorm(stream, hidden, nullptr, L.post_norm, n, H, d.rms_norm_eps, xn,
+                                 presplit));
+    gu_f.x_hilo = gu_f.out_hilo = presplit;
     HIP_TRY(st, gemm_on(m->dev, fused ? hidden : xn, L.w_gu, nullptr, n, 2 * F, H,
                         Epilogue::kSwiGLU, act, &gu_f));
     GemmFuse down_f = accumulate;
+    down_f.x_hilo = presplit;
     if (pack_layers) down_f.w_packed = L.p_down;
     HIP_TRY(st, gemm_on(m->dev, act, L.w_down, nullptr, n, H, F, Epilogue::kAccumulate, hidden,
                         &down_f));
@@ -1814,6 +1836,10 @@ ORION_EXPORT int orion_hip_paged_attention_prefill(
     const uint32_t* d_bt_ids, int64_t max_rows, int64_t max_position, int32_t hilo,
     float* d_out) {
   const char* st = "paged_attention_prefill";
+  // value 16 added: write the output rows in the split operand layout of
+  // the O GEMM (GemmFuse::x_hilo) instead of f32
+  const bool out_split = (hilo & 16) != 0;
+  hilo &= ~16;
   if (hilo < 0 || hilo > 3) return internal(st, "operand mode %d is not 0..3", (int)hilo);
   // 0: bf16 Q and P; 1: hi/lo both; 2: hi/lo Q, bf16 P; 3: bf16 Q, hi/lo P
   static const int kOps[4] = {0, kPrefillQHiLo | kPrefillPHiLo, kPrefillQHiLo, kPrefillPHiLo};
@@ -1876,6 +1902,10 @@ ORION_EXPORT int orion_hip_paged_attention_prefill(
     out_parts.ws_ml = merge.ws + rows * num_q_heads * pfp.max_parts * g.head_dim;
     out_parts.max_parts = pfp.max_parts;
   }
+  if (out_split && split)
+    return set_err(ORION_HIP_ERR_BACKEND, st,
+                   "the split output layout needs every sequence whole (no key parts)");
+  out_parts.out_hilo = out_split ? 1 : 0;
   // (timed together: the kernel and, for split sequences, the merge of parts)
   HIP_TRY(st, timed_launch(dev, 2, [&] {
             hipError_t e = launch_paged_prefill(dev->stream, g, d_arena, layer, d_q, num_q_heads,

@@ -76,10 +76,10 @@ def bf16_round(x):
     return r.view(np.float32)
 
 
-def oracle_model(spec, W):
+def oracle_model(spec, W, kv_bf16=False):
     m = orc.OracleTransformer(spec.L, spec.H, spec.hq, spec.hkv, spec.d, spec.F, spec.V,
                               spec.max_pos, spec.eps, spec.theta, spec.bias, spec.tied,
-                              spec.num_blocks, spec.block_size)
+                              spec.num_blocks, spec.block_size, kv_bf16=kv_bf16)
     m.set_weight(orc.W_EMBED, -1, W["embed"])
     m.set_weight(orc.W_FINAL_NORM, -1, W["final_norm"])
     if W["lm_head"] is not None:

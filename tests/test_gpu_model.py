@@ -564,3 +564,39 @@ def test_prepared_batch_forward_is_identical(backend):
     g3 = m.forward(b2).logits  # reused arrays, same KV writes
     assert np.array_equal(g1, g3)
     m.close()
+
+
+@pytest.mark.parametrize("H,F,rows", [(512, 1408, 300), (1024, 2816, 1000), (256, 704, 100)])
+def test_presplit_activations_are_bit_identical(backend, monkeypatch, H, F, rows):
+    # Prefill-shaped forwards (every layer GEMM on the LDS-tiled kernel) have
+    # the RMSNorms and the SwiGLU epilogue write their outputs already split
+    # into the GEMMs' bf16 hi/lo operands; the split is the same truncation
+    # the GEMM applies to f32 activations, so logits and the KV arena must be
+    # bit-identical to ORION_GEMM_PRESPLIT=0, and close to the oracle.
+    spec = Spec(2, H, 8, 2, 64, F, 900, max_pos=2048, bias=True, tied=False,
+                num_blocks=128, block_size=16)
+    W = random_weights(spec, np.random.default_rng(H + rows), std=0.05)
+    lens = [rows - rows // 3, rows // 3]
+    tables = [list(range(0, 64)), list(range(64, 128))]
+    rng = np.random.default_rng(rows)
+    toks = rng.integers(0, spec.V, sum(lens))
+    pos = np.concatenate([np.arange(n) for n in lens])
+    out = {}
+    for knob in ("1", "0"):
+        monkeypatch.setenv("ORION_GEMM_PRESPLIT", knob)
+        gm = gpu_model(backend, spec, W, oh.BF16)
+        out[knob] = gm.forward(batch(toks, pos, lens, tables)).logits
+        ptr, nbytes = gm.kv_arena()
+        arena = np.empty(nbytes, np.uint8)
+        oh._check(backend.lib.orion_hip_memcpy_d2h(backend.handle, arena.ctypes.data, ptr, nbytes))
+        out[knob + "kv"] = arena
+        gm.close()
+    monkeypatch.delenv("ORION_GEMM_PRESPLIT")
+    print(f"[presplit] H={H} F={F} rows={rows}: identical "
+          f"{np.array_equal(out['1'].view(np.uint32), out['0'].view(np.uint32))}", flush=True)
+    assert np.array_equal(out["1"].view(np.uint32), out["0"].view(np.uint32))
+    assert np.array_equal(out["1kv"], out["0kv"])
+    om = oracle_model(spec, W, kv_bf16=True)
+    o = om.forward(toks, pos, lens, lens, tables)
+    assert rel_err(out["1"], o) <= 1e-3, rel_err(out["1"], o)
+    om.close()

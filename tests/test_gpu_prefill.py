@@ -190,3 +190,20 @@ def test_single_operand_hilo_modes(backend, mode, hq, hkv, d):
           f"mode{mode} {errs[mode]:.2e} hilo {errs[1]:.2e}", flush=True)
     assert errs[mode] <= 1e-2
     assert errs[1] <= 1e-4
+
+
+def test_split_output_layout_is_the_split_of_the_f32_output(backend):
+    # Operand mode + 16 writes each finished row as the O GEMM's pre-split
+    # operand: per 8 dims, 8 hi bf16 (the f32 value's top 16 bits) then 8 lo
+    # bf16 (the top 16 bits of value - hi).  It must be exactly the split of
+    # the f32 output the same launch writes without it.
+    case = PrefillCase(61, [0, 37, 300], [100, 64, 129], 32, 8, 128, 16)
+    f32 = run_prefill(backend, case, 1)
+    raw = run_prefill(backend, case, 1 | 16).view(np.uint32).reshape(f32.shape[0], -1, 8)
+    u16 = raw.view(np.uint16).reshape(f32.shape[0], -1, 16)
+    bits = f32.view(np.uint32).reshape(f32.shape[0], -1, 8)
+    hi = (bits >> 16).astype(np.uint16)
+    rem = f32.reshape(bits.shape) - (bits & np.uint32(0xFFFF0000)).view(np.float32)
+    lo = (rem.view(np.uint32) >> 16).astype(np.uint16)
+    assert np.array_equal(u16[..., :8], hi)
+    assert np.array_equal(u16[..., 8:], lo)
