@@ -359,7 +359,11 @@ int orion_hip_paged_attention_decode(orion_hip_device* dev, const orion_hip_kv_l
  * 0 rounds Q and the softmax weights P to bf16 (the MFMA-rate path for bf16
  * inputs); 1 carries each as a hi + lo bf16 pair (~16-bit products, twice the
  * MFMA work); 2 carries Q as a pair and rounds P; 3 rounds Q and carries P as
- * a pair.  Other values are an Internal error.
+ * a pair.  Adding 16 to the mode writes each output row in the split operand
+ * layout the prefill GEMMs read (per 8 values: 8 hi bf16, the value's top 16
+ * bits, then 8 lo bf16, the top 16 bits of the remainder; the same bytes as
+ * f32), which needs every sequence whole (a batch the kernel would cut into
+ * key parts is a Backend error).  Other values are an Internal error.
  * Table lengths and block ids are the caller's guarantee, as for decode. */
 int orion_hip_paged_attention_prefill(orion_hip_device* dev, const orion_hip_kv_layout* kv,
                                       const void* d_arena, int64_t layer, const float* d_q,

@@ -51,7 +51,6 @@ typedef __attribute__((address_space(3))) v4s lds_v4s;
 typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 typedef float f32x2 __attribute__((ext_vector_type(2)));
 
-constexpr int kNR = kPrefillWaveRowTiles;   // 16-row MFMA tiles per wave
 constexpr int kBN = 64;                     // keys per tile
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kLazy = 8.0f;               // log2 units: weights stay <= 2^8
@@ -108,7 +107,8 @@ __global__ void __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu
                          const uint32_t* __restrict__ bt_ids, float scale_log2,
                          float* __restrict__ out, PrefillSplitOut split) {
   constexpr int kWaves = WAVES;
-  constexpr int kBM = kWaves * 16 * kNR;  // packed rows per workgroup
+  constexpr int kNR = prefill_wave_row_tiles(D);  // 16-row MFMA tiles per wave
+  constexpr int kBM = kWaves * 16 * kNR;          // packed rows per workgroup
   constexpr bool QHL = (OPS & kPrefillQHiLo) != 0, PHL = (OPS & kPrefillPHiLo) != 0;
   constexpr int kStages = STAGES;
   static_assert(kStages >= 2 && kStages <= 3, "LDS stages");
@@ -502,7 +502,7 @@ hipError_t launch_paged_prefill(hipStream_t st, const KvGeom& kv, const void* ar
   if (num_tiles == 0) return hipSuccess;
   if (!kv.dtype_bf16) return hipErrorNotSupported;
   const int64_t hkv = kv.num_kv_heads, D = kv.head_dim;
-  if (hkv <= 0 || hq % hkv != 0 || (D != 64 && D != 128)) return hipErrorInvalidValue;
+  if (hkv <= 0 || hq % hkv != 0 || (D != 64 && D != 128 && D != 256)) return hipErrorInvalidValue;
   int bs_log2 = 0;
   while ((1 << bs_log2) < kv.block_size) ++bs_log2;
   const ArenaStrides a = arena_strides(kv);
@@ -522,12 +522,13 @@ hipError_t launch_paged_prefill(hipStream_t st, const KvGeom& kv, const void* ar
                      bs_log2,                                                                  \
                      (int)hkv, (int)hq, q, order, row_start, row_count, first_pos, bt_offsets, \
                      bt_ids, scale_log2, out, split)
-#define ORION_PREFILL_B(DD, HH, BB)           \
-  do {                                        \
-    if (waves == 4)                           \
-      ORION_PREFILL_W(DD, HH, BB, 4, 2);      \
-    else                                      \
-      ORION_PREFILL_W(DD, HH, BB, 8, 3);      \
+// (head_dim 256: 8 waves with 2 stages, 128 KiB of LDS, whatever the knob)
+#define ORION_PREFILL_B(DD, HH, BB)                       \
+  do {                                                    \
+    if (waves == 4 && DD <= 128)                          \
+      ORION_PREFILL_W(DD, HH, BB, (DD > 128 ? 8 : 4), 2); \
+    else                                                  \
+      ORION_PREFILL_W(DD, HH, BB, 8, (DD > 128 ? 2 : 3)); \
   } while (0)
 #define ORION_PREFILL(DD, HH)        \
   do {                               \
@@ -545,7 +546,9 @@ hipError_t launch_paged_prefill(hipStream_t st, const KvGeom& kv, const void* ar
     else if (ops == kPrefillPHiLo) ORION_PREFILL(DD, 2);              \
     else ORION_PREFILL(DD, 0);                                        \
   } while (0)
-  if (D == 128)
+  if (D == 256)
+    ORION_PREFILL_D(256);
+  else if (D == 128)
     ORION_PREFILL_D(128);
   else
     ORION_PREFILL_D(64);

@@ -141,12 +141,14 @@ struct PrefillPlan {
   // rows of unsplit sequences; sized to the batch's rows)
   std::vector<int32_t> split_rows, row_parts;
 };
-int prefill_tile_rows();  // packed rows per prefill workgroup
 int prefill_waves();      // waves per prefill workgroup (8, or 4 with ORION_PREFILL_WAVES=4)
+// 16-row MFMA tiles of packed rows per prefill wave: two, one at head_dim 256
+// (its query operands and output accumulators take twice the registers).
+constexpr int prefill_wave_row_tiles(int64_t head_dim) { return head_dim > 128 ? 1 : 2; }
+int prefill_tile_rows(int64_t head_dim);  // packed rows per prefill workgroup
 // Largest head_dim the attention and RoPE kernels take (any even value up to
 // it; the reference accepts any even head_dim).
 constexpr int kMaxHeadDim = 2048;
-constexpr int kPrefillWaveRowTiles = 2;  // 16-row MFMA tiles per prefill wave
 // Prefill operand precision bits (launch_paged_prefill `operands`): each set
 // bit carries that operand as a hi + lo bf16 pair, each clear one rounds it
 // to bf16.
@@ -155,7 +157,7 @@ constexpr int kPrefillQHiLo = 1, kPrefillPHiLo = 2;
 // per work-list entry); cus = 0 never splits.
 void build_prefill_order(const int32_t* row_start, const int32_t* row_count,
                          const uint32_t* first_pos, int64_t num_seqs, int64_t group, int64_t hkv,
-                         int64_t cus, PrefillPlan* plan);
+                         int64_t cus, PrefillPlan* plan, int64_t head_dim = 128);
 // Where split parts go: the decode split workspace layout over the batch's
 // rows (slot = (row * hq + head) * max_parts + part).
 struct PrefillSplitOut {

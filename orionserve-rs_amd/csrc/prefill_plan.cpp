@@ -23,7 +23,10 @@ int prefill_waves() {
   return w;
 }
 
-int prefill_tile_rows() { return prefill_waves() * 16 * kPrefillWaveRowTiles; }
+// (head_dim 256 always runs 8 waves: its 2-stage ring fills 128 KiB of LDS)
+int prefill_tile_rows(int64_t head_dim) {
+  return (head_dim > 128 ? 8 : prefill_waves()) * 16 * prefill_wave_row_tiles(head_dim);
+}
 
 // Key parts: a sequence is cut into nparts key ranges when its longest tile
 // reads more than an even share of all the tiles' key reads over the CUs
@@ -35,8 +38,8 @@ constexpr int kMinPartTiles = 16;
 
 void build_prefill_order(const int32_t* row_start, const int32_t* row_count,
                          const uint32_t* first_pos, int64_t num_seqs, int64_t group, int64_t hkv,
-                         int64_t cus, PrefillPlan* plan) {
-  const int64_t kBM = prefill_tile_rows();
+                         int64_t cus, PrefillPlan* plan, int64_t head_dim) {
+  const int64_t kBM = prefill_tile_rows(head_dim);
   struct Tile {
     int64_t seq, tile, kv_tiles;
   };

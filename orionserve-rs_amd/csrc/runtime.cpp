@@ -1442,7 +1442,8 @@ ORION_EXPORT int orion_hip_model_forward(orion_hip_model* m, const orion_hip_bat
   // call; lets tests compare the two routes on one batch).
   const char* route = getenv("ORION_PREFILL_ROUTE");
   const bool route_pf = !(route && route[0] == '0');
-  if (route_pf && m->kv.dtype_bf16 && (d.head_dim == 64 || d.head_dim == 128)) {
+  if (route_pf && m->kv.dtype_bf16 &&
+      (d.head_dim == 64 || d.head_dim == 128 || d.head_dim == 256)) {
     int64_t r0 = 0;
     for (int64_t s = 0; s < S; ++s) {
       const int64_t c = b->slot_token_counts[s];
@@ -1463,7 +1464,7 @@ ORION_EXPORT int orion_hip_model_forward(orion_hip_model* m, const orion_hip_bat
   PrefillPlan pfp;
   if (npf)
     build_prefill_order(pf_start.data(), pf_count.data(), pf_pos.data(), npf, G, d.num_kv_heads,
-                        m->dev->wave_slots / 8, &pfp);
+                        m->dev->wave_slots / 8, &pfp, d.head_dim);
   const std::vector<PrefillTile>& pf_order = pfp.order;
   const bool pf_split = pfp.max_parts > 1;
   // Decode plan (longest-first chunk list) over the remaining rows.
@@ -1847,9 +1848,9 @@ ORION_EXPORT int orion_hip_paged_attention_prefill(
   if (int rc = kv_geom_from(kv, &g, st)) return rc;
   if (g.num_kv_heads <= 0 || num_q_heads % g.num_kv_heads)
     return internal(st, "query heads cannot be grouped over kv heads");
-  if (g.head_dim != 64 && g.head_dim != 128)
+  if (g.head_dim != 64 && g.head_dim != 128 && g.head_dim != 256)
     return set_err(ORION_HIP_ERR_BACKEND, st,
-                   "prefill attention covers head_dim 64 and 128 (got %lld); other shapes take "
+                   "prefill attention covers head_dim 64, 128 and 256 (got %lld); other shapes take "
                    "the decode entry point row by row", (long long)g.head_dim);
   HIP_TRY(st, hipSetDevice(dev->ordinal));
   (void)max_rows;
@@ -1870,7 +1871,8 @@ ORION_EXPORT int orion_hip_paged_attention_prefill(
   }
   PrefillPlan pfp;
   build_prefill_order(h_start.data(), h_count.data(), h_first.data(), num_seqs,
-                      num_q_heads / g.num_kv_heads, g.num_kv_heads, dev->wave_slots / 8, &pfp);
+                      num_q_heads / g.num_kv_heads, g.num_kv_heads, dev->wave_slots / 8, &pfp,
+                      g.head_dim);
   const std::vector<PrefillTile>& order = pfp.order;
   // work list, then (when sequences are split into key parts) the merge's
   // row list and parts per row, in one device buffer

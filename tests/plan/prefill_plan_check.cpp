@@ -3,13 +3,13 @@
 //
 //   prefill_plan_check random TRIALS
 //     For random batches (chunk lengths, prefixes, query-head groups, KV
-//     heads, CU counts) every plan must give each (sequence, tile of packed
+//     heads, CU counts, head_dim 128 and 256) every plan must give each (sequence, tile of packed
 //     rows) exactly `nparts` entries, parts 0 .. nparts-1 in key order, whose
 //     key-tile ranges tile [0, key tiles the tile's last row attends) with no
 //     gap or overlap; nparts must be the same for every tile of a sequence;
 //     row_parts / split_rows must list exactly the rows of split sequences;
 //     and the list must be sorted longest first.
-//   prefill_plan_check case CUS GROUP HKV P0,P1,... C0,C1,...
+//   prefill_plan_check case CUS GROUP HKV P0,P1,... C0,C1,... [HEAD_DIM]
 //     Plans one batch (prefixes P, chunk lengths C) and prints
 //       parts=<max parts> entries=<n> empty=<parts reading no key>
 //       straddle=<parts whose first key lies inside the positions of one
@@ -43,7 +43,7 @@ struct Stats {
 };
 
 Stats check(const std::vector<int32_t>& prefix, const std::vector<int32_t>& chunk, int group,
-            int hkv, int cus) {
+            int hkv, int cus, int head_dim = 128) {
   const int S = (int)chunk.size();
   std::vector<int32_t> start(S);
   std::vector<uint32_t> first(S);
@@ -54,8 +54,9 @@ Stats check(const std::vector<int32_t>& prefix, const std::vector<int32_t>& chun
     first[s] = (uint32_t)prefix[s];
   }
   PrefillPlan plan;
-  orion::build_prefill_order(start.data(), chunk.data(), first.data(), S, group, hkv, cus, &plan);
-  const int64_t kBM = orion::prefill_tile_rows();
+  orion::build_prefill_order(start.data(), chunk.data(), first.data(), S, group, hkv, cus, &plan,
+                             head_dim);
+  const int64_t kBM = orion::prefill_tile_rows(head_dim);
   Stats st;
   // expected tiles and their key-tile counts
   std::map<std::pair<int, int>, std::vector<const PrefillTile*>> by_tile;
@@ -151,7 +152,8 @@ int main(int argc, char** argv) {
         chunk[s] = (rng() % 6 == 0) ? 0 : 1 + rng() % 3000;
         prefix[s] = (rng() % 3 == 0) ? 0 : (int)(rng() % 30000);
       }
-      const Stats st = check(prefix, chunk, group, hkv, cus);
+      // head_dim 256 plans tiles of half as many packed rows
+      const Stats st = check(prefix, chunk, group, hkv, cus, trial % 2 ? 256 : 128);
       empty += st.empty;
       straddle += st.straddle;
       split += st.empty + st.straddle > 0;
@@ -159,15 +161,16 @@ int main(int argc, char** argv) {
     printf("%d trials empty=%ld straddle=%ld failures=%d\n", trials, empty, straddle, g_fails);
     return g_fails ? 1 : 0;
   }
-  if (argc == 7 && std::string(argv[1]) == "case") {
+  if ((argc == 7 || argc == 8) && std::string(argv[1]) == "case") {
     const int cus = atoi(argv[2]), group = atoi(argv[3]), hkv = atoi(argv[4]);
+    const int head_dim = argc == 8 ? atoi(argv[7]) : 128;
     const auto prefix = parse_list(argv[5]), chunk = parse_list(argv[6]);
     if (prefix.size() != chunk.size()) {
       printf("prefix and chunk lists differ in length\n");
       return 2;
     }
     std::vector<int32_t> start(chunk.size());
-    const Stats st = check(prefix, chunk, group, hkv, cus);
+    const Stats st = check(prefix, chunk, group, hkv, cus, head_dim);
     // max parts, entries
     PrefillPlan plan;
     std::vector<uint32_t> first(prefix.begin(), prefix.end());
@@ -177,11 +180,12 @@ int main(int argc, char** argv) {
       rows += chunk[s];
     }
     orion::build_prefill_order(start.data(), chunk.data(), first.data(), (int64_t)chunk.size(),
-                               group, hkv, cus, &plan);
+                               group, hkv, cus, &plan, head_dim);
     printf("parts=%d entries=%zu empty=%d straddle=%d failures=%d\n", plan.max_parts,
            plan.order.size(), st.empty, st.straddle, g_fails);
     return g_fails ? 1 : 0;
   }
-  printf("usage: prefill_plan_check random TRIALS | case CUS GROUP HKV PREFIXES CHUNKS\n");
+  printf("usage: prefill_plan_check random TRIALS | case CUS GROUP HKV PREFIXES CHUNKS "
+         "[HEAD_DIM]\n");
   return 2;
 }

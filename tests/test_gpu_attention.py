@@ -121,29 +121,31 @@ def test_any_head_dim_and_group(backend, hq, hkv, d, bs, dtype):
     assert mm == 0, (ma, mr, wi)
 
 
-def shared_prefix_case(seed, hq, hkv, d, bs):
+def shared_prefix_case(seed, hq, hkv, d, bs, head_major=False):
     # 40 rows: rows 0-19 share 1,024 tokens; rows 20-26 share 320; rows
     # 30-35 share 640 with row 30 except row 33, which shares 288 (a pack's
     # prefix is what all its rows share); rows 36-39 share 2 blocks (too
     # short to pack); the rest are private.
     rng = np.random.default_rng(seed)
     ctxs = rng.integers(1100, 3000, 40)
-    case = PagedCase(seed, ctxs, hq, hkv, d, bs, dtype="bf16")
+    case = PagedCase(seed, ctxs, hq, hkv, d, bs, dtype="bf16", head_major=head_major)
     tok = lambda n: -(-n // bs)
     return case.share_prefixes([(list(range(20)), tok(1024)), (list(range(20, 27)), tok(320)),
                                 ([30, 31, 32, 34, 35], tok(640)), ([30, 33], tok(288)),
                                 ([36, 37, 38, 39], 2)])
 
 
-@pytest.mark.parametrize("hq,hkv,d,bs", [(28, 4, 128, 16), (32, 8, 128, 16), (8, 8, 64, 16),
-                                         (16, 4, 64, 16), (16, 2, 128, 32), (12, 4, 64, 8)])
-def test_packed_shared_prefixes(backend, monkeypatch, hq, hkv, d, bs):
+@pytest.mark.parametrize("hq,hkv,d,bs,hm", [(28, 4, 128, 16, False), (32, 8, 128, 16, False),
+                                            (8, 8, 64, 16, False), (16, 4, 64, 16, False),
+                                            (16, 2, 128, 32, False), (12, 4, 64, 8, False),
+                                            (28, 4, 128, 16, True)])
+def test_packed_shared_prefixes(backend, monkeypatch, hq, hkv, d, bs, hm):
     # Rows whose tables start with the same block ids attend that prefix
     # together: up to 16 / G rows' query heads fill one MFMA wave's query
     # columns, and the prefix pieces are splits of every row of the pack.
     # Against the oracle, and against the same plan without packing
     # (ORION_DECODE_PACK=0), which plans no packed item.
-    case = shared_prefix_case(hq + d + bs, hq, hkv, d, bs)
+    case = shared_prefix_case(hq + d + bs, hq, hkv, d, bs, head_major=hm)
     args = (case.positions, case.row_seq, case.bt_offsets, case.bt_ids, hq, hkv, d, bs)
     items = oh.DecodePlan(backend, *args)
     info = items.info()

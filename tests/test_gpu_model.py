@@ -459,7 +459,7 @@ def test_fused_decode_layer_matches_oracle_and_unfused(backend, monkeypatch, H, 
 @pytest.mark.parametrize("H,hq,hkv,d,kv", [(320, 4, 2, 80, oh.F32), (320, 4, 2, 80, oh.BF16),
                                            (256, 16, 1, 48, oh.F32), (384, 24, 2, 96, oh.BF16),
                                            (512, 2, 1, 384, oh.F32), (1024, 2, 2, 1024, oh.F32),
-                                           (1024, 16, 1, 64, oh.BF16)])
+                                           (1024, 16, 1, 64, oh.BF16), (1024, 4, 2, 256, oh.BF16)])
 def test_any_head_dim_and_group_forward(backend, H, hq, hkv, d, kv):
     # head_dim 80 / 48 / 96 / 384 / 1024 and groups of 1, 2, 16 and 12 query
     # heads per KV head (and head_dim 64 with 16, whose prompts take the MFMA

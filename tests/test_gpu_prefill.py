@@ -66,6 +66,8 @@ def test_cfg3_full_size_sampled_rows(backend, hilo, head_major):
     (12, 4, 128, 32), (6, 1, 64, 1), (16, 16, 128, 64),
     # groups above 8 (Llama-3.1-405B has 16 query heads per KV head; MQA)
     (32, 2, 128, 16), (12, 1, 128, 16), (32, 1, 64, 16),
+    # head_dim 256 (one 16-row tile per wave, a 2-stage ring)
+    (8, 2, 256, 16), (16, 1, 256, 16), (4, 4, 256, 32),
 ])
 @pytest.mark.parametrize("hilo", [False, True])
 @pytest.mark.parametrize("head_major", [False, True])
@@ -94,10 +96,11 @@ def test_shapes_against_oracle(backend, hq, hkv, d, bs, hilo, head_major):
 KEY_PART_CASES = [
     ([9000, 400, 60, 0], [256, 256, 100, 1500], 28, 4, 128),
     ([0, 0, 0, 26474], [2575, 414, 1096, 343], 2, 1, 128),
+    ([0, 12000, 300], [700, 200, 500], 8, 2, 256),  # head_dim 256 with parts
 ]
 
 
-@pytest.mark.parametrize("which", [0, 1])
+@pytest.mark.parametrize("which", [0, 1, 2])
 @pytest.mark.parametrize("hilo", [False, True])
 def test_key_parts_for_long_prefixes(backend, monkeypatch, hilo, which):
     # Sequences whose tiles read far more keys than an even share of the CUs
@@ -165,11 +168,11 @@ def test_f32_arena_is_a_backend_error(backend):
         run_prefill(backend, case, False)
 
 
-@pytest.mark.parametrize("hq,hkv,d", [(8, 2, 80), (4, 2, 256), (8, 1, 96)])
+@pytest.mark.parametrize("hq,hkv,d", [(8, 2, 80), (4, 2, 192), (8, 1, 96)])
 def test_uncovered_prefill_shapes_are_backend_errors(backend, hq, hkv, d):
-    # The MFMA prefill kernel covers head_dim 64/128 with any grouping; the
+    # The MFMA prefill kernel covers head_dim 64/128/256 with any grouping; the
     # model forward sends other shapes' rows to the decode kernel (which
-    # covers every even head_dim up to 256 and any group), and the op-level
+    # covers every even head_dim up to 2048 and any group), and the op-level
     # entry point refuses them with a Backend error before any launch.
     case = PrefillCase(4, [20], [8], hq, hkv, d, 16)
     with pytest.raises(oh.BackendError):

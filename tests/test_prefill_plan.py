@@ -26,9 +26,9 @@ def check_exe(tmp_path_factory):
     return exe
 
 
-def run_case(exe, prefixes, chunks, hq, hkv):
+def run_case(exe, prefixes, chunks, hq, hkv, d=128):
     p = subprocess.run([exe, "case", str(CUS), str(hq // hkv), str(hkv),
-                        ",".join(map(str, prefixes)), ",".join(map(str, chunks))],
+                        ",".join(map(str, prefixes)), ",".join(map(str, chunks)), str(d)],
                        capture_output=True, text=True)
     print(p.stdout)
     assert p.returncode == 0, p.stdout
@@ -51,6 +51,9 @@ def test_key_part_cases_cover_what_the_gpu_test_claims(check_exe):
     prefixes, chunks, hq, hkv, _ = KEY_PART_CASES[1]
     st = run_case(check_exe, prefixes, chunks, hq, hkv)
     assert int(st["parts"]) > 1 and int(st["empty"]) > 0 and int(st["straddle"]) > 0
+    prefixes, chunks, hq, hkv, d = KEY_PART_CASES[2]
+    st = run_case(check_exe, prefixes, chunks, hq, hkv, d)
+    assert d == 256 and int(st["parts"]) > 1
 
 
 def test_no_split_when_disabled(check_exe):
