@@ -6,6 +6,8 @@
 #include <algorithm>
 #include <cstdint>
 #include <cstdlib>
+#include <map>
+#include <tuple>
 #include <unordered_map>
 #include <utility>
 #include <vector>
@@ -265,17 +267,49 @@ void build_decode_plan(const uint32_t* positions, const int32_t* row_seq,
                    [](const Piece& a, const Piece& b) { return a.len > b.len; });
   plan->work.reserve(pcs.size() * hkv);
   plan->num_packed = 0;
-  for (const Piece& pc : pcs) {
+  auto tbl_of = [&](const Piece& pc) {
     const int64_t r0 = pc.packed ? plan->pack_rows[pc.row * pack_r] : pc.row;
-    const int64_t tbl_off = bt_offsets[row_seq[r0]] + (pc.start >> bs_log2);
-    // a packed item always writes partials (nsplit 2: every row of the pack
-    // has a private piece too) and is flagged shared = 2
-    const int32_t n = pc.packed ? 2 : plan->row_nsplit[pc.row];
+    return bt_offsets[row_seq[r0]] + (pc.start >> bs_log2);
+  };
+  // Packed items first.  Packs on one prefix share its pieces' blocks, so a
+  // piece is taken by kItemsPerWorkgroup packs at a time with the KV head
+  // outer: the waves of one workgroup (adjacent items) then read the same
+  // K/V rows together and the repeats hit the CU's cache.  (A packed item
+  // always writes partials, nsplit 2 -- every row of a pack has a private
+  // piece too -- and is flagged shared = 2.)
+  constexpr int kItemsPerWorkgroup = 4;
+  std::vector<std::vector<const Piece*>> same_piece;  // packs reading one piece
+  std::map<std::tuple<int, int, uint32_t>, size_t> piece_index;
+  for (const Piece& pc : pcs) {
+    if (!pc.packed) continue;
+    const auto key = std::make_tuple(pc.start, pc.len, bt_ids[tbl_of(pc)]);
+    auto it = piece_index.find(key);
+    if (it == piece_index.end()) {
+      piece_index[key] = same_piece.size();
+      same_piece.push_back({&pc});
+    } else {
+      same_piece[it->second].push_back(&pc);
+    }
+  }
+  for (const auto& packs : same_piece)
+    for (size_t g = 0; g < packs.size(); g += kItemsPerWorkgroup) {
+      const size_t ge = std::min(packs.size(), g + kItemsPerWorkgroup);
+      for (int64_t h = 0; h < hkv; ++h)
+        for (size_t j = g; j < ge; ++j) {
+          const Piece& pc = *packs[j];
+          const int64_t tbl_off = tbl_of(pc);
+          plan->work.push_back({(int32_t)(pc.row * hkv + h), pc.start, pc.start + pc.len, 2,
+                                (int32_t)tbl_off, (int32_t)bt_ids[tbl_off], 2, pc.split});
+          ++plan->num_packed;
+        }
+    }
+  for (const Piece& pc : pcs) {
+    if (pc.packed) continue;
+    const int64_t tbl_off = tbl_of(pc);
+    const int32_t n = plan->row_nsplit[pc.row];
     for (int64_t h = 0; h < hkv; ++h)
       plan->work.push_back({(int32_t)(pc.row * hkv + h), pc.start, pc.start + pc.len, n,
-                            (int32_t)tbl_off, (int32_t)bt_ids[tbl_off], pc.packed ? 2 : 0,
-                            pc.split});
-    if (pc.packed) plan->num_packed += (int)hkv;
+                            (int32_t)tbl_off, (int32_t)bt_ids[tbl_off], 0, pc.split});
   }
   const int64_t num_plain = (int64_t)plan->work.size() - plan->num_packed;
   // Shared blocks: a block id attended by two planned rows (two rows of one

@@ -51,7 +51,8 @@ struct DecodeWork {
   // reads, 2 for a packed prefix item (DecodePlanHost::num_packed)
   int32_t item, start, end, nsplit, tbl_off, blk0, shared, split;
 };
-// Decode work plan: items in longest-first order; built on the host from the
+// Decode work plan: packed prefix items first, then the others longest first;
+// built on the host from the
 // query positions and block tables, shared by every layer of a forward.
 struct DecodePlanHost {
   int chunk = 0;       // longest piece, in tokens
