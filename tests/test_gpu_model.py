@@ -566,7 +566,8 @@ def test_prepared_batch_forward_is_identical(backend):
     m.close()
 
 
-@pytest.mark.parametrize("H,F,rows", [(512, 1408, 300), (1024, 2816, 1000), (256, 704, 100)])
+@pytest.mark.parametrize("H,F,rows", [(512, 1408, 300), (1024, 2816, 1000), (256, 704, 100),
+                                      (8224, 256, 80)])  # hidden > 8192: rmsnorm's loop path
 def test_presplit_activations_are_bit_identical(backend, monkeypatch, H, F, rows):
     # Prefill-shaped forwards (every layer GEMM on the LDS-tiled kernel) have
     # the RMSNorms and the SwiGLU epilogue write their outputs already split
