@@ -392,6 +392,38 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(NTW ==
       }
     return;
   }
+  if (ep == (int)Epilogue::kAccumulate) {
+    // Residual add, one 16-row tile at a time: all of its residual values are
+    // loaded before any sum is stored.  Written as `out[i] += v` per element,
+    // every load would wait for the stores before it (loads and stores to one
+    // array keep their order), one memory round trip per element: at config
+    // 4's prefill O and down shapes that epilogue cost 76 and 84 us per
+    // launch.  (Loading the whole tile at once, or before the k-loop, takes
+    // the kernel past the registers of three workgroups per CU.)
+#pragma unroll
+    for (int mt = 0; mt < 4; ++mt) {
+      float res[NTW][4];
+#pragma unroll
+      for (int nt = 0; nt < NTW; ++nt) {
+        const int col = n0 + wn * 16 * NTW + nt * 16 + l16;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int row = m0 + wm * 64 + mt * 16 + 4 * grp + i;
+          res[nt][i] = (row < M && col < N) ? out[(int64_t)row * N + col] : 0.f;
+        }
+      }
+#pragma unroll
+      for (int nt = 0; nt < NTW; ++nt) {
+        const int col = n0 + wn * 16 * NTW + nt * 16 + l16;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int row = m0 + wm * 64 + mt * 16 + 4 * grp + i;
+          if (row < M && col < N) out[(int64_t)row * N + col] = res[nt][i] + acc[mt][nt][i];
+        }
+      }
+    }
+    return;
+  }
 #pragma unroll
   for (int mt = 0; mt < 4; ++mt) {
 #pragma unroll
@@ -418,11 +450,7 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(NTW ==
             }
           }
         } else if (row < M && col < N) {
-          float* op = out + (int64_t)row * N + col;
-          if (ep == (int)Epilogue::kAccumulate)
-            *op += v;
-          else
-            *op = bias ? v + bias[col] : v;
+          out[(int64_t)row * N + col] = bias ? v + bias[col] : v;
         }
       }
     }
