@@ -239,3 +239,36 @@ def test_golden_cfg1_fixture(backend):
     got = run_decode(backend, case)
     mm, ma, mr, wi = orc.validate(g["out"], got, orc.Tolerance.F32)
     assert mm == 0, (ma, mr, wi)
+
+
+@pytest.mark.parametrize("seed", [1, 2, 3, 4])
+def test_packed_random_sharing_patterns(backend, seed):
+    # Random batches of rows sharing prefixes of random depths (several
+    # groups, nested depths, rows whose context barely passes the prefix),
+    # random grouping and head_dim 64/128 on bf16 arenas, against the oracle.
+    rng = np.random.default_rng(1000 + seed)
+    hkv = int(rng.choice([1, 2, 4, 8]))
+    G = int(rng.choice([1, 2, 3, 4, 5, 7, 8]))
+    d = int(rng.choice([64, 128]))
+    bs = int(rng.choice([8, 16, 32]))
+    rows = int(rng.integers(8, 48))
+    ctxs = rng.integers(300, 2600, rows)
+    case = PagedCase(2000 + seed, ctxs, G * hkv, hkv, d, bs, dtype="bf16")
+    groups, r = [], 0
+    while r < rows - 1:
+        n = int(rng.integers(2, 9))
+        members = list(range(r, min(rows, r + n)))
+        depth = int(min(ctxs[m] for m in members) // bs)
+        nb = int(rng.integers(1, depth + 1))
+        groups.append((members, nb))
+        r += n + int(rng.integers(0, 3))
+    case.share_prefixes(groups)
+    plan = oh.DecodePlan(backend, case.positions, case.row_seq, case.bt_offsets, case.bt_ids,
+                         case.hq, hkv, d, bs)
+    info = plan.info()
+    plan.close()
+    got = run_decode(backend, case)
+    err = float(np.abs(got - case.oracle()).max())
+    print(f"[packed random] seed={seed} G={G} hkv={hkv} d={d} bs={bs} rows={rows} "
+          f"packed items {info['packed_items']} of {info['num_work']}, err {err:.2e}", flush=True)
+    assert err <= 1e-4
