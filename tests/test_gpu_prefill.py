@@ -210,3 +210,29 @@ def test_split_output_layout_is_the_split_of_the_f32_output(backend):
     lo = (rem.view(np.uint32) >> 16).astype(np.uint16)
     assert np.array_equal(u16[..., :8], hi)
     assert np.array_equal(u16[..., 8:], lo)
+
+
+@pytest.mark.parametrize("seed", [1, 2, 3, 4, 5, 6])
+def test_random_prefill_batches(backend, seed):
+    # Random batches: 1-6 sequences with prefixes 0-6000 and chunks 1-700,
+    # random grouping, head_dim 64/128/256 and block size, both operand
+    # precisions; every output row against the oracle on sampled rows, and
+    # everything finite.
+    rng = np.random.default_rng(3000 + seed)
+    S = int(rng.integers(1, 7))
+    hkv = int(rng.choice([1, 2, 4, 8]))
+    G = int(rng.choice([1, 2, 4, 7, 8, 12, 16]))
+    d = int(rng.choice([64, 128, 256]))
+    bs = int(rng.choice([8, 16, 32]))
+    prefixes = [int(rng.integers(0, 6000)) if rng.random() < 0.7 else 0 for _ in range(S)]
+    chunks = [int(rng.integers(1, 700)) for _ in range(S)]
+    case = PrefillCase(4000 + seed, prefixes, chunks, G * hkv, hkv, d, bs)
+    rows = sample_rows(case, 12, seed=seed)
+    want = case.oracle_rows(rows)
+    for hilo, tol in ((True, 1e-4), (False, 1e-2)):
+        got = run_prefill(backend, case, hilo)
+        err = float(np.abs(got[rows] - want).max())
+        print(f"[prefill random] seed={seed} S={S} G={G} hkv={hkv} d={d} bs={bs} hilo={hilo} "
+              f"rows={len(rows)} err {err:.2e}", flush=True)
+        assert np.isfinite(got).all()
+        assert err <= tol
