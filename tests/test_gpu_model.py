@@ -1,6 +1,8 @@
 """LanguageModel::forward on the MI355X against the CPU oracle, plus the
 reference's model invariants (crates/orion-models/src/transformer.rs:590-746)
 checked GPU against GPU."""
+import os
+
 import numpy as np
 import pytest
 
@@ -601,3 +603,57 @@ def test_presplit_activations_are_bit_identical(backend, monkeypatch, H, F, rows
     o = om.forward(toks, pos, lens, lens, tables)
     assert rel_err(out["1"], o) <= 1e-3, rel_err(out["1"], o)
     om.close()
+
+
+@pytest.mark.parametrize("kv,G", [(oh.F32, 4), (oh.BF16, 4), (oh.BF16, 7)])
+def test_continuous_batch_with_a_shared_prefix(backend, kv, G):
+    # Three forwards as an engine with prefix caching drives them.  Forward 1
+    # prefills sequence A (600 tokens).  Forward 2 mixes A's first decode
+    # step, B = a sequence whose table starts with A's first 32 blocks (512
+    # cached tokens, not recomputed) and which appends 10 rows of its own
+    # (decode-kernel rows: 10 x G < 64 (row, head) pairs at G = 4), a second
+    # sharer C appending one row, and a fresh prefill D.  Forward 3 decodes
+    # A, B, C and D together (A, B and C attend the shared blocks: packed
+    # items on a bf16 arena).  Logits against the oracle running the same
+    # calls, and identical between packed and unpacked plans.
+    hkv = 2
+    spec = Spec(2, G * hkv * 64, G * hkv, hkv, 64, 512, 700,
+                max_pos=1024, bias=True, tied=False, num_blocks=160, block_size=16)
+    rng = np.random.default_rng(91 + G)
+    W = random_weights(spec, rng, std=0.05)
+    tA = list(range(0, 40))
+    tB = tA[:32] + list(range(40, 60))
+    tC = tA[:32] + list(range(60, 80))
+    tD = list(range(80, 100))
+    promptA = rng.integers(0, spec.V, 600)
+    tokB = rng.integers(0, spec.V, 10)
+    tokD = rng.integers(0, spec.V, 200)
+    bound = 1e-4 if kv == oh.F32 else 2e-3
+
+    def run(env):
+        gm = gpu_model(backend, spec, W, kv)
+        om = oracle_model(spec, W, kv_bf16=kv == oh.BF16)
+        outs = []
+        for toks, pos, counts, ctx, tables in [
+                (promptA, np.arange(600), [600], [600], [tA]),
+                (np.concatenate([[int(promptA[-1])], tokB, [7], tokD]),
+                 np.concatenate([[600], np.arange(512, 522), [512], np.arange(200)]),
+                 [1, 10, 1, 200], [601, 522, 513, 200], [tA, tB, tC, tD]),
+                ([5, 6, 8, 9], [601, 522, 513, 200], [1, 1, 1, 1], [602, 523, 514, 201],
+                 [tA, tB, tC, tD])]:
+            g = gm.forward(batch(toks, pos, counts, tables, ctx)).logits
+            o = om.forward(list(toks), list(pos), counts, ctx, tables)
+            assert rel_err(g, o) <= bound, (env, rel_err(g, o))
+            outs.append(g)
+        gm.close()
+        om.close()
+        return outs
+
+    packed = run("packed")
+    os.environ["ORION_DECODE_PACK"] = "0"
+    try:
+        plain = run("plain")
+    finally:
+        del os.environ["ORION_DECODE_PACK"]
+    for a, b in zip(packed, plain):
+        assert float(np.abs(a - b).max()) <= 2e-5 * max(float(np.abs(b).max()), 1.0)
