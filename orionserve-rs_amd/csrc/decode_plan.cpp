@@ -42,11 +42,12 @@ constexpr int64_t kMaxBalancedRounds = 4;
 // streaming (set-up, split-K partial write and merge read).
 constexpr int64_t kItemOverhead = 96;
 
-static int64_t estimate_split_time(const std::vector<int>& lens, int64_t hkv, int C,
+// C is a power of two (2^c_log2).
+static int64_t estimate_split_time(const std::vector<int>& lens, int64_t hkv, int C, int c_log2,
                                    int64_t slots) {
   int64_t total = 0, items = 0, largest = 0;
   for (int L : lens) {
-    const int64_t full = L / C, tail = L % C;
+    const int64_t full = L >> c_log2, tail = L & (C - 1);
     items += hkv * (full + (tail ? 1 : 0));
     total += (int64_t)hkv * L;
     largest = std::max<int64_t>(largest, full ? C : tail);
@@ -134,18 +135,21 @@ void build_decode_plan(const uint32_t* positions, const int32_t* row_seq,
   const int npacks = (int)pack_len.size();
 
   // The segments the pieces are cut from: each row's private part [prefix,
-  // len) and each pack's prefix [0, L).
+  // len) and each pack's prefix [0, L).  Empty ones (skipped rows) are left
+  // out: they add no items, bytes or length to any estimate below.
   std::vector<int> seg;
+  seg.reserve(rows + pack_len.size());
   int max_len = 0;
-  for (int64_t r = 0; r < rows; ++r) seg.push_back(lens[r] - prefix[r]);
+  for (int64_t r = 0; r < rows; ++r)
+    if (lens[r] - prefix[r] > 0) seg.push_back(lens[r] - prefix[r]);
   for (int L : pack_len) seg.push_back(L);
   for (int L : seg) max_len = std::max(max_len, L);
 
   int best_c = 0;
   int64_t best_t = 0;
-  for (int C = 64; C <= 2048; C <<= 1) {
+  for (int C = 64, c_log2 = 6; C <= 2048; C <<= 1, ++c_log2) {
     if (C < block_size || C / block_size > 64) continue;
-    const int64_t t = estimate_split_time(seg, hkv, C, wave_slots);
+    const int64_t t = estimate_split_time(seg, hkv, C, c_log2, wave_slots);
     if (best_c == 0 || t < best_t) {
       best_c = C;
       best_t = t;
@@ -313,33 +317,41 @@ void build_decode_plan(const uint32_t* positions, const int32_t* row_seq,
   }
   const int64_t num_plain = (int64_t)plan->work.size() - plan->num_packed;
   // Shared blocks: a block id attended by two planned rows (two rows of one
-  // sequence share their prefix blocks too).  One pass over the attended
-  // ids with two bitmaps (seen, seen again) that are cleared afterwards;
-  // then each plain work item is flagged when its token range reads a
-  // shared block (packed items, shared = 2, keep cached loads).
+  // sequence share their prefix blocks too).  Two passes over the attended
+  // ids: the first finds their range (the bitmap words touched), the second
+  // sets two bitmaps (seen, seen again) without branches; both are cleared
+  // afterwards.  Then each plain work item is flagged when its token range
+  // reads a shared block (packed items, shared = 2, keep cached loads).
   static thread_local std::vector<uint64_t> seen, again;
+  uint32_t id_lo = UINT32_MAX, id_hi = 0;
+  for (int64_t r = 0; r < rows; ++r) {
+    if (lens[r] == 0) continue;
+    const uint32_t* t = bt_ids + bt_offsets[row_seq[r]];
+    const int64_t nb = ((int64_t)lens[r] + block_size - 1) >> bs_log2;
+    for (int64_t j = 0; j < nb; ++j) {
+      id_lo = std::min(id_lo, t[j]);
+      id_hi = std::max(id_hi, t[j]);
+    }
+  }
   bool shared = false;
-  size_t w_lo = SIZE_MAX, w_hi = 0;  // words touched (cleared afterwards)
-  auto attended = [&](auto&& f) {
+  const size_t w_lo = id_lo >> 6, w_hi = id_hi >> 6;  // words touched (when id_lo <= id_hi)
+  if (id_lo <= id_hi) {
+    if (w_hi >= seen.size()) seen.resize(w_hi + 1, 0), again.resize(w_hi + 1, 0);
+    uint64_t* sn = seen.data();
+    uint64_t* ag = again.data();
     for (int64_t r = 0; r < rows; ++r) {
       if (lens[r] == 0) continue;
-      const int64_t o = bt_offsets[row_seq[r]];
+      const uint32_t* t = bt_ids + bt_offsets[row_seq[r]];
       const int64_t nb = ((int64_t)lens[r] + block_size - 1) >> bs_log2;
-      for (int64_t j = 0; j < nb; ++j) f(bt_ids[o + j]);
+      for (int64_t j = 0; j < nb; ++j) {
+        const uint32_t id = t[j];
+        const uint64_t bit = 1ull << (id & 63);
+        ag[id >> 6] |= sn[id >> 6] & bit;
+        sn[id >> 6] |= bit;
+      }
     }
-  };
-  attended([&](uint32_t id) {
-    const size_t w = id >> 6;
-    if (w >= seen.size()) seen.resize(w + 1, 0), again.resize(w + 1, 0);
-    w_lo = std::min(w_lo, w);
-    w_hi = std::max(w_hi, w);
-    const uint64_t bit = 1ull << (id & 63);
-    if (seen[w] & bit) {
-      again[w] |= bit;
-      shared = true;
-    }
-    seen[w] |= bit;
-  });
+    for (size_t w = w_lo; w <= w_hi && !shared; ++w) shared = again[w] != 0;
+  }
   int64_t shared_items = 0;
   if (shared) {
     // the hkv items of a piece are adjacent and read the same blocks
@@ -356,7 +368,7 @@ void build_decode_plan(const uint32_t* positions, const int32_t* row_seq,
       shared_items += s ? hkv : 0;
     }
   }
-  if (w_lo <= w_hi) {
+  if (id_lo <= id_hi) {
     std::fill(seen.begin() + w_lo, seen.begin() + w_hi + 1, 0);
     std::fill(again.begin() + w_lo, again.begin() + w_hi + 1, 0);
   }

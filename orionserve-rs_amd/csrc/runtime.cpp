@@ -255,17 +255,17 @@ struct orion_hip_model {
 
   // activations / batch buffers (grown on demand)
   DevBuf hidden, xn, qkv, qrot, attn, act, logits, argmax, ws, sumsq;
-  DevBuf b_tokens, b_positions, b_rowseq, b_btoff, b_btids, b_last;
-  void* pinned = nullptr;
-  size_t pinned_bytes = 0;
+  DevBuf b_batch, b_plan;  // the batch and the attention plans (one copy each)
+  void* pinned[2] = {nullptr, nullptr};  // their pinned staging areas
+  size_t pinned_bytes[2] = {0, 0};
 
   ~orion_hip_model() {
     for (void* p : allocations) (void)hipFree(p);
     for (DevBuf* b : {&hidden, &xn, &qkv, &qrot, &attn, &act, &logits, &argmax, &ws, &sumsq,
-                      &b_tokens,
-                      &b_positions, &b_rowseq, &b_btoff, &b_btids, &b_last})
+                      &b_batch, &b_plan})
       b->release();
-    if (pinned) (void)hipHostFree(pinned);
+    for (void* p : pinned)
+      if (p) (void)hipHostFree(p);
   }
 
   // Frees one allocation made by alloc (the device is synchronised first).
@@ -1461,118 +1461,159 @@ ORION_EXPORT int orion_hip_model_forward(orion_hip_model* m, const orion_hip_bat
     }
   }
   const int64_t npf = (int64_t)pf_start.size();
-  PrefillPlan pfp;
-  if (npf)
-    build_prefill_order(pf_start.data(), pf_count.data(), pf_pos.data(), npf, G, d.num_kv_heads,
-                        m->dev->wave_slots / 8, &pfp, d.head_dim);
-  const std::vector<PrefillTile>& pf_order = pfp.order;
-  const bool pf_split = pfp.max_parts > 1;
-  // Decode plan (longest-first chunk list) over the remaining rows.
-  DecodePlanHost plan;
-  build_decode_plan(b->positions, hb.row_seq.data(), b->block_table_offsets, b->block_table_ids, n,
-                    d.num_kv_heads, d.block_size, m->dev->wave_slots,
-                    npf ? skip.data() : nullptr, &plan, decode_pack_rows(m->kv, Hq));
-  // One workspace for the decode splits and the prefill key parts (their
-  // launches are ordered on the stream: the decode merge has read the splits
-  // before the prefill kernel writes its parts).
-  HIP_TRY(st, m->ws.reserve(std::max(decode_workspace_bytes(n, Hq, d.head_dim, plan.max_splits),
-                                     decode_workspace_bytes(n, Hq, d.head_dim, pfp.max_parts))));
 
-  // ---- upload the batch: one pinned staging area, one copy ----
+  // Pinned staging area i (0: the batch, 1: the attention plans), grown on
+  // demand.  Each forward ends with a stream sync, so the previous forward's
+  // copies out of both are complete.
+  auto staging = [&](int i, size_t bytes) -> hipError_t {
+    if (bytes <= m->pinned_bytes[i]) return hipSuccess;
+    if (m->pinned[i]) {
+      hipError_t e = hipStreamSynchronize(stream);
+      if (e == hipSuccess) e = hipHostFree(m->pinned[i]);
+      if (e != hipSuccess) return e;
+      m->pinned[i] = nullptr;
+      m->pinned_bytes[i] = 0;
+    }
+    const size_t cap = std::max<size_t>(bytes * 2, 1 << 16);
+    hipError_t e = hipHostMalloc(&m->pinned[i], cap, hipHostMallocDefault);
+    if (e != hipSuccess) {
+      m->pinned[i] = nullptr;
+      return e;
+    }
+    m->pinned_bytes[i] = cap;
+    return hipSuccess;
+  };
+
+  // ---- upload the batch: tokens, positions, row sequences, last rows and
+  // block tables, one pinned staging area, one copy ----
   const size_t o_tok = 0;
   const size_t o_pos = o_tok + n * 4;
   const size_t o_rs = o_pos + n * 4;
   const size_t o_last = o_rs + n * 4;
   const size_t o_btoff = (o_last + S * 4 + 7) & ~(size_t)7;
   const size_t o_btids = o_btoff + (S + 1) * 8;
-  const size_t o_work = (o_btids + nbt * 4 + 31) & ~(size_t)31;
-  const size_t o_nsplit = o_work + plan.work.size() * sizeof(DecodeWork);
-  const size_t o_pfoff = (o_nsplit + plan.row_nsplit.size() * 4 + 7) & ~(size_t)7;
-  const size_t o_pfstart = o_pfoff + npf * 8;
-  const size_t o_pfcount = o_pfstart + npf * 4;
-  const size_t o_pfpos = o_pfcount + npf * 4;
-  const size_t o_drows = o_pfpos + npf * 4;
-  const size_t o_pforder = (o_drows + plan.rows.size() * 4 + 7) & ~(size_t)7;
-  const size_t o_pfsplit = o_pforder + pf_order.size() * sizeof(PrefillTile);
-  const size_t o_pfparts = o_pfsplit + (pf_split ? pfp.split_rows.size() * 4 : 0);
-  const size_t o_packrows = o_pfparts + (pf_split ? pfp.row_parts.size() * 4 : 0);
-  const size_t total = o_packrows + plan.pack_rows.size() * 4;
-  if (total > m->pinned_bytes) {
-    if (m->pinned) {
-      HIP_TRY(st, hipStreamSynchronize(stream));
-      HIP_TRY(st, hipHostFree(m->pinned));
-      m->pinned = nullptr;
-    }
-    const size_t cap = std::max<size_t>(total * 2, 1 << 16);
-    HIP_TRY(st, hipHostMalloc(&m->pinned, cap, hipHostMallocDefault));
-    m->pinned_bytes = cap;
+  const size_t total = o_btids + nbt * 4;
+  HIP_TRY(st, staging(0, total));
+  HIP_TRY(st, m->b_batch.reserve(total));
+  {
+    char* hp = static_cast<char*>(m->pinned[0]);
+    std::memcpy(hp + o_tok, b->tokens, n * 4);
+    std::memcpy(hp + o_pos, b->positions, n * 4);
+    std::memcpy(hp + o_rs, hb.row_seq.data(), n * 4);
+    std::memcpy(hp + o_last, hb.last_rows.data(), S * 4);
+    std::memcpy(hp + o_btoff, b->block_table_offsets, (S + 1) * 8);
+    std::memcpy(hp + o_btids, b->block_table_ids, nbt * 4);
+    HIP_TRY(st, hipMemcpyAsync(m->b_batch.ptr, hp, total, hipMemcpyHostToDevice, stream));
   }
-  HIP_TRY(st, m->b_tokens.reserve(total));
-  char* hp = static_cast<char*>(m->pinned);
-  // The previous forward's copy out of the staging area completed at its sync.
-  std::memcpy(hp + o_tok, b->tokens, n * 4);
-  std::memcpy(hp + o_pos, b->positions, n * 4);
-  std::memcpy(hp + o_rs, hb.row_seq.data(), n * 4);
-  std::memcpy(hp + o_last, hb.last_rows.data(), S * 4);
-  std::memcpy(hp + o_btoff, b->block_table_offsets, (S + 1) * 8);
-  std::memcpy(hp + o_btids, b->block_table_ids, nbt * 4);
-  std::memcpy(hp + o_work, plan.work.data(), plan.work.size() * sizeof(DecodeWork));
-  std::memcpy(hp + o_nsplit, plan.row_nsplit.data(), plan.row_nsplit.size() * 4);
-  std::memcpy(hp + o_pfoff, pf_btoff.data(), npf * 8);
-  std::memcpy(hp + o_pfstart, pf_start.data(), npf * 4);
-  std::memcpy(hp + o_pfcount, pf_count.data(), npf * 4);
-  std::memcpy(hp + o_pfpos, pf_pos.data(), npf * 4);
-  std::memcpy(hp + o_drows, plan.rows.data(), plan.rows.size() * 4);
-  std::memcpy(hp + o_pforder, pf_order.data(), pf_order.size() * sizeof(PrefillTile));
-  if (pf_split) {
-    std::memcpy(hp + o_pfsplit, pfp.split_rows.data(), pfp.split_rows.size() * 4);
-    std::memcpy(hp + o_pfparts, pfp.row_parts.data(), pfp.row_parts.size() * 4);
-  }
-  std::memcpy(hp + o_packrows, plan.pack_rows.data(), plan.pack_rows.size() * 4);
-  char* dp = m->b_tokens.as<char>();
-  HIP_TRY(st, hipMemcpyAsync(dp, hp, total, hipMemcpyHostToDevice, stream));
+  const char* dp = m->b_batch.as<char>();
   const uint32_t* d_tok = reinterpret_cast<const uint32_t*>(dp + o_tok);
   const uint32_t* d_pos = reinterpret_cast<const uint32_t*>(dp + o_pos);
   const int32_t* d_rs = reinterpret_cast<const int32_t*>(dp + o_rs);
   const int32_t* d_last = reinterpret_cast<const int32_t*>(dp + o_last);
   const int64_t* d_btoff = reinterpret_cast<const int64_t*>(dp + o_btoff);
   const uint32_t* d_btids = reinterpret_cast<const uint32_t*>(dp + o_btids);
-  DecodePlanDev dplan;
-  dplan.work = reinterpret_cast<const DecodeWork*>(dp + o_work);
-  dplan.row_nsplit = reinterpret_cast<const int32_t*>(dp + o_nsplit);
-  dplan.num_work = (int)plan.work.size();
-  dplan.chunk = plan.chunk;
-  dplan.max_splits = plan.max_splits;
-  dplan.ws = m->ws.as<float>();
-  dplan.ws_bytes = m->ws.bytes;
-  dplan.stream_kv = plan.stream_kv;
-  dplan.mixed_kv = plan.mixed_kv;
-  dplan.num_packed = plan.num_packed;
-  dplan.pack_rows = reinterpret_cast<const int32_t*>(dp + o_packrows);
-  dplan.pack_r = plan.pack_r;
-  if (npf) {
-    dplan.rows = reinterpret_cast<const int32_t*>(dp + o_drows);
-    dplan.num_rows = (int)plan.rows.size();
-  }
-  const int64_t* d_pfoff = reinterpret_cast<const int64_t*>(dp + o_pfoff);
-  const int32_t* d_pfstart = reinterpret_cast<const int32_t*>(dp + o_pfstart);
-  const int32_t* d_pfcount = reinterpret_cast<const int32_t*>(dp + o_pfcount);
-  const uint32_t* d_pfpos = reinterpret_cast<const uint32_t*>(dp + o_pfpos);
-  const PrefillTile* d_pforder = reinterpret_cast<const PrefillTile*>(dp + o_pforder);
-  // the prefill key parts' merge (split rows, parts per row, the workspace)
-  DecodePlanDev pf_merge;
+
+  // ---- attention plans.  Nothing before layer 0's attention reads them, so
+  // they are built on the host (and copied up) while the GPU runs the
+  // embedding and layer 0's QKV GEMM and RoPE / KV write. ----
+  PrefillPlan pfp;
+  DecodePlanHost plan;
+  DecodePlanDev dplan, pf_merge;
   PrefillSplitOut pf_out;
-  if (pf_split) {
-    pf_merge.rows = reinterpret_cast<const int32_t*>(dp + o_pfsplit);
-    pf_merge.num_rows = (int)pfp.split_rows.size();
-    pf_merge.row_nsplit = reinterpret_cast<const int32_t*>(dp + o_pfparts);
-    pf_merge.max_splits = pfp.max_parts;
-    pf_merge.ws = m->ws.as<float>();
-    pf_merge.ws_bytes = m->ws.bytes;
-    pf_out.ws_o = pf_merge.ws;
-    pf_out.ws_ml = pf_merge.ws + n * Hq * pfp.max_parts * d.head_dim;
-    pf_out.max_parts = pfp.max_parts;
-  }
+  const PrefillTile* d_pforder = nullptr;
+  const int64_t* d_pfoff = nullptr;
+  const int32_t *d_pfstart = nullptr, *d_pfcount = nullptr;
+  const uint32_t* d_pfpos = nullptr;
+  bool pf_split = false, o_presplit = false;
+  // (set below, before the plans are built: whether layers run on pre-split
+  // activations decides whether the O GEMM can take them too)
+  bool presplit = false;
+  auto plan_attention = [&]() -> int {
+    if (npf)
+      build_prefill_order(pf_start.data(), pf_count.data(), pf_pos.data(), npf, G,
+                          d.num_kv_heads, m->dev->wave_slots / 8, &pfp, d.head_dim);
+    pf_split = pfp.max_parts > 1;
+    // Decode plan (longest-first chunk list) over the remaining rows.
+    build_decode_plan(b->positions, hb.row_seq.data(), b->block_table_offsets,
+                      b->block_table_ids, n, d.num_kv_heads, d.block_size, m->dev->wave_slots,
+                      npf ? skip.data() : nullptr, &plan, decode_pack_rows(m->kv, Hq));
+    // One workspace for the decode splits and the prefill key parts (their
+    // launches are ordered on the stream: the decode merge has read the
+    // splits before the prefill kernel writes its parts).
+    HIP_TRY(st, m->ws.reserve(std::max(decode_workspace_bytes(n, Hq, d.head_dim, plan.max_splits),
+                                       decode_workspace_bytes(n, Hq, d.head_dim, pfp.max_parts))));
+    const std::vector<PrefillTile>& pf_order = pfp.order;
+    const size_t o_work = 0;
+    const size_t o_nsplit = o_work + plan.work.size() * sizeof(DecodeWork);
+    const size_t o_pfoff = (o_nsplit + plan.row_nsplit.size() * 4 + 7) & ~(size_t)7;
+    const size_t o_pfstart = o_pfoff + npf * 8;
+    const size_t o_pfcount = o_pfstart + npf * 4;
+    const size_t o_pfpos = o_pfcount + npf * 4;
+    const size_t o_drows = o_pfpos + npf * 4;
+    const size_t o_pforder = (o_drows + plan.rows.size() * 4 + 7) & ~(size_t)7;
+    const size_t o_pfsplit = o_pforder + pf_order.size() * sizeof(PrefillTile);
+    const size_t o_pfparts = o_pfsplit + (pf_split ? pfp.split_rows.size() * 4 : 0);
+    const size_t o_packrows = o_pfparts + (pf_split ? pfp.row_parts.size() * 4 : 0);
+    const size_t ptotal = std::max<size_t>(o_packrows + plan.pack_rows.size() * 4, 8);
+    HIP_TRY(st, staging(1, ptotal));
+    HIP_TRY(st, m->b_plan.reserve(ptotal));
+    char* hp = static_cast<char*>(m->pinned[1]);
+    std::memcpy(hp + o_work, plan.work.data(), plan.work.size() * sizeof(DecodeWork));
+    std::memcpy(hp + o_nsplit, plan.row_nsplit.data(), plan.row_nsplit.size() * 4);
+    std::memcpy(hp + o_pfoff, pf_btoff.data(), npf * 8);
+    std::memcpy(hp + o_pfstart, pf_start.data(), npf * 4);
+    std::memcpy(hp + o_pfcount, pf_count.data(), npf * 4);
+    std::memcpy(hp + o_pfpos, pf_pos.data(), npf * 4);
+    std::memcpy(hp + o_drows, plan.rows.data(), plan.rows.size() * 4);
+    std::memcpy(hp + o_pforder, pf_order.data(), pf_order.size() * sizeof(PrefillTile));
+    if (pf_split) {
+      std::memcpy(hp + o_pfsplit, pfp.split_rows.data(), pfp.split_rows.size() * 4);
+      std::memcpy(hp + o_pfparts, pfp.row_parts.data(), pfp.row_parts.size() * 4);
+    }
+    std::memcpy(hp + o_packrows, plan.pack_rows.data(), plan.pack_rows.size() * 4);
+    char* pp = m->b_plan.as<char>();
+    HIP_TRY(st, hipMemcpyAsync(pp, hp, ptotal, hipMemcpyHostToDevice, stream));
+    dplan.work = reinterpret_cast<const DecodeWork*>(pp + o_work);
+    dplan.row_nsplit = reinterpret_cast<const int32_t*>(pp + o_nsplit);
+    dplan.num_work = (int)plan.work.size();
+    dplan.chunk = plan.chunk;
+    dplan.max_splits = plan.max_splits;
+    dplan.ws = m->ws.as<float>();
+    dplan.ws_bytes = m->ws.bytes;
+    dplan.stream_kv = plan.stream_kv;
+    dplan.mixed_kv = plan.mixed_kv;
+    dplan.num_packed = plan.num_packed;
+    dplan.pack_rows = reinterpret_cast<const int32_t*>(pp + o_packrows);
+    dplan.pack_r = plan.pack_r;
+    if (npf) {
+      dplan.rows = reinterpret_cast<const int32_t*>(pp + o_drows);
+      dplan.num_rows = (int)plan.rows.size();
+    }
+    d_pfoff = reinterpret_cast<const int64_t*>(pp + o_pfoff);
+    d_pfstart = reinterpret_cast<const int32_t*>(pp + o_pfstart);
+    d_pfcount = reinterpret_cast<const int32_t*>(pp + o_pfcount);
+    d_pfpos = reinterpret_cast<const uint32_t*>(pp + o_pfpos);
+    d_pforder = reinterpret_cast<const PrefillTile*>(pp + o_pforder);
+    // the prefill key parts' merge (split rows, parts per row, the workspace)
+    if (pf_split) {
+      pf_merge.rows = reinterpret_cast<const int32_t*>(pp + o_pfsplit);
+      pf_merge.num_rows = (int)pfp.split_rows.size();
+      pf_merge.row_nsplit = reinterpret_cast<const int32_t*>(pp + o_pfparts);
+      pf_merge.max_splits = pfp.max_parts;
+      pf_merge.ws = m->ws.as<float>();
+      pf_merge.ws_bytes = m->ws.bytes;
+      pf_out.ws_o = pf_merge.ws;
+      pf_out.ws_ml = pf_merge.ws + n * Hq * pfp.max_parts * d.head_dim;
+      pf_out.max_parts = pfp.max_parts;
+    }
+    // The O GEMM's input is pre-split too when the prefill kernel writes
+    // every attention row itself (no decode rows, no key parts).
+    const char* presplit_env = getenv("ORION_GEMM_PRESPLIT");
+    o_presplit = presplit && plan.work.empty() && npf > 0 && !pf_split &&
+                 !(presplit_env && presplit_env[0] == '2');
+    pf_out.out_hilo = o_presplit ? 1 : 0;
+    return ORION_HIP_OK;
+  };
 
   float* hidden = m->hidden.as<float>();
   float* xn = m->xn.as<float>();
@@ -1604,14 +1645,8 @@ ORION_EXPORT int orion_hip_model_forward(orion_hip_model* m, const orion_hip_bat
   // activations (measurement knob, read per call).
   const char* presplit_env = getenv("ORION_GEMM_PRESPLIT");
   const char* act_env = getenv("ORION_GEMM_ACT");
-  const bool presplit = !fused && n > 64 && pack_layers && H % 8 == 0 && F % 8 == 0 &&
-                        !(presplit_env && presplit_env[0] == '0') &&
-                        !(act_env && act_env[0] == 'b');
-  // The O GEMM's input too, when the prefill kernel writes every attention
-  // row itself (no decode rows, no key parts).
-  const bool o_presplit = presplit && plan.work.empty() && npf > 0 && !pf_split &&
-                          !(presplit_env && presplit_env[0] == '2');
-  pf_out.out_hilo = o_presplit ? 1 : 0;
+  presplit = !fused && n > 64 && pack_layers && H % 8 == 0 && F % 8 == 0 &&
+             !(presplit_env && presplit_env[0] == '0') && !(act_env && act_env[0] == 'b');
   // (the fused route's embed also leaves the row sums of squares, so layer
   // 0's QKV GEMM applies its RMSNorm like every later layer's)
   HIP_TRY(st, launch_embed(stream, d_tok, n, m->w_embed, H, hidden, sumsq));
@@ -1635,11 +1670,13 @@ ORION_EXPORT int orion_hip_model_forward(orion_hip_model* m, const orion_hip_bat
     HIP_TRY(st, launch_rope_and_cache(stream, m->kv, m->arena, l, n, Hq, qkv, m->qkvd, qrot,
                                       qkv + m->qd, m->qkvd, qkv + m->qd + m->kvd, m->qkvd, d_pos,
                                       d_rs, d_btoff, d_btids, m->rope_cos, m->rope_sin, &part));
+    if (l == 0)
+      if (int rc = plan_attention()) return rc;
     HIP_TRY(st, launch_paged_decode(stream, m->kv, m->arena, l, qrot, n, Hq, d_pos, d_rs, d_btoff,
                                     d_btids, dplan, attn));
     if (npf) {
       HIP_TRY(st, launch_paged_prefill(stream, m->kv, m->arena, l, qrot, Hq, d_pforder,
-                                       (int64_t)pf_order.size(), d_pfstart, d_pfcount, d_pfpos,
+                                       (int64_t)pfp.order.size(), d_pfstart, d_pfcount, d_pfpos,
                                        d_pfoff, d_btids, pf_ops, attn, pf_out));
       if (pf_split)
         HIP_TRY(st, launch_split_merge(stream, d.head_dim, n, Hq, pf_merge, attn));
