@@ -1229,12 +1229,15 @@ namespace {
 struct HostBatch {
   std::vector<int32_t> row_seq;
   std::vector<int32_t> last_rows;
+  std::vector<int64_t> seq_max_pos;  // largest position of each sequence's rows
   int64_t max_position = 0;
 };
 
 // ForwardBatch::validate (traits.rs:232-261) plus every check the reference
 // performs while computing (transformer.rs:212-217, :257-262, :376-385,
-// attention.rs:136-175, :411-419), done once on the host before launch.
+// attention.rs:136-175, :411-419), done once on the host before launch; the
+// block ids themselves are checked by validate_tables, before the first
+// launch that reads or writes the KV arena.
 int validate_batch(orion_hip_model* m, const orion_hip_batch* b, HostBatch* hb) {
   const char* st = "forward";
   const auto& d = m->desc;
@@ -1258,7 +1261,8 @@ int validate_batch(orion_hip_model* m, const orion_hip_batch* b, HostBatch* hb) 
   }
   hb->row_seq.resize(n);
   hb->last_rows.resize(S);
-  std::vector<int64_t> seq_max_pos(S, -1);
+  std::vector<int64_t>& seq_max_pos = hb->seq_max_pos;
+  seq_max_pos.assign(S, -1);
   int64_t row = 0;
   for (int64_t s = 0; s < S; ++s) {
     for (int64_t c = 0; c < b->slot_token_counts[s]; ++c, ++row) {
@@ -1279,9 +1283,16 @@ int validate_batch(orion_hip_model* m, const orion_hip_batch* b, HostBatch* hb) 
     }
     hb->last_rows[s] = (int32_t)(row - 1);
   }
-  // Every block a row can attend to (positions 0..=pos) must exist in the arena.
-  for (int64_t s = 0; s < S; ++s) {
-    const int64_t used = seq_max_pos[s] / d.block_size + 1;
+  return ORION_HIP_OK;
+}
+
+// Every block a row can attend to (positions 0..=pos) must exist in the arena
+// (attention.rs:136-175: the reference's KvStore bounds check).
+int validate_tables(orion_hip_model* m, const orion_hip_batch* b, const HostBatch& hb) {
+  const char* st = "forward";
+  const auto& d = m->desc;
+  for (int64_t s = 0; s < b->num_seqs; ++s) {
+    const int64_t used = hb.seq_max_pos[s] / d.block_size + 1;
     const uint32_t* tbl = b->block_table_ids + b->block_table_offsets[s];
     for (int64_t i = 0; i < used; ++i)
       if ((int64_t)tbl[i] >= d.num_blocks)
@@ -1513,9 +1524,10 @@ ORION_EXPORT int orion_hip_model_forward(orion_hip_model* m, const orion_hip_bat
   const int64_t* d_btoff = reinterpret_cast<const int64_t*>(dp + o_btoff);
   const uint32_t* d_btids = reinterpret_cast<const uint32_t*>(dp + o_btids);
 
-  // ---- attention plans.  Nothing before layer 0's attention reads them, so
-  // they are built on the host (and copied up) while the GPU runs the
-  // embedding and layer 0's QKV GEMM and RoPE / KV write. ----
+  // ---- block ids and attention plans.  Nothing before layer 0's RoPE / KV
+  // write reads the arena or the plans, so the block ids are checked and the
+  // plans built on the host (and copied up) while the GPU runs the embedding
+  // and layer 0's QKV GEMM. ----
   PrefillPlan pfp;
   DecodePlanHost plan;
   DecodePlanDev dplan, pf_merge;
@@ -1529,6 +1541,7 @@ ORION_EXPORT int orion_hip_model_forward(orion_hip_model* m, const orion_hip_bat
   // activations decides whether the O GEMM can take them too)
   bool presplit = false;
   auto plan_attention = [&]() -> int {
+    if (int rc = validate_tables(m, b, hb)) return rc;
     if (npf)
       build_prefill_order(pf_start.data(), pf_count.data(), pf_pos.data(), npf, G,
                           d.num_kv_heads, m->dev->wave_slots / 8, &pfp, d.head_dim);
@@ -1667,11 +1680,11 @@ ORION_EXPORT int orion_hip_model_forward(orion_hip_model* m, const orion_hip_bat
     if (pack_layers) qkv_f.w_packed = L.p_qkv, qkv_f.w_packed_deferred = true;
     HIP_TRY(st, gemm_on(m->dev, qkv_x, L.w_qkv, L.b_qkv, n, m->qkvd, H, Epilogue::kStore, qkv,
                         &qkv_f));
+    if (l == 0)
+      if (int rc = plan_attention()) return rc;
     HIP_TRY(st, launch_rope_and_cache(stream, m->kv, m->arena, l, n, Hq, qkv, m->qkvd, qrot,
                                       qkv + m->qd, m->qkvd, qkv + m->qd + m->kvd, m->qkvd, d_pos,
                                       d_rs, d_btoff, d_btids, m->rope_cos, m->rope_sin, &part));
-    if (l == 0)
-      if (int rc = plan_attention()) return rc;
     HIP_TRY(st, launch_paged_decode(stream, m->kv, m->arena, l, qrot, n, Hq, d_pos, d_rs, d_btoff,
                                     d_btids, dplan, attn));
     if (npf) {

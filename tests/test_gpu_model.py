@@ -155,6 +155,7 @@ def test_model_invariants_gpu(backend):
 def test_forward_errors_are_internal(backend):
     spec = small_spec(L=1)
     m = gpu_model(backend, spec, random_weights(spec, np.random.default_rng(0)))
+    good = m.forward(batch([1], [0], [1], [[0]])).logits
     with pytest.raises(oh.InternalError):  # OOV token (transformer.rs:769-776)
         m.forward(batch([spec.V + 5], [0], [1], [[0]]))
     with pytest.raises(oh.InternalError):  # beyond RoPE table (:778-793)
@@ -169,6 +170,10 @@ def test_forward_errors_are_internal(backend):
         m.forward(bad)
     out = m.forward(oh.ForwardBatch([], [], [], [], [], []))  # empty batch (:551-566)
     assert out.logits.shape == (0, spec.V)
+    # A refused batch leaves the model as it was (the block ids are checked
+    # after the embedding and the first QKV GEMM are queued, before anything
+    # touches the arena): the first batch again gives the same logits.
+    assert np.array_equal(m.forward(batch([1], [0], [1], [[0]])).logits, good)
     m.close()
 
 
