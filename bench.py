@@ -216,12 +216,19 @@ def decode_e2e(steps=64, seqs=32, seed=20261204, cpu=True):
     last = out.argmax.tolist()
     ctx = [int(n) for n in lens]
     generated = [last]
+    # The decode batch is flattened once; each step then replaces its tokens
+    # and advances positions and context lengths in place (advance_decode).
+    # The library still validates and plans every step.
+    dec = None
 
     def step():
-        nonlocal last
-        b = oh.ForwardBatch(last, ctx, list(range(seqs)), [1] * seqs, [c + 1 for c in ctx],
-                            tables, False)
-        o = model.forward(b, want_logits=False, want_argmax=True)
+        nonlocal last, dec
+        if dec is None:
+            dec = oh.ForwardBatch(last, list(ctx), list(range(seqs)), [1] * seqs,
+                                  [c + 1 for c in ctx], tables, False).prepare()
+        else:
+            dec.advance_decode(last)
+        o = model.forward(dec, want_logits=False, want_argmax=True)
         last = o.argmax.tolist()
         generated.append(last)
         for i in range(seqs):
@@ -277,6 +284,7 @@ def decode_e2e(steps=64, seqs=32, seed=20261204, cpu=True):
     last = out.argmax.tolist()
     ctx = [int(n) for n in lens]
     generated = [last]
+    dec = None
     for _ in range(steps):
         step()
     res["greedy_vs_oracle_f32kv"] = greedy_vs_golden(generated, steps, seqs, "f32")

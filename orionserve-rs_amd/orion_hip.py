@@ -406,6 +406,29 @@ class ForwardBatch:
         self._prepared = self.to_csr()
         return self
 
+    def advance_decode(self, next_tokens: Sequence[int]) -> "ForwardBatch":
+        """The next step of a prepared decode batch (one row per sequence, no
+        prefill): sequence i's token becomes next_tokens[i], and its position
+        and context length advance by one, in the lists and in the prepared
+        arrays alike (no re-flattening of the block tables).  The tables are
+        kept as they are; each must already hold a block for the new position,
+        which the library checks on forward as for any batch."""
+        prepared = getattr(self, "_prepared", None)
+        if prepared is None or self.has_prefill or any(c != 1 for c in self.slot_token_counts):
+            raise InternalError("advance_decode needs a prepared decode batch "
+                                "(one row per sequence)")
+        if len(next_tokens) != len(self.tokens):
+            raise InternalError(f"advance_decode got {len(next_tokens)} tokens for "
+                                f"{len(self.tokens)} sequences")
+        tokens, positions, _, ctx, _, _ = prepared
+        tokens[:] = array.array("I", next_tokens)  # (raises on out-of-range ids)
+        positions += 1
+        ctx += 1
+        self.tokens = list(next_tokens)
+        self.positions = [p + 1 for p in self.positions]
+        self.context_lens = [c + 1 for c in self.context_lens]
+        return self
+
     def to_csr(self):
         """Flattened arrays in the layout of orion_hip_batch.  Built with
         array.array (straight from Python ints; an out-of-range value raises

@@ -101,6 +101,28 @@ def test_prepared_batch_reuses_the_flattened_arrays():
         bad.prepare()
 
 
+def test_advance_decode_updates_lists_and_prepared_arrays():
+    """ForwardBatch.advance_decode: the next decode step of a prepared batch
+    equals the batch built from scratch for that step (the reference's
+    scheduler gives each decoding sequence its next token at position + 1,
+    context + 1, the same table)."""
+    oh = orion_hip
+    b = oh.ForwardBatch([5, 6], [3, 9], [0, 1], [1, 1], [4, 10], [[3], [4]], False).prepare()
+    assert b.advance_decode([7, 8]) is b
+    want = oh.ForwardBatch([7, 8], [4, 10], [0, 1], [1, 1], [5, 11], [[3], [4]], False)
+    assert (b.tokens, b.positions, b.context_lens) == ([7, 8], [4, 10], [5, 11])
+    for got, w in zip(b._prepared, want.to_csr()):
+        assert np.array_equal(got, w)
+    with pytest.raises(oh.InternalError):  # not prepared
+        oh.ForwardBatch([5], [0], [0], [1], [1], [[3]], False).advance_decode([1])
+    with pytest.raises(oh.InternalError):  # a prefill chunk
+        oh.ForwardBatch([5, 6], [0, 1], [0], [2], [2], [[3]], True).prepare().advance_decode([1, 2])
+    with pytest.raises(oh.InternalError):  # wrong number of tokens
+        b.advance_decode([1])
+    with pytest.raises(OverflowError):  # a token id that is no u32
+        b.advance_decode([-1, 2])
+
+
 def test_bench_measures_one_gpu_only():
     """bench.py --gpus N with N > 1 exits with a message (this build measures
     one GPU); the check runs before the library is loaded."""

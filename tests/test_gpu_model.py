@@ -570,6 +570,16 @@ def test_prepared_batch_forward_is_identical(backend):
     assert np.array_equal(g1, g2)
     g3 = m.forward(b2).logits  # reused arrays, same KV writes
     assert np.array_equal(g1, g3)
+    # the next decode step, advanced in place and built from scratch
+    def dec(tokens, positions):
+        return oh.ForwardBatch(tokens, positions, [1, 2], [1, 1], [p + 1 for p in positions],
+                               [[0], [1]], False)
+    d = dec([11, 13], [5, 2]).prepare()
+    m.forward(d)
+    d.advance_decode([17, 19])
+    g4 = m.forward(d).logits
+    g5 = m.forward(dec([17, 19], [6, 3])).logits
+    assert np.array_equal(g4, g5)
     m.close()
 
 
