@@ -672,3 +672,75 @@ def test_continuous_batch_with_a_shared_prefix(backend, kv, G):
         del os.environ["ORION_DECODE_PACK"]
     for a, b in zip(packed, plain):
         assert float(np.abs(a - b).max()) <= 2e-5 * max(float(np.abs(b).max()), 1.0)
+
+
+@pytest.mark.parametrize("seed", [1, 2, 4, 5, 7, 8, 13, 14])
+def test_random_mixed_forwards(backend, seed):
+    """Random continuous batches through the whole forward, against the
+    oracle running the same calls (transformer.rs:359-442): head groups,
+    head_dim, block size, arena dtype, QKV bias and tied head drawn at
+    random; sequences with random cached prefixes (some sharing sequence 0's
+    leading blocks, as prefix caching leaves them) then a step mixing
+    prefill chunks and decode rows, then a joint decode step."""
+    rng = np.random.default_rng(1000 + seed)
+    G = int(rng.choice([1, 2, 4, 7]))
+    hkv = int(rng.choice([1, 2]))
+    d = int(rng.choice([64, 128]))
+    bs = int(rng.choice([8, 16, 32]))
+    kv = oh.BF16 if rng.random() < 0.5 else oh.F32
+    S = int(rng.integers(2, 6))
+    cached = [int(rng.integers(0, 200)) for _ in range(S)]
+    cached[0] = max(cached[0], 64)
+    new = [1 if rng.random() < 0.5 else int(rng.integers(8, 56)) for _ in range(S)]
+    # sharers start with sequence 0's first m blocks (identical tokens there)
+    share = [0] * S
+    for s in range(1, S):
+        m = min(cached[0], cached[s]) // bs
+        if m and rng.random() < 0.6:
+            share[s] = int(rng.integers(1, m + 1))
+    need = [-(-(c + n + 1) // bs) for c, n in zip(cached, new)]
+    own = [need[s] - share[s] for s in range(S)]
+    num_blocks = sum(own) + 8
+    perm = [int(b) for b in rng.permutation(num_blocks)]
+    tables, cur = [], 0
+    for s in range(S):
+        tables.append(perm[cur:cur + own[s]])
+        cur += own[s]
+    for s in range(1, S):
+        tables[s] = tables[0][:share[s]] + tables[s]
+    hq = G * hkv
+    spec = Spec(2, hq * d, hq, hkv, d, 384, 500, max_pos=512, bias=bool(rng.random() < 0.5),
+                tied=bool(rng.random() < 0.5), num_blocks=num_blocks, block_size=bs)
+    W = random_weights(spec, rng, std=0.05)
+    toks = [list(rng.integers(0, spec.V, cached[s] + new[s] + 1)) for s in range(S)]
+    for s in range(1, S):
+        toks[s][:share[s] * bs] = toks[0][:share[s] * bs]
+    print(f"[random mixed {seed}] G={G} hkv={hkv} d={d} bs={bs} kv={kv} cached={cached} "
+          f"new={new} share={share}", flush=True)
+    # forward 1: sequence 0's cached prompt; forward 2: the others' cached
+    # parts past their shared blocks; forward 3: the mixed step; forward 4: one
+    # decode row each
+    calls = [[(0, 0, cached[0])],
+             [(s, share[s] * bs, cached[s]) for s in range(1, S) if cached[s] > share[s] * bs],
+             [(s, cached[s], cached[s] + new[s]) for s in range(S)],
+             [(s, cached[s] + new[s], cached[s] + new[s] + 1) for s in range(S)]]
+    gm = gpu_model(backend, spec, W, kv)
+    om = oracle_model(spec, W, kv_bf16=kv == oh.BF16)
+    # f32 arithmetic in another summation order; on a bf16 arena also K/V
+    # elements whose f32 values straddle a bf16 rounding boundary on the two
+    # sides, more of them in wider models (measured: f32 <= 9.6e-5, bf16
+    # <= 1.0e-3 below H = 1024 and 2.1e-3 at H = 1792)
+    bound = 1e-4 if kv == oh.F32 else (2e-3 if spec.H < 1024 else 3e-3)
+    for i, call in enumerate(calls):
+        if not call:
+            continue
+        t = [int(x) for s, a, b in call for x in toks[s][a:b]]
+        p = [x for s, a, b in call for x in range(a, b)]
+        counts = [b - a for s, a, b in call]
+        ctx = [b for s, a, b in call]
+        tb = [tables[s] for s, a, b in call]
+        g = gm.forward(batch(t, p, counts, tb, ctx)).logits
+        o = om.forward(t, p, counts, ctx, tb)
+        assert rel_err(g, o) <= bound, (i, rel_err(g, o))
+    gm.close()
+    om.close()
