@@ -266,7 +266,9 @@ typedef struct orion_hip_batch {
  * `logits` may be NULL when only `argmax_out` is wanted.  `argmax_out`
  * (optional, [num_seqs]) receives the greedy token of each row with the
  * reference's tie rule (runtime/src/sampling.rs:196-207); -1 where no logit
- * exceeds -inf. */
+ * exceeds -inf.  A refused batch (ORION_HIP_ERR_INTERNAL) leaves the arena and
+ * the weights untouched: its block ids are checked before any K/V is written
+ * (the other checks before anything is launched). */
 int orion_hip_model_forward(orion_hip_model* model, const orion_hip_batch* batch, float* logits,
                             int64_t* argmax_out);
 
